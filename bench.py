@@ -1,0 +1,226 @@
+"""Benchmark of the block-wise FP8 GEMM and paged-KV decode path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-extra]
+
+Prints ONE JSON line.  Headline (``value``): fp8_gemm TFLOP/s over the
+cfg2 sweep's compute-bound shapes, one step = the six GEMMs
+M in {4096, 16384} x (K, N) in {(1024,4096), (4096,1024), (2048,5632)} with
+1x128 activation / 128x128 weight scales, inputs already quantised and
+resident in HBM.  ``roofline`` prices the GEMM against the dense FP8 MFMA
+peak (5.0 PFLOP/s); each launch is bracketed by HIP events on the stream it
+runs on.  ``paged_decode`` (cfg3 and cfg4) and ``act_quant`` report HBM
+GB/s against 8 TB/s, with the 256 MB last-level cache flushed between timed
+decode calls.  ``cpu_baseline`` times the numpy oracle (blockwise fp32 GEMM)
+on the host for the three M=4096 shapes.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+HBM_PEAK_GBS = 8000.0
+FP8_PEAK_TFLOPS = 5000.0
+METRIC = "FP8 block-GEMM TFLOP/s & paged-decode HBM GB/s (% of MI355X roofline)"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def timed_launches(fns, reps, flush=None):
+    """Run each fn `reps` times, bracketing every launch with events on the
+    current stream; returns per-fn mean kernel-time in seconds."""
+    stream = torch.cuda.current_stream()
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in range(reps)] for _ in fns]
+    for r in range(reps):
+        for i, fn in enumerate(fns):
+            if flush is not None:
+                flush()
+            evs[i][r][0].record(stream)
+            fn()
+            evs[i][r][1].record(stream)
+    torch.cuda.synchronize()
+    return [sum(a.elapsed_time(b) for a, b in e) / reps / 1e3 for e in evs]
+
+
+def gemm_setup(device):
+    from llm_from_scratch_amd import kernels as K
+    from llm_from_scratch_amd import workloads as W
+    cases = []
+    for M in (4096, 16384):
+        for Kd, N in W.GEMM_KN:
+            x = W.activation(M, Kd, seed=1 + M + Kd, device=device)
+            w = W.weight(N, Kd, seed=31 + Kd, device=device)
+            xq, xs = K.act_quant(x)
+            wq, ws = K.weight_quant(w)
+            del x, w
+            cases.append(dict(M=M, K=Kd, N=N, a=xq, a_s=xs, b=wq, b_s=ws,
+                              flops=2.0 * M * N * Kd))
+    return cases
+
+
+def bench_gemm(cases, steps, warmup):
+    """Warm up, then time exactly `steps` steps between two synchronizes;
+    inside that region every launch is bracketed by events on its stream."""
+    from llm_from_scratch_amd import kernels as K
+    fns = [lambda c=c: K.fp8_gemm(c["a"], c["a_s"], c["b"], c["b_s"]) for c in cases]
+    for _ in range(warmup):
+        for f in fns:
+            f()
+    stream = torch.cuda.current_stream()
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in range(steps)] for _ in fns]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for r in range(steps):
+        for i, f in enumerate(fns):
+            evs[i][r][0].record(stream)
+            f()
+            evs[i][r][1].record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    per = [sum(a.elapsed_time(b) for a, b in e) / steps / 1e3 for e in evs]
+    return wall, per
+
+
+def bench_act_quant(device, reps):
+    from llm_from_scratch_amd import kernels as K
+    from llm_from_scratch_amd import workloads as W
+    M, Kd = 16384, 4096
+    x = W.activation(M, Kd, seed=77, device=device)
+    t = timed_launches([lambda: K.act_quant(x)], reps)[0]
+    nbytes = 3 * M * Kd + 4 * M * Kd // 128
+    return {"shape": [M, Kd], "us": t * 1e6, "GB/s": nbytes / t / 1e9,
+            "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "bytes": nbytes}
+
+
+def bench_decode(name, device, reps, flush_buf):
+    from llm_from_scratch_amd import kernels as K
+    from llm_from_scratch_amd import workloads as W
+    case = W.paged_case(name, seed=2 if name == "cfg3" else 3)
+    kc, vc = W.fill_pool(case, seed=2, device=device, only_referenced=(name == "cfg4"))
+    g = torch.Generator(device=device).manual_seed(5)
+    q = torch.randn(case.batch, case.num_q_heads, case.head_dim, generator=g, device=device,
+                    dtype=torch.bfloat16)
+    cl = torch.from_numpy(case.context_lens).to(device)
+    bt = torch.from_numpy(case.block_tables).to(device)
+    bps = K.default_blocks_per_split(case.batch, bt.shape[1], case.block_size)
+    ws = torch.empty(K.paged_decode_workspace_bytes(case.batch, case.num_q_heads, case.head_dim,
+                                                    bt.shape[1], bps), dtype=torch.uint8, device=device)
+    fn = lambda: K.paged_attention_decode(q, kc, vc, cl, bt, case.scale, bps, ws)  # noqa: E731
+    fn()
+    torch.cuda.synchronize()
+    t = timed_launches([fn], reps, flush=lambda: flush_buf.add_(1))[0]
+    nbytes = case.kv_bytes()
+    out = {"config": name, "batch": case.batch, "heads": [case.num_q_heads, case.num_kv_heads],
+           "head_dim": case.head_dim, "tokens": int(case.context_lens.sum()), "us": t * 1e6,
+           "GB/s": nbytes / t / 1e9, "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "bytes": nbytes,
+           "blocks_per_split": bps}
+    del kc, vc
+    torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baseline():
+    """Numpy oracle (blockwise fp32 GEMM, one matmul per 128-wide K block with
+    the scale product applied to the partial) on the three M=4096 shapes."""
+    from threadpoolctl import threadpool_limits
+    from oracle import fp8 as F
+    from llm_from_scratch_amd import workloads as W
+    threads = min(16, os.cpu_count() or 1)
+    flops, secs = 0.0, 0.0
+    with threadpool_limits(threads):
+        for Kd, N in W.GEMM_KN:
+            M = 4096
+            x = W.activation(M, Kd, seed=1 + M + Kd).float().numpy()
+            w = W.weight(N, Kd, seed=31 + Kd).float().numpy()
+            a, a_s = F.act_quant(x)
+            b, b_s = F.weight_quant(w)
+            t0 = time.perf_counter()
+            F.fp8_gemm(a, a_s, b, b_s, accum=np.float32)
+            secs += time.perf_counter() - t0
+            flops += 2.0 * M * N * Kd
+    return {"value": flops / secs / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": "numpy oracle fp8_gemm (blockwise fp32) on cfg2 M=4096 x 3 (K,N) shapes, "
+                      f"{secs:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-extra", action="store_true", help="skip decode / act_quant lines")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+    log("bench: setting up fp8_gemm inputs")
+    cases = gemm_setup(dev)
+    log("bench: timing fp8_gemm")
+    wall, per = bench_gemm(cases, args.steps, args.warmup)
+    total_flops = sum(c["flops"] for c in cases)
+    kern_time = sum(per)
+    achieved = total_flops / kern_time / 1e12
+    shapes = [{"M": c["M"], "K": c["K"], "N": c["N"], "us": t * 1e6,
+               "TFLOP/s": c["flops"] / t / 1e12, "frac": c["flops"] / t / 1e12 / FP8_PEAK_TFLOPS}
+              for c, t in zip(cases, per)]
+    del cases
+    torch.cuda.empty_cache()
+    out = {
+        "metric": METRIC,
+        "value": total_flops / wall / 1e12,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": wall * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3",
+        "data": "synthetic",
+        "config": {"workload": "cfg2 fp8_gemm sweep: M in {4096,16384} x (K,N) in "
+                               "{(1024,4096),(4096,1024),(2048,5632)}, 1x128 act / 128x128 weight "
+                               "e4m3fn scales, bf16 out",
+                   "launches_per_step": len(per)},
+        "roofline": {"bound": "mfma", "kernel": "fp8_gemm", "achieved": achieved,
+                     "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": achieved / FP8_PEAK_TFLOPS,
+                     "traffic": None},
+        "gemm_shapes": shapes,
+    }
+    if not args.no_extra:
+        try:
+            log("bench: act_quant")
+            out["act_quant"] = bench_act_quant(dev, 20)
+            flush_buf = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev).zero_()
+            out["paged_decode"] = []
+            for name in ("cfg3", "cfg4"):
+                log(f"bench: paged decode {name}")
+                out["paged_decode"].append(bench_decode(name, dev, 20, flush_buf))
+            del flush_buf
+        except Exception as e:  # report, keep the headline line
+            out["extra_error"] = repr(e)
+    if not args.no_cpu:
+        log("bench: cpu baseline")
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,79 @@
+// Shared device helpers and the C-ABI error plumbing for the gfx950 kernels.
+//
+// Every exported entry point returns int: 0 on success, a negative LFS_E*
+// code for an argument error detected on the host (nothing was launched), or
+// a positive hipError_t from the launch.  The message for the last failure on
+// the calling thread is available from lfs_last_error().
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/lfs_kernels.h"
+
+namespace lfs {
+
+// ---------------------------------------------------------------- errors --
+void set_error(const char* fmt, ...);
+int check_launch(const char* what);  // hipGetLastError -> code + message
+
+#define LFS_REQUIRE(cond, ...)            \
+  do {                                    \
+    if (!(cond)) {                        \
+      ::lfs::set_error(__VA_ARGS__);      \
+      return LFS_EINVAL;                  \
+    }                                     \
+  } while (0)
+
+// ------------------------------------------------------------ conversions --
+__device__ __forceinline__ float bf16_to_f32(uint32_t h16) {
+  return __uint_as_float(h16 << 16);
+}
+// two bf16 packed in one dword -> floats
+__device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// fp32 -> bf16 bits, round to nearest even (NaN kept quiet)
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+}
+
+// Four floats -> four OCP e4m3fn codes in one dword (byte i = value i).
+// v_cvt_pk_fp8_f32 rounds to nearest even; callers clamp to +-448 first.
+__device__ __forceinline__ uint32_t f32x4_to_e4m3(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return (uint32_t)w;
+}
+
+// e4m3fn code pairs -> floats (exact); word_sel picks bytes 0-1 or 2-3
+__device__ __forceinline__ void e4m3x4_to_f32(uint32_t w, float* o) {
+  auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  o[0] = lo[0]; o[1] = lo[1]; o[2] = hi[0]; o[3] = hi[1];
+}
+
+// ------------------------------------------------------- wave reductions --
+// xor-butterfly over groups of W consecutive lanes (W a power of two <= 64)
+template <int W>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+}  // namespace lfs

@@ -1,0 +1,222 @@
+// Block-wise FP8 (OCP e4m3fn) quantisation kernels for gfx950.
+//
+//  act_quant       1 x GS groups along rows (GS = 32/64/128), one 16-byte
+//                  chunk (8 bf16) per lane, group amax by an xor butterfly
+//                  over GS/8 lanes.  Restates model/attention/utils.py:97-172.
+//  weight_quant    GS x GS blocks, one workgroup per block, block amax via
+//                  a wave butterfly plus LDS across the four waves.
+//  weight_dequant  bf16_RNE(e4m3 * block scale), 8 elements per lane.
+//
+// All three are HBM-bound streaming kernels (2 B read + 1 B written per
+// element for the quantisers, 1 B read + 2 B written for dequant).
+#include "common.h"
+
+namespace lfs {
+
+// fp32(1/448): the reference multiplies the fp32 amax by fp8_max_inv
+// (utils.py:101, :135); 1.0f/448.0f is the same correctly rounded constant.
+constexpr float kFp8Max = 448.0f;
+constexpr float kFp8MaxInv = 1.0f / 448.0f;
+constexpr float kAmaxFloor = 1e-4f;  // utils.py:131
+
+__device__ __forceinline__ float scale_from_amax(float amax, bool round_scale) {
+  float s = fmaxf(amax, kAmaxFloor) * kFp8MaxInv;
+  if (round_scale) {
+    // ue8m0: smallest power of two >= s (utils.py:81-94)
+    uint32_t b = __float_as_uint(s);
+    int e = (int)((b >> 23) & 0xFFu) - 127 + ((b & 0x7FFFFFu) != 0u ? 1 : 0);
+    s = __uint_as_float((uint32_t)(e + 127) << 23);
+  }
+  return s;
+}
+
+// clamp(x / s, -448, 448) with an IEEE divide; NaN passes through
+__device__ __forceinline__ float qdiv(float x, float s) {
+  float q = x / s;
+  q = q > kFp8Max ? kFp8Max : q;
+  q = q < -kFp8Max ? -kFp8Max : q;
+  return q;
+}
+
+__device__ __forceinline__ void unpack8(const uint4& v, float* f) {
+  f[0] = bf16lo(v.x); f[1] = bf16hi(v.x);
+  f[2] = bf16lo(v.y); f[3] = bf16hi(v.y);
+  f[4] = bf16lo(v.z); f[5] = bf16hi(v.z);
+  f[6] = bf16lo(v.w); f[7] = bf16hi(v.w);
+}
+
+__device__ __forceinline__ uint2 quant8(const float* f, float s) {
+  uint2 o;
+  o.x = f32x4_to_e4m3(qdiv(f[0], s), qdiv(f[1], s), qdiv(f[2], s), qdiv(f[3], s));
+  o.y = f32x4_to_e4m3(qdiv(f[4], s), qdiv(f[5], s), qdiv(f[6], s), qdiv(f[7], s));
+  return o;
+}
+
+// ------------------------------------------------------------ act_quant --
+template <int GS, bool ROUND>
+__global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                        uint8_t* __restrict__ y,
+                                                        float* __restrict__ s, int64_t M,
+                                                        int64_t K) {
+  constexpr int LPG = GS / 8;  // lanes per group; groups never straddle waves
+  const int64_t cpr = K / 8;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  // K % GS == 0 and 256 % LPG == 0, so a group's lanes are all in or all out
+  if (idx >= M * cpr) return;
+  const int64_t row = idx / cpr;
+  const int64_t c8 = idx - row * cpr;
+  const uint4 v = *reinterpret_cast<const uint4*>(x + row * ldx + c8 * 8);
+  float f[8];
+  unpack8(v, f);
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[i]));
+  amax = group_max<LPG>(amax);
+  const float sc = scale_from_amax(amax, ROUND);
+  *reinterpret_cast<uint2*>(y + row * K + c8 * 8) = quant8(f, sc);
+  if ((c8 & (LPG - 1)) == 0) s[row * (K / GS) + c8 / LPG] = sc;
+}
+
+// --------------------------------------------------------- weight_quant --
+template <int BS>
+__global__ __launch_bounds__(256) void weight_quant_kernel(const uint16_t* __restrict__ w,
+                                                           uint8_t* __restrict__ y,
+                                                           float* __restrict__ s, int64_t N,
+                                                           int64_t K, int64_t kblocks) {
+  constexpr int CPR = BS / 8;                     // 16-byte chunks per block row
+  constexpr int CHUNKS = BS * CPR;
+  constexpr int PER = (CHUNKS + 255) / 256;       // chunks per thread
+  __shared__ float red[4];
+  const int64_t r0 = (int64_t)blockIdx.y * BS;
+  const int64_t c0 = (int64_t)blockIdx.x * BS;
+  float f[PER][8];
+  bool ok[PER];
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    const int64_t row = r0 + c / CPR;
+    const int64_t col = c0 + (c % CPR) * 8;
+    ok[i] = (c < CHUNKS) && row < N && col < K;
+    if (ok[i]) {
+      const uint4 v = *reinterpret_cast<const uint4*>(w + row * K + col);
+      unpack8(v, f[i]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(f[i][e]));
+    }
+  }
+  amax = group_max<64>(amax);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float sc = scale_from_amax(amax, false);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    if (ok[i]) {
+      const int c = threadIdx.x + 256 * i;
+      const int64_t row = r0 + c / CPR;
+      const int64_t col = c0 + (c % CPR) * 8;
+      *reinterpret_cast<uint2*>(y + row * K + col) = quant8(f[i], sc);
+    }
+  }
+  if (threadIdx.x == 0) s[(int64_t)blockIdx.y * kblocks + blockIdx.x] = sc;
+}
+
+// ------------------------------------------------------- weight_dequant --
+__global__ __launch_bounds__(256) void weight_dequant_kernel(const uint8_t* __restrict__ w,
+                                                             const float* __restrict__ s,
+                                                             uint16_t* __restrict__ y, int64_t N,
+                                                             int64_t K, int bs, int64_t kblocks) {
+  const int64_t cpr = K / 8;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= N * cpr) return;
+  const int64_t row = idx / cpr;
+  const int64_t col = (idx - row * cpr) * 8;
+  const float sc = s[(row / bs) * kblocks + col / bs];  // a chunk never straddles a block
+  const uint2 v = *reinterpret_cast<const uint2*>(w + row * K + col);
+  float f[8];
+  e4m3x4_to_f32(v.x, f);
+  e4m3x4_to_f32(v.y, f + 4);
+  uint4 o;
+  o.x = pack_bf16x2(f[0] * sc, f[1] * sc);
+  o.y = pack_bf16x2(f[2] * sc, f[3] * sc);
+  o.z = pack_bf16x2(f[4] * sc, f[5] * sc);
+  o.w = pack_bf16x2(f[6] * sc, f[7] * sc);
+  *reinterpret_cast<uint4*>(y + row * K + col) = o;
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace lfs
+
+using namespace lfs;
+
+extern "C" int lfs_act_quant(const void* x, int64_t ldx, void* y, float* s, int64_t M, int64_t K,
+                             int32_t block_size, int32_t round_scale, void* stream) {
+  LFS_REQUIRE(M >= 0 && K >= 0, "act_quant: negative shape M=%lld K=%lld", (long long)M,
+              (long long)K);
+  LFS_REQUIRE(block_size == 32 || block_size == 64 || block_size == 128,
+              "act_quant: block_size must be 32, 64 or 128 (got %d)", block_size);
+  LFS_REQUIRE(K % block_size == 0,
+              "Last dimension size must be divisible by block_size (block_size=%d)", block_size);
+  LFS_REQUIRE(ldx >= K && ldx % 8 == 0, "act_quant: row stride %lld must be >= K and a multiple of 8",
+              (long long)ldx);
+  if (M == 0 || K == 0) return 0;
+  LFS_REQUIRE(x && y && s, "act_quant: null pointer");
+  LFS_REQUIRE(aligned16(x) && ((uintptr_t)y & 7u) == 0 && ((uintptr_t)s & 3u) == 0,
+              "act_quant: misaligned buffer");
+  const int64_t chunks = M * (K / 8);
+  const dim3 grid((unsigned)((chunks + 255) / 256));
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t* xp = (const uint16_t*)x;
+  uint8_t* yp = (uint8_t*)y;
+#define LFS_AQ(GS, R) hipLaunchKernelGGL((act_quant_kernel<GS, R>), grid, dim3(256), 0, st, xp, ldx, yp, s, M, K)
+  if (round_scale) {
+    if (block_size == 32) LFS_AQ(32, true);
+    else if (block_size == 64) LFS_AQ(64, true);
+    else LFS_AQ(128, true);
+  } else {
+    if (block_size == 32) LFS_AQ(32, false);
+    else if (block_size == 64) LFS_AQ(64, false);
+    else LFS_AQ(128, false);
+  }
+#undef LFS_AQ
+  return check_launch("act_quant");
+}
+
+extern "C" int lfs_weight_quant(const void* w, void* y, float* s, int64_t N, int64_t K,
+                                int32_t block_size, void* stream) {
+  LFS_REQUIRE(N >= 0 && K >= 0, "weight_quant: negative shape");
+  LFS_REQUIRE(block_size == 32 || block_size == 64 || block_size == 128,
+              "weight_quant: block_size must be 32, 64 or 128 (got %d)", block_size);
+  LFS_REQUIRE(K % 8 == 0, "weight_quant: K=%lld must be a multiple of 8", (long long)K);
+  if (N == 0 || K == 0) return 0;
+  LFS_REQUIRE(w && y && s, "weight_quant: null pointer");
+  LFS_REQUIRE(aligned16(w) && ((uintptr_t)y & 7u) == 0, "weight_quant: misaligned buffer");
+  const int64_t nb = (N + block_size - 1) / block_size, kb = (K + block_size - 1) / block_size;
+  LFS_REQUIRE(nb < 65536, "weight_quant: N too large");
+  const dim3 grid((unsigned)kb, (unsigned)nb);
+  hipStream_t st = (hipStream_t)stream;
+  if (block_size == 128)
+    hipLaunchKernelGGL(weight_quant_kernel<128>, grid, dim3(256), 0, st, (const uint16_t*)w, (uint8_t*)y, s, N, K, kb);
+  else if (block_size == 64)
+    hipLaunchKernelGGL(weight_quant_kernel<64>, grid, dim3(256), 0, st, (const uint16_t*)w, (uint8_t*)y, s, N, K, kb);
+  else
+    hipLaunchKernelGGL(weight_quant_kernel<32>, grid, dim3(256), 0, st, (const uint16_t*)w, (uint8_t*)y, s, N, K, kb);
+  return check_launch("weight_quant");
+}
+
+extern "C" int lfs_weight_dequant(const void* w, const float* s, void* y, int64_t N, int64_t K,
+                                  int32_t block_size, void* stream) {
+  LFS_REQUIRE(N >= 0 && K >= 0, "weight_dequant: negative shape");
+  LFS_REQUIRE(block_size >= 8 && block_size % 8 == 0, "weight_dequant: block_size must be a multiple of 8");
+  LFS_REQUIRE(K % 8 == 0, "weight_dequant: K=%lld must be a multiple of 8", (long long)K);
+  if (N == 0 || K == 0) return 0;
+  LFS_REQUIRE(w && s && y, "weight_dequant: null pointer");
+  LFS_REQUIRE(((uintptr_t)w & 7u) == 0 && aligned16(y), "weight_dequant: misaligned buffer");
+  const int64_t kb = (K + block_size - 1) / block_size;
+  const int64_t chunks = N * (K / 8);
+  hipLaunchKernelGGL(weight_dequant_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint8_t*)w, s, (uint16_t*)y, N, K, block_size, kb);
+  return check_launch("weight_dequant");
+}

@@ -1,0 +1,233 @@
+"""Operator surface of the block-wise FP8 and paged-KV path, on gfx950 kernels.
+
+Same names, arguments and return values as the reference's operators:
+  act_quant(x, block_size=128, scale_fmt=None) -> (y, s)
+      model/attention/utils.py:148-172 (asserts kept word for word)
+  weight_quant(x, block_size=128) -> (y, s)      128x128 block scales
+  weight_dequant(x, s, block_size=128) -> y      bf16
+  fp8_gemm(a, a_s, b, b_s, bias=None) -> c       bf16, fp32 accumulation
+  store_kvcache(key, value, k_cache, v_cache, slot_mapping)
+      KV slot write with the slot contract of engine/model_runner.py:226-230,
+      :261, :303 (-1 = skip)
+  paged_attention_decode(q, k_cache, v_cache, context_lens, block_tables,
+                         scale=None) -> o
+      GQA decode over block tables, math of model/attention/GQA.py:118-130
+
+Every call goes through the C ABI of liblfs_kernels.so on torch's current
+stream; outputs are allocated here, as the reference wrappers do
+(utils.py:168-169).  There is no CPU path: tensors must live on a GPU.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+FP8 = torch.float8_e4m3fn
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _on_gpu(*ts: torch.Tensor) -> None:
+    dev = ts[0].device
+    for t in ts:
+        if t.device.type != "cuda":
+            raise ValueError(f"tensor on {t.device}: the FP8/paged-KV kernels run on the GPU only")
+        if t.device != dev:
+            raise ValueError(f"tensors on different devices: {t.device} vs {dev}")
+
+
+def _dtype(t: torch.Tensor, dt: torch.dtype, name: str) -> None:
+    if t.dtype != dt:
+        raise TypeError(f"{name} must be {dt}, got {t.dtype}")
+
+
+# ----------------------------------------------------------------- FP8 path --
+def act_quant(x: torch.Tensor, block_size: int = 128, scale_fmt: Optional[str] = None
+              ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Block-wise activation quantisation (model/attention/utils.py:148-172).
+
+    Per row, per ``block_size`` consecutive elements of the last dimension:
+    s = max(amax, 1e-4) * fp32(1/448) (``scale_fmt`` set: rounded up to a
+    power of two, the ue8m0 form), y = e4m3fn(clamp(x / s, -448, 448)).
+    Returns (y float8_e4m3fn like x, s float32 [..., N // block_size]).
+    ``block_size`` is honoured (32, 64 or 128), unlike the reference wrapper,
+    whose kernel always used 128.
+    """
+    assert x.is_contiguous(), "Input tensor must be contiguous"
+    assert x.size(-1) % block_size == 0, (
+        f"Last dimension size must be divisible by block_size (block_size={block_size})"
+    )
+    _on_gpu(x)
+    _dtype(x, torch.bfloat16, "x")
+    N = x.size(-1)
+    y = torch.empty_like(x, dtype=FP8)
+    s = x.new_empty(*x.size()[:-1], N // block_size, dtype=torch.float32)
+    M = x.numel() // N if N else 0
+    rc = _lib.load().lfs_act_quant(_ptr(x), N, _ptr(y), _ptr(s), M, N, block_size,
+                                   int(scale_fmt is not None), _stream(x))
+    _lib.check(rc, "act_quant")
+    return y, s
+
+
+def weight_quant(x: torch.Tensor, block_size: int = 128) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-(block_size x block_size) quantisation of a [N, K] weight.
+
+    Same scale formula as act_quant over 2-D blocks; ragged tail blocks use
+    their valid elements.  Returns (y float8_e4m3fn [N, K],
+    s float32 [ceil(N/bs), ceil(K/bs)]).
+    """
+    assert x.is_contiguous(), "Input tensor must be contiguous"
+    assert x.dim() == 2, "Input tensor must have 2 dimensions"
+    _on_gpu(x)
+    _dtype(x, torch.bfloat16, "x")
+    N, K = x.shape
+    y = torch.empty_like(x, dtype=FP8)
+    s = x.new_empty(math.ceil(N / block_size), math.ceil(K / block_size), dtype=torch.float32)
+    rc = _lib.load().lfs_weight_quant(_ptr(x), _ptr(y), _ptr(s), N, K, block_size, _stream(x))
+    _lib.check(rc, "weight_quant")
+    return y, s
+
+
+def weight_dequant(x: torch.Tensor, s: torch.Tensor, block_size: int = 128) -> torch.Tensor:
+    """y = bf16(fp32(x) * s[n // bs, k // bs]) for a block-quantised weight."""
+    assert x.is_contiguous() and s.is_contiguous(), "Input tensors must be contiguous"
+    assert x.dim() == 2 and s.dim() == 2, "Input tensors must have 2 dimensions"
+    _on_gpu(x, s)
+    _dtype(x, FP8, "x")
+    _dtype(s, torch.float32, "s")
+    N, K = x.shape
+    assert s.shape == (math.ceil(N / block_size), math.ceil(K / block_size)), "scale shape mismatch"
+    y = torch.empty_like(x, dtype=torch.bfloat16)
+    rc = _lib.load().lfs_weight_dequant(_ptr(x), _ptr(s), _ptr(y), N, K, block_size, _stream(x))
+    _lib.check(rc, "weight_dequant")
+    return y
+
+
+def fp8_gemm(a: torch.Tensor, a_s: torch.Tensor, b: torch.Tensor, b_s: torch.Tensor,
+             bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """c = a @ b^T with 1x128 activation scales and 128x128 weight scales.
+
+    a: e4m3fn [..., K], a_s: fp32 [..., K/128]; b: e4m3fn [N, K] (nn.Linear
+    weight layout), b_s: fp32 [ceil(N/128), K/128]; bias: fp32 [N] or None.
+    The scale products are applied to each 128-wide K-block partial in an
+    fp32 accumulator; the result is rounded once to bf16 [..., N].
+    """
+    assert a.is_contiguous() and b.is_contiguous(), "Input tensors must be contiguous"
+    assert a_s.is_contiguous() and b_s.is_contiguous(), "Scaling factor tensors must be contiguous"
+    _on_gpu(a, a_s, b, b_s)
+    _dtype(a, FP8, "a")
+    _dtype(b, FP8, "b")
+    _dtype(a_s, torch.float32, "a_s")
+    _dtype(b_s, torch.float32, "b_s")
+    K = a.size(-1)
+    M = a.numel() // K if K else 0
+    N = b.size(0)
+    assert b.dim() == 2 and b.size(1) == K, "b must be [N, K]"
+    assert K % 128 == 0, "K must be a multiple of 128"
+    assert a_s.shape == (*a.shape[:-1], K // 128), "a_s must be [..., K/128]"
+    assert b_s.shape == (math.ceil(N / 128), K // 128), "b_s must be [ceil(N/128), K/128]"
+    if bias is not None:
+        _on_gpu(a, bias)
+        _dtype(bias, torch.float32, "bias")
+        assert bias.is_contiguous() and bias.shape == (N,), "bias must be fp32 [N]"
+    c = a.new_empty(*a.shape[:-1], N, dtype=torch.bfloat16)
+    rc = _lib.load().lfs_fp8_gemm(_ptr(a), _ptr(a_s), _ptr(b), _ptr(b_s), _ptr(bias), _ptr(c),
+                                  M, N, K, _stream(a))
+    _lib.check(rc, "fp8_gemm")
+    return c
+
+
+# ------------------------------------------------------------- paged KV path --
+def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                  v_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+    """k_cache.view(-1, Hkv, D)[slot_mapping[t]] = key[t] for slot != -1.
+
+    key/value: bf16 [T, Hkv, D] (heads and dims contiguous, any token stride);
+    caches: bf16 [num_blocks, block_size, Hkv, D] contiguous; slot_mapping:
+    int64 [T].  Slots outside the pool are skipped like -1.
+    """
+    N, num_heads, head_dim = key.shape
+    D = num_heads * head_dim
+    assert key.stride(-1) == 1 and value.stride(-1) == 1
+    assert key.stride(1) == head_dim and value.stride(1) == head_dim
+    assert k_cache.is_contiguous() and v_cache.is_contiguous()
+    assert k_cache.dim() == 4 and k_cache.shape[2:] == (num_heads, head_dim)
+    assert v_cache.shape == k_cache.shape and value.shape == key.shape
+    assert slot_mapping.numel() == N and slot_mapping.is_contiguous()
+    _on_gpu(key, value, k_cache, v_cache, slot_mapping)
+    for t, n in ((key, "key"), (value, "value"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _dtype(t, torch.bfloat16, n)
+    _dtype(slot_mapping, torch.int64, "slot_mapping")
+    num_slots = k_cache.shape[0] * k_cache.shape[1]
+    rc = _lib.load().lfs_store_kvcache(_ptr(key), key.stride(0), _ptr(value), value.stride(0),
+                                       _ptr(k_cache), _ptr(v_cache), _ptr(slot_mapping), N,
+                                       num_heads, head_dim, num_slots, _stream(key))
+    _lib.check(rc, "store_kvcache")
+
+
+def default_blocks_per_split(batch: int, max_blocks: int, block_size: int) -> int:
+    """KV blocks per split-K chunk: one 256-token block per workgroup at the
+    reference's block size, fewer larger chunks for small blocks."""
+    return max(1, 256 // max(block_size, 1))
+
+
+def paged_decode_workspace_bytes(batch: int, num_q_heads: int, head_dim: int, max_blocks: int,
+                                 blocks_per_split: int) -> int:
+    return int(_lib.load().lfs_paged_decode_workspace_bytes(batch, num_q_heads, head_dim,
+                                                            max_blocks, blocks_per_split))
+
+
+def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                           context_lens: torch.Tensor, block_tables: torch.Tensor,
+                           scale: Optional[float] = None, blocks_per_split: Optional[int] = None,
+                           workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """One decode step of GQA attention over a paged KV pool.
+
+    q: bf16 [B, Hq, D]; caches bf16 [num_blocks, block_size, Hkv, D];
+    context_lens int64 [B] (0 = padding row, output zeros); block_tables
+    int32 [B, max_blocks] padded with -1.  scale defaults to 1/sqrt(D) as
+    SDPA (model/attention/GQA.py:130).  Returns bf16 [B, Hq, D].
+    The grid depends only on B and max_blocks, so the call can be captured
+    in a HIP graph (pass a preallocated ``workspace`` of
+    ``paged_decode_workspace_bytes`` bytes to keep the capture free of
+    allocations).
+    """
+    assert q.dim() == 3 and q.is_contiguous(), "q must be contiguous [B, Hq, D]"
+    assert k_cache.is_contiguous() and v_cache.is_contiguous() and k_cache.shape == v_cache.shape
+    assert k_cache.dim() == 4, "caches must be [num_blocks, block_size, Hkv, D]"
+    assert block_tables.dim() == 2 and block_tables.stride(1) == 1, "block_tables must be [B, max_blocks]"
+    assert context_lens.is_contiguous() and context_lens.numel() == q.size(0)
+    _on_gpu(q, k_cache, v_cache, context_lens, block_tables)
+    for t, n in ((q, "q"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _dtype(t, torch.bfloat16, n)
+    _dtype(context_lens, torch.int64, "context_lens")
+    _dtype(block_tables, torch.int32, "block_tables")
+    B, Hq, D = q.shape
+    NB, BS, Hkv, Dk = k_cache.shape
+    assert Dk == D, "head_dim mismatch between q and the caches"
+    assert block_tables.size(0) == B
+    max_blocks = block_tables.size(1)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    bps = blocks_per_split or default_blocks_per_split(B, max_blocks, BS)
+    need = paged_decode_workspace_bytes(B, Hq, D, max_blocks, bps)
+    if workspace is None:
+        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=q.device)
+    o = torch.empty_like(q)
+    rc = _lib.load().lfs_paged_decode(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(context_lens),
+                                      _ptr(block_tables), block_tables.stride(0), _ptr(o),
+                                      _ptr(workspace), workspace.numel() * workspace.element_size(),
+                                      B, Hq, Hkv, D, BS, NB, max_blocks, float(scale), bps,
+                                      _stream(q))
+    _lib.check(rc, "paged_attention_decode")
+    return o

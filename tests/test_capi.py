@@ -1,0 +1,67 @@
+"""The C-ABI library loads and exports every symbol include/lfs_kernels.h
+declares; host-side argument checks fail with negative codes before any
+launch (no GPU work is done here)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from llm_from_scratch_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "lfs_kernels.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(lfs_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        pytest.fail("liblfs_kernels.so is not built (run __graft_entry__.build())")
+    return _lib.load()
+
+
+def test_header_and_binding_agree():
+    assert declared_symbols() == sorted(_lib.SIGNATURES)
+
+
+def test_every_declared_symbol_is_exported(lib):
+    raw = ctypes.CDLL(str(_lib.LIB_PATH))
+    for name in declared_symbols():
+        assert hasattr(raw, name), name
+    assert lib.lfs_abi_version() == _lib.ABI_VERSION
+
+
+def test_argument_errors_are_reported_without_launch(lib):
+    # block_size 100 is rejected on the host
+    rc = lib.lfs_act_quant(None, 128, None, None, 4, 128, 100, 0, None)
+    assert rc == -1 and b"block_size" in lib.lfs_last_error()
+    rc = lib.lfs_act_quant(None, 256, None, None, 4, 200, 128, 0, None)
+    assert rc == -1 and b"divisible" in lib.lfs_last_error()
+    rc = lib.lfs_fp8_gemm(None, None, None, None, None, None, 4, 4, 100, None)
+    assert rc == -1 and b"multiple of 128" in lib.lfs_last_error()
+    rc = lib.lfs_paged_decode(None, None, None, None, None, 4, None, None, 0, 2, 16, 4, 96, 256, 8, 4,
+                              0.1, 1, None)
+    assert rc == -1 and b"head_dim" in lib.lfs_last_error()
+    rc = lib.lfs_paged_decode(None, None, None, None, None, 4, None, None, 0, 2, 12, 5, 64, 256, 8, 4,
+                              0.1, 1, None)
+    assert rc == -1 and b"multiple of num_kv_heads" in lib.lfs_last_error()
+    with pytest.raises(ValueError, match="block_size"):
+        _lib.check(lib.lfs_weight_quant(None, None, None, 8, 8, 7, None), "weight_quant")
+
+
+def test_empty_shapes_are_no_ops(lib):
+    assert lib.lfs_act_quant(None, 128, None, None, 0, 128, 128, 0, None) == 0
+    assert lib.lfs_fp8_gemm(None, None, None, None, None, None, 0, 64, 128, None) == 0
+    assert lib.lfs_store_kvcache(None, 0, None, 0, None, None, None, 0, 4, 64, 0, None) == 0
+
+
+def test_workspace_bytes(lib):
+    # 4 bytes * B * splits * Hq * (D + 2)
+    assert lib.lfs_paged_decode_workspace_bytes(64, 16, 64, 16, 1) == 4 * 64 * 16 * 16 * 66
+    assert lib.lfs_paged_decode_workspace_bytes(3, 8, 128, 10, 4) == 4 * 3 * 3 * 8 * 130
+    assert lib.lfs_paged_decode_workspace_bytes(3, 8, 128, 10, 0) == -1

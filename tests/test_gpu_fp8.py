@@ -1,0 +1,215 @@
+"""GPU parity of the FP8 kernels against the CPU oracle (through the C ABI).
+
+Bar: act_quant / weight_quant codes and scales and weight_dequant outputs
+bit-exact; fp8_gemm within rtol 1e-2 / atol 2e-2 of the float64 oracle on
+the same codes and scales (bf16 output, fp32 accumulation), and bit-exact on
+small-integer operands with unit scales (every partial sum is an exact fp32
+integer, so the order of accumulation cannot matter).
+"""
+import numpy as np
+import pytest
+import torch
+
+from llm_from_scratch_amd import kernels as K
+from llm_from_scratch_amd import workloads as W
+from oracle import fp8 as F
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+RTOL, ATOL = 1e-2, 2e-2
+
+
+def codes(t):
+    return t.view(torch.uint8).cpu().numpy()
+
+
+def f32(t):
+    return t.float().cpu().numpy()
+
+
+def check_act_quant(x, block_size=128, scale_fmt=None):
+    y, s = K.act_quant(x, block_size, scale_fmt)
+    torch.cuda.synchronize()
+    ry, rs = F.act_quant(f32(x), block_size, scale_fmt)
+    assert y.dtype == torch.float8_e4m3fn and y.shape == x.shape
+    assert s.shape == (*x.shape[:-1], x.shape[-1] // block_size)
+    np.testing.assert_array_equal(f32(s), rs)
+    got = codes(y)
+    bad = np.argwhere(got != ry)
+    assert bad.size == 0, f"{len(bad)} code mismatches, first at {bad[:3].tolist()}"
+    return y, s
+
+
+# -------------------------------------------------------------- act_quant --
+def test_act_quant_cfg1():
+    check_act_quant(W.activation(256, 512, seed=0, outliers=False).to(DEV))
+
+
+@pytest.mark.parametrize("M", [1, 16, 128, 4096])
+@pytest.mark.parametrize("Kd", [1024, 4096, 2048])
+def test_act_quant_cfg2_outliers(M, Kd):
+    check_act_quant(W.activation(M, Kd, seed=1 + M + Kd).to(DEV))
+
+
+def test_act_quant_every_bf16_quotient():
+    """Groups whose amax is 448*2^k have s == 2^k exactly (448*fp32(1/448)
+    rounds to 1), so x/s runs over every bf16 value in [-448, 448]: an
+    exhaustive check of the divide + e4m3 rounding path incl. ties and
+    subnormals."""
+    bits = np.arange(1 << 16, dtype=np.uint32) << 16
+    vals = bits.view(np.float32)
+    vals = vals[np.isfinite(vals) & (np.abs(vals) <= 448)]
+    rows = []
+    for k in (0, -3, 5):
+        v = vals * np.float32(2.0 ** k)
+        n = -(-len(v) // 127)
+        v = np.concatenate([v, np.zeros(n * 127 - len(v), np.float32)]).reshape(n, 127)
+        grp = np.concatenate([np.full((n, 1), 448 * 2.0 ** k, np.float32), v], axis=1)
+        rows.append(grp)
+    x = torch.from_numpy(np.concatenate(rows).reshape(-1, 128)).to(torch.bfloat16)
+    y, s = check_act_quant(x.to(DEV))
+    sc = f32(s).reshape(-1)
+    assert set(np.unique(sc).tolist()) == {1.0, 2.0 ** -3, 32.0}
+
+
+def test_act_quant_edge_groups():
+    x = torch.randn(8, 256).to(torch.bfloat16)
+    x[0, :128] = 0.0
+    x[1, :128] = -0.0
+    x[2, :128] *= 1e-7                     # below the 1e-4 amax floor
+    x[3, :128] = torch.tensor(-1e-40)      # bf16 subnormal, negative
+    x[4, 5] = 3.0e38                       # huge amax, everything else -> +-0
+    x[5, :] = 448.0
+    x[6, :] = -1.0
+    check_act_quant(x.to(DEV))
+
+
+@pytest.mark.parametrize("bs", [32, 64, 128])
+def test_act_quant_block_sizes_and_ue8m0(bs):
+    x = W.activation(64, 512, seed=11).to(DEV)
+    check_act_quant(x, bs)
+    check_act_quant(x, bs, "ue8m0")
+
+
+def test_act_quant_batched_shape_and_asserts():
+    x = W.activation(6, 384, seed=12).reshape(2, 3, 384).to(DEV)
+    check_act_quant(x)
+    with pytest.raises(AssertionError, match="contiguous"):
+        K.act_quant(x.transpose(0, 1))
+    with pytest.raises(AssertionError, match="divisible"):
+        K.act_quant(W.activation(2, 200, seed=1).to(DEV))
+    y, s = K.act_quant(torch.empty(0, 256, dtype=torch.bfloat16, device=DEV))
+    assert y.shape == (0, 256) and s.shape == (0, 2)
+
+
+# ---------------------------------------------------- weight quant/dequant --
+@pytest.mark.parametrize("shape", [(1344, 512), (200, 136), (4096, 1024), (72, 8)])
+def test_weight_quant_bitexact(shape):
+    w = W.weight(*shape, seed=13).to(DEV)
+    y, s = K.weight_quant(w)
+    torch.cuda.synchronize()
+    ry, rs = F.weight_quant(f32(w))
+    np.testing.assert_array_equal(f32(s), rs)
+    np.testing.assert_array_equal(codes(y), ry)
+
+
+@pytest.mark.parametrize("shape", [(1344, 512), (200, 136), (5632, 2048)])
+def test_weight_dequant_bitexact(shape):
+    w = W.weight(*shape, seed=14).to(DEV)
+    y, s = K.weight_quant(w)
+    d = K.weight_dequant(y, s)
+    torch.cuda.synchronize()
+    ref = F.weight_dequant(codes(y), f32(s))
+    np.testing.assert_array_equal(f32(d), ref)
+    # and against torch's own fp32 product + bf16 cast of the same operands
+    st = s.repeat_interleave(128, 0).repeat_interleave(128, 1)[: shape[0], : shape[1]]
+    np.testing.assert_array_equal(f32(d), f32((y.float() * st).to(torch.bfloat16)))
+
+
+# ---------------------------------------------------------------- fp8_gemm --
+def gemm_oracle(a, a_s, b, b_s, bias=None, rows=None):
+    an, asn = codes(a), f32(a_s)
+    if rows is not None:
+        an, asn = an[rows], asn[rows]
+    return F.fp8_gemm(an, asn, codes(b), f32(b_s), None if bias is None else f32(bias))
+
+
+def assert_close(got, ref, what=""):
+    err = np.abs(got - ref)
+    tol = ATOL + RTOL * np.abs(ref)
+    bad = np.argwhere(err > tol)
+    assert bad.size == 0, f"{what}: {len(bad)} mismatches, worst {err.max():.4g}, first {bad[:3].tolist()}"
+
+
+def test_fp8_linear_cfg1():
+    """cfg1: quantise x (1x128) and W (128x128) on the GPU, GEMM, compare."""
+    x = W.activation(256, 512, seed=0, outliers=False).to(DEV)
+    w = W.weight(1344, 512, seed=100).to(DEV)
+    xq, xs = check_act_quant(x)
+    wq, ws = K.weight_quant(w)
+    c = K.fp8_gemm(xq, xs, wq, ws)
+    torch.cuda.synchronize()
+    assert c.shape == (256, 1344) and c.dtype == torch.bfloat16
+    assert_close(f32(c), gemm_oracle(xq, xs, wq, ws), "cfg1")
+    # the FP8 linear approximates the bf16 one
+    ref = (x.float() @ w.float().T).cpu().numpy()
+    assert np.abs(f32(c) - ref).max() < 0.1 * np.abs(ref).max()
+
+
+def test_fp8_gemm_exact_small_integers():
+    rng = np.random.default_rng(20)
+    M, N, Kd = 256, 320, 512
+    ints = np.arange(-8, 9, dtype=np.float32)
+    a = torch.from_numpy(F.e4m3_encode(rng.choice(ints, (M, Kd)))).view(torch.float8_e4m3fn).to(DEV)
+    b = torch.from_numpy(F.e4m3_encode(rng.choice(ints, (N, Kd)))).view(torch.float8_e4m3fn).to(DEV)
+    a_s = torch.ones(M, Kd // 128, device=DEV)
+    b_s = torch.ones(-(-N // 128), Kd // 128, device=DEV)
+    c = K.fp8_gemm(a, a_s, b, b_s)
+    exact = F.e4m3_decode(codes(a)).astype(np.int64) @ F.e4m3_decode(codes(b)).astype(np.int64).T
+    np.testing.assert_array_equal(f32(c), F.bf16_round(exact.astype(np.float32)))
+
+
+def test_fp8_gemm_random_codes_and_scales():
+    """Every byte pattern but NaN, distinct scale per (row, k-block) and per
+    (128-col block, k-block): catches a transposed or shifted scale index."""
+    rng = np.random.default_rng(21)
+    M, N, Kd = 300, 400, 640
+    ac = rng.integers(0, 256, (M, Kd), dtype=np.uint8)
+    bc = rng.integers(0, 256, (N, Kd), dtype=np.uint8)
+    ac[(ac & 0x7F) == 0x7F] = 0
+    bc[(bc & 0x7F) == 0x7F] = 0
+    a = torch.from_numpy(ac).view(torch.float8_e4m3fn).to(DEV)
+    b = torch.from_numpy(bc).view(torch.float8_e4m3fn).to(DEV)
+    a_s = torch.from_numpy(rng.uniform(1e-3, 1e-2, (M, Kd // 128)).astype(np.float32)).to(DEV)
+    b_s = torch.from_numpy(rng.uniform(1e-3, 1e-2, (-(-N // 128), Kd // 128)).astype(np.float32)).to(DEV)
+    bias = torch.from_numpy(rng.standard_normal(N).astype(np.float32)).to(DEV)
+    assert_close(f32(K.fp8_gemm(a, a_s, b, b_s)), gemm_oracle(a, a_s, b, b_s), "nobias")
+    assert_close(f32(K.fp8_gemm(a, a_s, b, b_s, bias)), gemm_oracle(a, a_s, b, b_s, bias), "bias")
+
+
+@pytest.mark.parametrize("M", [1, 16, 128, 4096])
+@pytest.mark.parametrize("KN", W.GEMM_KN)
+def test_fp8_gemm_cfg2_shapes(M, KN):
+    Kd, N = KN
+    x = W.activation(M, Kd, seed=30 + M).to(DEV)
+    w = W.weight(N, Kd, seed=31).to(DEV)
+    xq, xs = K.act_quant(x)
+    wq, ws = K.weight_quant(w)
+    c = K.fp8_gemm(xq, xs, wq, ws)
+    torch.cuda.synchronize()
+    rows = None if M <= 128 else np.random.default_rng(M).choice(M, 192, replace=False)
+    ref = gemm_oracle(xq, xs, wq, ws, rows=rows)
+    got = f32(c) if rows is None else f32(c)[rows]
+    assert_close(got, ref, f"M={M} K={Kd} N={N}")
+
+
+def test_fp8_gemm_m16384_sampled_rows():
+    Kd, N = 2048, 5632
+    x = W.activation(16384, Kd, seed=40).to(DEV)
+    w = W.weight(N, Kd, seed=41).to(DEV)
+    xq, xs = K.act_quant(x)
+    wq, ws = K.weight_quant(w)
+    c = K.fp8_gemm(xq, xs, wq, ws)
+    torch.cuda.synchronize()
+    rows = np.concatenate([[0, 16383], np.random.default_rng(3).choice(16384, 126, replace=False)])
+    assert_close(f32(c)[rows], gemm_oracle(xq, xs, wq, ws, rows=rows), "M=16384")

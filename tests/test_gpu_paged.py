@@ -1,0 +1,189 @@
+"""GPU parity of the paged-KV kernels against the CPU oracle (C ABI).
+
+Bar: store_kvcache bit-exact (and nothing else in the pool changes);
+paged decode within rtol 1e-2 / atol 2e-2 of the float64 oracle on the same
+bf16 inputs; properties that hold at any size: split-count independence,
+zero padding rows, L=1 -> v0.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from llm_from_scratch_amd import kernels as K
+from llm_from_scratch_amd import workloads as W
+from oracle import paged_kv as P
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+RTOL, ATOL = 1e-2, 2e-2
+
+
+def bits(t):
+    return t.view(torch.int16).cpu().numpy()
+
+
+def assert_close(got, ref, what=""):
+    err = np.abs(got - ref)
+    bad = np.argwhere(err > ATOL + RTOL * np.abs(ref))
+    assert bad.size == 0, f"{what}: {len(bad)} mismatches, worst {err.max():.4g}, first {bad[:3].tolist()}"
+
+
+# ----------------------------------------------------------- store_kvcache --
+@pytest.mark.parametrize("Hkv,D", [(4, 64), (8, 128), (3, 36)])
+def test_store_kvcache_bitexact(Hkv, D):
+    NB, BS, T = 64, 16, 200
+    g = torch.Generator(device=DEV).manual_seed(Hkv * D)
+    kc = torch.randn(NB, BS, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
+    vc = torch.randn(NB, BS, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
+    k0, v0 = bits(kc), bits(vc)
+    key = torch.randn(T, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
+    val = torch.randn(T, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
+    rng = np.random.default_rng(D)
+    slots = rng.choice(NB * BS, T, replace=False).astype(np.int64)
+    slots[::7] = -1
+    K.store_kvcache(key, val, kc, vc, torch.from_numpy(slots).to(DEV))
+    torch.cuda.synchronize()
+    P.store_kvcache(bits(key), bits(val), k0, v0, slots)
+    np.testing.assert_array_equal(bits(kc), k0)
+    np.testing.assert_array_equal(bits(vc), v0)
+
+
+def test_store_kvcache_strided_views_of_fused_qkv():
+    """key/value as column slices of a fused qkv projection output (token
+    stride = qkv width), as an attention layer produces them."""
+    T, Hq, Hkv, D, NB, BS = 37, 16, 4, 64, 8, 256
+    qkv = torch.randn(T, (Hq + 2 * Hkv) * D, device=DEV).to(torch.bfloat16)
+    k = qkv[:, Hq * D:(Hq + Hkv) * D].view(T, Hkv, D)
+    v = qkv[:, (Hq + Hkv) * D:].view(T, Hkv, D)
+    kc = torch.zeros(NB, BS, Hkv, D, device=DEV, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    slots = torch.arange(T, device=DEV, dtype=torch.int64) * 3
+    K.store_kvcache(k, v, kc, vc, slots)
+    torch.cuda.synchronize()
+    assert torch.equal(kc.view(-1, Hkv, D)[slots], k)
+    assert torch.equal(vc.view(-1, Hkv, D)[slots], v)
+    mask = torch.ones(NB * BS, dtype=torch.bool, device=DEV)
+    mask[slots] = False
+    assert not kc.view(-1, Hkv, D)[mask].any() and not vc.view(-1, Hkv, D)[mask].any()
+
+
+def test_store_kvcache_skips_all_padding():
+    kc = torch.ones(4, 16, 2, 64, device=DEV, dtype=torch.bfloat16)
+    vc = torch.ones_like(kc)
+    key = torch.zeros(5, 2, 64, device=DEV, dtype=torch.bfloat16)
+    K.store_kvcache(key, key, kc, vc, torch.full((5,), -1, device=DEV, dtype=torch.int64))
+    torch.cuda.synchronize()
+    assert bool((kc == 1).all()) and bool((vc == 1).all())
+
+
+# ------------------------------------------------------------ paged decode --
+def host_inputs(case, kc, vc, q):
+    """Copy only the referenced blocks to the host for the oracle."""
+    ids = W.referenced_blocks(case)
+    remap = np.full(case.num_blocks, -1, np.int64)
+    remap[ids] = np.arange(len(ids))
+    idt = torch.from_numpy(ids).to(DEV)
+    kh = kc[idt].float().cpu().numpy()
+    vh = vc[idt].float().cpu().numpy()
+    bt = case.block_tables
+    bt_local = np.where(bt >= 0, remap[np.maximum(bt, 0)], -1)
+    return q.float().cpu().numpy(), kh, vh, bt_local
+
+
+def run_decode(case, kc, vc, q, bps=None):
+    cl = torch.from_numpy(case.context_lens).to(DEV)
+    bt = torch.from_numpy(case.block_tables).to(DEV)
+    return K.paged_attention_decode(q, kc, vc, cl, bt, case.scale, blocks_per_split=bps)
+
+
+def make_q(case, seed):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    return torch.randn(case.batch, case.num_q_heads, case.head_dim, generator=g, device=DEV,
+                       dtype=torch.bfloat16)
+
+
+def test_paged_decode_cfg3_full():
+    case = W.paged_case("cfg3", seed=2)
+    kc, vc = W.fill_pool(case, seed=2, device=DEV, only_referenced=False)
+    q = make_q(case, 2)
+    o = run_decode(case, kc, vc, q)
+    torch.cuda.synchronize()
+    qh, kh, vh, bth = host_inputs(case, kc, vc, q)
+    ref = P.paged_decode(qh, kh, vh, case.context_lens, bth, case.scale)
+    assert_close(o.float().cpu().numpy(), ref, "cfg3")
+
+
+def test_paged_decode_cfg4_subset_full_pool():
+    """16 sequences of cfg4 over the full 65536-block pool (2^34 elements
+    per cache: exercises 64-bit addressing and long split-K reductions)."""
+    case = W.paged_case("cfg4", seed=3, batch=16)
+    kc, vc = W.fill_pool(case, seed=3, device=DEV, only_referenced=True)
+    q = make_q(case, 3)
+    o = run_decode(case, kc, vc, q)
+    torch.cuda.synchronize()
+    qh, kh, vh, bth = host_inputs(case, kc, vc, q)
+    ref = P.paged_decode(qh, kh, vh, case.context_lens, bth, case.scale)
+    assert_close(o.float().cpu().numpy(), ref, "cfg4-subset")
+    del kc, vc
+    torch.cuda.empty_cache()
+
+
+def test_paged_decode_split_independence():
+    case = W.paged_case("cfg3", seed=5, batch=12)
+    kc, vc = W.fill_pool(case, seed=5, device=DEV)
+    q = make_q(case, 5)
+    outs = [run_decode(case, kc, vc, q, bps).float() for bps in (1, 2, 3, 16)]
+    for o in outs[1:]:
+        assert_close(o.cpu().numpy(), outs[0].cpu().numpy(), "split")
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,BS", [(12, 4, 64, 256), (8, 8, 128, 16), (16, 2, 128, 32),
+                                         (32, 4, 64, 64), (6, 2, 64, 48)])
+def test_paged_decode_shapes(Hq, Hkv, D, BS):
+    rng = np.random.default_rng(Hq * 1000 + D + BS)
+    B, NB = 7, 128
+    lens = np.array([1, 0, BS, BS + 1, 3 * BS - 1, 5, 2 * BS], np.int64)
+    maxb = int((-(-lens // BS)).max()) + 1   # one extra -1 column
+    perm = rng.permutation(NB)
+    bt = np.full((B, maxb), -1, np.int32)
+    pos = 0
+    for b, L in enumerate(lens):
+        nb = -(-int(L) // BS)
+        bt[b, :nb] = perm[pos:pos + nb]
+        pos += nb
+    g = torch.Generator(device=DEV).manual_seed(7)
+    kc = torch.randn(NB, BS, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
+    vc = torch.randn(NB, BS, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
+    q = torch.randn(B, Hq, D, generator=g, device=DEV).to(torch.bfloat16)
+    scale = 1 / math.sqrt(D)
+    o = K.paged_attention_decode(q, kc, vc, torch.from_numpy(lens).to(DEV), torch.from_numpy(bt).to(DEV))
+    torch.cuda.synchronize()
+    ref = P.paged_decode(q.float().cpu().numpy(), kc.float().cpu().numpy(), vc.float().cpu().numpy(),
+                         lens, bt, scale)
+    got = o.float().cpu().numpy()
+    assert_close(got, ref, f"Hq={Hq} Hkv={Hkv} D={D} BS={BS}")
+    assert np.all(got[1] == 0)  # padding row
+    G = Hq // Hkv
+    v0 = vc[int(bt[0, 0]), 0].float().cpu().numpy()  # L=1 -> v0 of the matching kv head
+    assert_close(got[0], np.repeat(v0, G, axis=0), "L=1")
+
+
+def test_decode_step_store_then_attend():
+    """The decode step of the attention layer: write the new token's K/V at
+    its slot, then attend over the context including it."""
+    case = W.paged_case("cfg3", seed=8, batch=8)
+    kc, vc = W.fill_pool(case, seed=8, device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(9)
+    k_new = torch.randn(case.batch, case.num_kv_heads, case.head_dim, generator=g, device=DEV).to(torch.bfloat16)
+    v_new = torch.randn(case.batch, case.num_kv_heads, case.head_dim, generator=g, device=DEV).to(torch.bfloat16)
+    slots = P.decode_slots(case.block_tables, case.context_lens, case.block_size)
+    np.testing.assert_array_equal(slots, case.slot_mapping)
+    K.store_kvcache(k_new, v_new, kc, vc, torch.from_numpy(slots).to(DEV))
+    q = make_q(case, 9)
+    o = run_decode(case, kc, vc, q)
+    torch.cuda.synchronize()
+    qh, kh, vh, bth = host_inputs(case, kc, vc, q)
+    assert_close(o.float().cpu().numpy(), P.paged_decode(qh, kh, vh, case.context_lens, bth, case.scale),
+                 "store+decode")
