@@ -112,7 +112,7 @@ def bench_decode(name, device, reps, flush_buf):
                     dtype=torch.bfloat16)
     cl = torch.from_numpy(case.context_lens).to(device)
     bt = torch.from_numpy(case.block_tables).to(device)
-    bps = K.default_blocks_per_split(case.batch, bt.shape[1], case.block_size)
+    bps = K.default_blocks_per_split(case.batch, case.num_kv_heads, bt.shape[1], case.block_size)
     ws = torch.empty(K.paged_decode_workspace_bytes(case.batch, case.num_q_heads, case.head_dim,
                                                     bt.shape[1], bps), dtype=torch.uint8, device=device)
     fn = lambda: K.paged_attention_decode(q, kc, vc, cl, bt, case.scale, bps, ws)  # noqa: E731

@@ -120,8 +120,7 @@ int lfs_store_kvcache(const void* key, int64_t k_stride_t, const void* value, in
  * parallel and merged by log-sum-exp; the grid depends only on B and
  * max_blocks (not on the lengths), so the call is graph-capturable.
  * workspace: at least lfs_paged_decode_workspace_bytes(...) bytes.
- * D in {64, 128}; Hq % Hkv == 0, Hq/Hkv <= 8; Hkv*D/8 divides 256;
- * block_size a multiple of 16.
+ * D in {64, 128}; Hq % Hkv == 0, Hq/Hkv <= 8; block_size a multiple of 16.
  */
 int64_t lfs_paged_decode_workspace_bytes(int64_t B, int32_t num_q_heads, int32_t head_dim,
                                          int32_t max_blocks, int32_t blocks_per_split);

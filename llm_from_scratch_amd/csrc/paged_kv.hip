@@ -50,230 +50,290 @@ __global__ __launch_bounds__(128) void store_kvcache_kernel(
 }
 
 // ------------------------------------------------------------ decode split --
-constexpr int kThreads = 256;
-constexpr int kMaxTile = 128;
-constexpr int kUnroll = 8;  // 16-byte loads kept in flight per lane
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ void unpack8(const uint4& v, float* f) {
-  f[0] = bf16lo(v.x); f[1] = bf16hi(v.x);
-  f[2] = bf16lo(v.y); f[3] = bf16hi(v.y);
-  f[4] = bf16lo(v.z); f[5] = bf16hi(v.z);
-  f[6] = bf16lo(v.w); f[7] = bf16hi(v.w);
+// One wave per (sequence, kv head, chunk of the context).  Per tile of T
+// tokens (one KV block never straddled):
+//   K  : MFMA A operand straight from HBM -- lane l loads token (l % 16) of a
+//        16-token group, dims c*32 + (l / 16)*8 .. +7 (16 B);
+//   q^T: MFMA B operand, column j = l % 16 is query head kh*G + j (zero for
+//        j >= G), preloaded once;
+//   S  = K q^T with v_mfma_f32_16x16x32_bf16: lane l ends with the scores of
+//        head (l % 16) for tokens 4*(l / 16) .. +3 of each group, so the
+//        online-softmax max/sum per head is a 2-step xor over lanes 16, 32;
+//   P  goes through a wave-private LDS slice [T][G] to the P.V mapping;
+//   V  : lane l owns token (l / (D/8)) + (64/(D/8))*i and dims
+//        (l % (D/8))*8 .. +7 (coalesced 16-byte loads), fp32 FMAs into
+//        acc[G][8], rescaled by exp2(m_old - m_new) read from lane g.
+// Loads are software-pipelined one tile ahead (K of the next tile behind the
+// QK MFMAs, V of the next tile behind the P.V) with nontemporal 16-byte
+// loads, since every KV row is read exactly once.  There is no workgroup
+// barrier: waves exit independently.  A chunk that covers
+// the whole context writes the normalised bf16 output directly; otherwise
+// the unnormalised partial (o, m, l) goes to the workspace for the merge.
+template <int D>
+struct DecodeGeom {
+  static constexpr int LPR = D / 8;               // lanes per token row in the P.V mapping
+  static constexpr int TPI = 64 / LPR;            // tokens per V load instruction
+  static constexpr int T = (D == 64) ? 64 : 32;   // tokens per tile
+  static constexpr int NG = T / 16;               // 16-token MFMA groups per tile
+  static constexpr int NDC = D / 32;              // 32-wide head-dim chunks
+  static constexpr int UV = T / TPI;              // V loads per lane per tile
+};
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+// 16-byte streaming load (nontemporal: the KV rows are read exactly once)
+__device__ __forceinline__ uint4 nt_load16(const uint16_t* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 template <int D, int G>
-__global__ __launch_bounds__(kThreads) void paged_decode_split(
+__global__ __launch_bounds__(256) void paged_decode_split(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int64_t* __restrict__ ctx_lens,
     const int32_t* __restrict__ bt, int64_t bt_stride, float* __restrict__ ws_o,
-    float* __restrict__ ws_ml, int Hkv, int BS, int64_t NB, int max_blocks, int bps, int tile,
-    float scale_log2, int max_splits) {
-  constexpr int DV = D / 8;  // lanes per (token, kv head)
-  extern __shared__ __attribute__((aligned(16))) float smem[];
-  const int Hq = Hkv * G;
-  float* sS = smem;                  // [Hq][kMaxTile] scores / probabilities
-  float* sO = sS + Hq * kMaxTile;    // [Hq][D] cross-subgroup reduction
-  float* sM = sO + Hq * D;           // [Hq] running max (log2 domain)
-  float* sL = sM + Hq;               // [Hq] running sum
-  float* sA = sL + Hq;               // [Hq] per-tile rescale factor
+    float* __restrict__ ws_ml, uint16_t* __restrict__ out, int Hkv, int BS, int64_t NB,
+    int max_blocks, int bps, int tile, float scale_log2, int max_splits) {
+  using Geo = DecodeGeom<D>;
+  constexpr int GP = G <= 4 ? 4 : 8;  // padded heads per token in the P slice
+  __shared__ __attribute__((aligned(16))) float p_lds[4][Geo::T * GP];
 
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int kh = blockIdx.z * (blockDim.x >> 6) + wave;
+  if (kh >= Hkv) return;
   const int b = blockIdx.y, split = blockIdx.x;
-  const int64_t L = ctx_lens[b];
-  const int64_t cap = (int64_t)max_blocks * BS;
-  const int64_t t_begin = (int64_t)split * bps * BS;
-  const int64_t t_end = min(min(L, cap), t_begin + (int64_t)bps * BS);
-  if (t_begin >= t_end) return;  // whole workgroup leaves together
+  const int64_t Lc = min(ctx_lens[b], (int64_t)max_blocks * BS);
+  const int64_t chunk = (int64_t)bps * BS;
+  const int64_t t_begin = (int64_t)split * chunk;
+  const int64_t t_end = min(Lc, t_begin + chunk);
+  if (t_begin >= t_end) return;
+  const int Hq = Hkv * G;
+  const int64_t row = (int64_t)Hkv * D;
 
-  const int tid = threadIdx.x;
-  const int LPT = Hkv * DV;  // lanes per token row (divides 256, host-checked)
-  const int TPP = kThreads / LPT;
-  const int jl = tid & (LPT - 1);
-  const int kh = jl / DV, ds = jl % DV;
-  const int sub = tid / LPT;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int row_elems = Hkv * D;
-
-  float qf[G][8];
+  const int j = lane & 15, kq = lane >> 4;
+  v8bf qb[Geo::NDC];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const uint4 v = *reinterpret_cast<const uint4*>(q + ((int64_t)b * Hq + kh * G + g) * D + ds * 8);
-    unpack8(v, qf[g]);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) qf[g][e] *= scale_log2;
+  for (int c = 0; c < Geo::NDC; ++c) {
+    uint4 w = make_uint4(0, 0, 0, 0);
+    if (j < G) w = *reinterpret_cast<const uint4*>(q + ((int64_t)b * Hq + kh * G + j) * D + c * 32 + kq * 8);
+    qb[c] = __builtin_bit_cast(v8bf, w);
   }
+  const int ts = lane / Geo::LPR, dc = lane % Geo::LPR;
   float acc[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
-
-  for (int i = tid; i < Hq * D; i += kThreads) sO[i] = 0.f;
-  for (int i = tid; i < Hq; i += kThreads) {
-    sM[i] = -INFINITY;
-    sL[i] = 0.f;
-  }
-  __syncthreads();
-
+  float m_run = -INFINITY, l_run = 0.f;
+  float* pw = p_lds[wave];
   const int32_t* btrow = bt + (int64_t)b * bt_stride;
-  for (int64_t t0 = t_begin; t0 < t_end; t0 += tile) {
-    const int n = (int)min((int64_t)tile, t_end - t0);
+
+  // tile descriptor: valid token count (0 = masked) and element offset
+  auto tile_at = [&](int64_t t0, int& n, int64_t& off) {
+    n = (int)min((int64_t)tile, t_end - t0);
     const int32_t blk = btrow[t0 / BS];
-    const bool valid = blk >= 0 && (int64_t)blk < NB;
-    const int64_t base = ((int64_t)(valid ? blk : 0) * BS + (t0 % BS)) * row_elems + kh * D + ds * 8;
+    if (blk < 0 || (int64_t)blk >= NB) n = 0;  // invalid block: contributes nothing
+    off = ((int64_t)(n > 0 ? blk : 0) * BS + (t0 % BS)) * row + (int64_t)kh * D;
+  };
+  uint4 ka[Geo::NG][Geo::NDC];
+  uint4 va[Geo::UV];
+  auto load_k = [&](int n, int64_t off) {
+    const uint16_t* kb = kc + off;
+#pragma unroll
+    for (int g16 = 0; g16 < Geo::NG; ++g16) {
+      const int tok = g16 * 16 + j;
+#pragma unroll
+      for (int c = 0; c < Geo::NDC; ++c)
+        ka[g16][c] = tok < n ? nt_load16(kb + tok * row + c * 32 + kq * 8) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto load_v = [&](int n, int64_t off) {
+    const uint16_t* vb = vc + off;
+#pragma unroll
+    for (int i = 0; i < Geo::UV; ++i) {
+      const int tok = ts + Geo::TPI * i;
+      va[i] = tok < n ? nt_load16(vb + tok * row + dc * 8) : make_uint4(0, 0, 0, 0);
+    }
+  };
 
-    // ---- phase A: scores for this tile
-    for (int p0 = sub; p0 < tile; p0 += TPP * kUnroll) {
-      uint4 kv[kUnroll];
+  // Software pipeline without extra registers: K of tile i+1 is requested as
+  // soon as the QK MFMAs of tile i have consumed ka, V of tile i+1 as soon as
+  // the P.V of tile i has consumed va, so one tile is always in flight.
+  int n_cur;
+  int64_t off_cur;
+  tile_at(t_begin, n_cur, off_cur);
+  load_k(n_cur, off_cur);
+  load_v(n_cur, off_cur);
+  for (int64_t t0 = t_begin; t0 < t_end; t0 += tile) {
+    const int n = n_cur;
+    const bool has_next = t0 + tile < t_end;
+    int n_nxt = 0;
+    int64_t off_nxt = 0;
+    if (has_next) tile_at(t0 + tile, n_nxt, off_nxt);
+
+    // ---- scores (log2 domain) and online-softmax update for head j
+    float s[Geo::NG][4];
+    float tmax = -INFINITY;
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int p = p0 + u * TPP;
-        kv[u] = (valid && p < n) ? *reinterpret_cast<const uint4*>(kc + base + (int64_t)p * row_elems)
-                                 : make_uint4(0, 0, 0, 0);
-      }
+    for (int g16 = 0; g16 < Geo::NG; ++g16) {
+      v4f sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int p = p0 + u * TPP;
-        float kf[8];
-        unpack8(kv[u], kf);
-        float sc[G];
+      for (int c = 0; c < Geo::NDC; ++c)
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, ka[g16][c]), qb[c], sc, 0, 0, 0);
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-          float d = 0.f;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) d = fmaf(qf[g][e], kf[e], d);
-          sc[g] = group_sum<DV>(d);
-        }
-        if (ds == 0 && p < tile) {
-          const bool live = valid && p < n;
-#pragma unroll
-          for (int g = 0; g < G; ++g) sS[(kh * G + g) * kMaxTile + p] = live ? sc[g] : -INFINITY;
-        }
+      for (int r = 0; r < 4; ++r) {
+        const int tok = g16 * 16 + kq * 4 + r;
+        s[g16][r] = tok < n ? sc[r] * scale_log2 : -INFINITY;
+        tmax = fmaxf(tmax, s[g16][r]);
       }
     }
-    __syncthreads();
-
-    // ---- phase B: online softmax update, one wave per head
-    for (int h = wave; h < Hq; h += kThreads / 64) {
-      float* srow = sS + h * kMaxTile;
-      const float v0 = lane < tile ? srow[lane] : -INFINITY;
-      const float v1 = lane + 64 < tile ? srow[lane + 64] : -INFINITY;
-      const float tmax = group_max<64>(fmaxf(v0, v1));
-      const float m_old = sM[h];
-      const float m_new = fmaxf(m_old, tmax);
-      float p0 = 0.f, p1 = 0.f, alpha = 1.f;
-      if (m_new != -INFINITY) {
-        p0 = exp2f(v0 - m_new);
-        p1 = exp2f(v1 - m_new);
-        alpha = exp2f(m_old - m_new);
+    if (has_next) load_k(n_nxt, off_nxt);
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m_run, tmax);
+    const bool live = m_new != -INFINITY;
+    const float alpha = live ? exp2f(m_run - m_new) : 1.f;
+    float psum = 0.f;
+#pragma unroll
+    for (int g16 = 0; g16 < Geo::NG; ++g16)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = live ? exp2f(s[g16][r] - m_new) : 0.f;
+        psum += p;
+        if (j < G) pw[(g16 * 16 + kq * 4 + r) * GP + j] = p;
       }
-      if (lane < tile) srow[lane] = p0;
-      if (lane + 64 < tile) srow[lane + 64] = p1;
-      const float psum = group_sum<64>(p0 + p1);
-      if (lane == 0) {
-        sM[h] = m_new;
-        sL[h] = sL[h] * alpha + psum;
-        sA[h] = alpha;
-      }
-    }
-    __syncthreads();
+    psum += __shfl_xor(psum, 16, 64);
+    psum += __shfl_xor(psum, 32, 64);
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+    wave_lds_sync();
 
-    // ---- phase C: P.V
+    // ---- P.V
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float a = sA[kh * G + g];
+      const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), g));
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[g][e] *= a;
     }
-    if (valid) {
-      for (int p0 = sub; p0 < n; p0 += TPP * kUnroll) {
-        uint4 vv[kUnroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-          const int p = p0 + u * TPP;
-          vv[u] = p < n ? *reinterpret_cast<const uint4*>(vc + base + (int64_t)p * row_elems)
-                        : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < Geo::UV; ++i) {
+      const int tok = ts + Geo::TPI * i;
+      if (tok < n) {
+        float vf[8];
+        unpack8(va[i], vf);
+        float pg[GP];
+#pragma unroll
+        for (int g4 = 0; g4 < GP; g4 += 4) {
+          const float4 p4 = *reinterpret_cast<const float4*>(&pw[tok * GP + g4]);
+          pg[g4] = p4.x; pg[g4 + 1] = p4.y; pg[g4 + 2] = p4.z; pg[g4 + 3] = p4.w;
         }
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-          const int p = p0 + u * TPP;
-          if (p < n) {
-            float vf[8];
-            unpack8(vv[u], vf);
+        for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-              const float w = sS[(kh * G + g) * kMaxTile + p];
-#pragma unroll
-              for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(w, vf[e], acc[g][e]);
-            }
-          }
-        }
+          for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pg[g], vf[e], acc[g][e]);
       }
     }
-    __syncthreads();
+    if (has_next) load_v(n_nxt, off_nxt);
+    wave_lds_sync();
+    n_cur = n_nxt;
+    off_cur = off_nxt;
   }
 
-  // ---- reduce the token subgroups, write the chunk partial
+  // ---- reduce the token subgroups (lanes with the same dc)
 #pragma unroll
-  for (int g = 0; g < G; ++g)
+  for (int o = Geo::LPR; o < 64; o <<= 1)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) atomicAdd(&sO[(kh * G + g) * D + ds * 8 + e], acc[g][e]);
-  __syncthreads();
-  const int64_t pbase = (int64_t)b * max_splits + split;
-  float* wo = ws_o + pbase * Hq * D;
-  for (int i = tid; i < Hq * D; i += kThreads) wo[i] = sO[i];
-  for (int h = tid; h < Hq; h += kThreads) {
-    ws_ml[(pbase * Hq + h) * 2 + 0] = sM[h];
-    ws_ml[(pbase * Hq + h) * 2 + 1] = sL[h];
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] += __shfl_xor(acc[g][e], o, 64);
+
+  if (t_begin == 0 && t_end >= Lc) {
+    // the whole context is in this chunk: normalise and write bf16
+    if (ts == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float lg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l_run), g));
+        const float inv = lg > 0.f ? 1.f / lg : 0.f;
+        uint4 o;
+        o.x = pack_bf16x2(acc[g][0] * inv, acc[g][1] * inv);
+        o.y = pack_bf16x2(acc[g][2] * inv, acc[g][3] * inv);
+        o.z = pack_bf16x2(acc[g][4] * inv, acc[g][5] * inv);
+        o.w = pack_bf16x2(acc[g][6] * inv, acc[g][7] * inv);
+        *reinterpret_cast<uint4*>(out + ((int64_t)b * Hq + kh * G + g) * D + dc * 8) = o;
+      }
+    }
+  } else {
+    const int64_t pbase = (int64_t)b * max_splits + split;
+    if (ts == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float* dst = ws_o + (pbase * Hq + kh * G + g) * D + dc * 8;
+        *reinterpret_cast<float4*>(dst) = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+        *reinterpret_cast<float4*>(dst + 4) = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
+      }
+    }
+    if (lane < G) {
+      ws_ml[(pbase * Hq + kh * G + lane) * 2 + 0] = m_run;
+      ws_ml[(pbase * Hq + kh * G + lane) * 2 + 1] = l_run;
+    }
   }
 }
 
 // ------------------------------------------------------------ decode merge --
-__global__ __launch_bounds__(256) void paged_decode_merge(
+// One workgroup per (head, sequence), one lane per head dim.  Sequences whose
+// context fits one chunk were finished by the split kernel; padding rows
+// (context 0) get zeros.
+__global__ __launch_bounds__(128) void paged_decode_merge(
     const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
     const int64_t* __restrict__ ctx_lens, uint16_t* __restrict__ out, int Hq, int D, int BS,
     int max_blocks, int bps, int max_splits) {
-  const int b = blockIdx.x;
-  const int64_t L = min(ctx_lens[b], (int64_t)max_blocks * BS);
+  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  const int64_t Lc = min(ctx_lens[b], (int64_t)max_blocks * BS);
   const int64_t chunk = (int64_t)bps * BS;
-  const int ns = L > 0 ? (int)min((L + chunk - 1) / chunk, (int64_t)max_splits) : 0;
-  const int64_t pbase = (int64_t)b * max_splits;
-  for (int i = threadIdx.x; i < Hq * D; i += blockDim.x) {
-    const int h = i / D;
-    float res = 0.f;
-    if (ns > 0) {
-      float M = -INFINITY;
-      for (int s = 0; s < ns; ++s) M = fmaxf(M, ws_ml[((pbase + s) * Hq + h) * 2]);
-      float num = 0.f, den = 0.f;
-      if (M != -INFINITY) {
-        for (int s = 0; s < ns; ++s) {
-          const float m = ws_ml[((pbase + s) * Hq + h) * 2];
-          const float w = exp2f(m - M);
-          den = fmaf(w, ws_ml[((pbase + s) * Hq + h) * 2 + 1], den);
-          num = fmaf(w, ws_o[(pbase + s) * Hq * D + i], num);
-        }
+  const int ns = (int)((Lc + chunk - 1) / chunk);
+  if (ns == 1 || d >= D) return;
+  float res = 0.f;
+  if (ns > 1) {
+    const int64_t pbase = (int64_t)b * max_splits;
+    float M = -INFINITY;
+    for (int s = 0; s < ns; ++s) M = fmaxf(M, ws_ml[((pbase + s) * Hq + h) * 2]);
+    float num = 0.f, den = 0.f;
+    if (M != -INFINITY) {
+      for (int s = 0; s < ns; ++s) {
+        const float w = exp2f(ws_ml[((pbase + s) * Hq + h) * 2] - M);
+        den = fmaf(w, ws_ml[((pbase + s) * Hq + h) * 2 + 1], den);
+        num = fmaf(w, ws_o[((pbase + s) * Hq + h) * D + d], num);
       }
-      res = den > 0.f ? num / den : 0.f;
     }
-    out[(int64_t)b * Hq * D + i] = (uint16_t)f32_to_bf16(res);
+    res = den > 0.f ? num / den : 0.f;
   }
+  out[((int64_t)b * Hq + h) * D + d] = (uint16_t)f32_to_bf16(res);
 }
 
 template <int D, int G>
-void launch_split(dim3 grid, size_t shmem, hipStream_t st, const uint16_t* q, const uint16_t* kc,
+void launch_split(dim3 grid, dim3 block, hipStream_t st, const uint16_t* q, const uint16_t* kc,
                   const uint16_t* vc, const int64_t* cl, const int32_t* bt, int64_t bts, float* wo,
-                  float* wml, int Hkv, int BS, int64_t NB, int max_blocks, int bps, int tile,
-                  float sl2, int max_splits) {
-  hipLaunchKernelGGL((paged_decode_split<D, G>), grid, dim3(kThreads), shmem, st, q, kc, vc, cl, bt,
-                     bts, wo, wml, Hkv, BS, NB, max_blocks, bps, tile, sl2, max_splits);
+                  float* wml, uint16_t* out, int Hkv, int BS, int64_t NB, int max_blocks, int bps,
+                  int tile, float sl2, int max_splits) {
+  hipLaunchKernelGGL((paged_decode_split<D, G>), grid, block, 0, st, q, kc, vc, cl, bt, bts, wo, wml,
+                     out, Hkv, BS, NB, max_blocks, bps, tile, sl2, max_splits);
 }
 
 template <int D>
-bool dispatch_g(int G, dim3 grid, size_t shmem, hipStream_t st, const uint16_t* q,
+bool dispatch_g(int G, dim3 grid, dim3 block, hipStream_t st, const uint16_t* q,
                 const uint16_t* kc, const uint16_t* vc, const int64_t* cl, const int32_t* bt,
-                int64_t bts, float* wo, float* wml, int Hkv, int BS, int64_t NB, int max_blocks,
-                int bps, int tile, float sl2, int max_splits) {
+                int64_t bts, float* wo, float* wml, uint16_t* out, int Hkv, int BS, int64_t NB,
+                int max_blocks, int bps, int tile, float sl2, int max_splits) {
 #define LFS_G(GG) \
-  case GG: launch_split<D, GG>(grid, shmem, st, q, kc, vc, cl, bt, bts, wo, wml, Hkv, BS, NB, max_blocks, bps, tile, sl2, max_splits); return true;
+  case GG: launch_split<D, GG>(grid, block, st, q, kc, vc, cl, bt, bts, wo, wml, out, Hkv, BS, NB, max_blocks, bps, tile, sl2, max_splits); return true;
   switch (G) {
     LFS_G(1) LFS_G(2) LFS_G(3) LFS_G(4) LFS_G(5) LFS_G(6) LFS_G(7) LFS_G(8)
     default: return false;
@@ -333,9 +393,6 @@ extern "C" int lfs_paged_decode(const void* q, const void* k_cache, const void* 
   LFS_REQUIRE(D == 64 || D == 128, "paged_decode: head_dim must be 64 or 128 (got %d)", D);
   LFS_REQUIRE(Hq % Hkv == 0 && Hq / Hkv <= 8,
               "paged_decode: num_q_heads (%d) must be a multiple of num_kv_heads (%d), ratio <= 8", Hq, Hkv);
-  const int LPT = Hkv * (D / 8);
-  LFS_REQUIRE(LPT <= 256 && (256 % LPT) == 0,
-              "paged_decode: num_kv_heads*head_dim/8 (%d) must divide 256", LPT);
   LFS_REQUIRE(BS % 16 == 0, "paged_decode: block_size must be a multiple of 16 (got %d)", BS);
   LFS_REQUIRE(blocks_per_split > 0, "paged_decode: blocks_per_split must be positive");
   LFS_REQUIRE(bt_stride >= max_blocks, "paged_decode: block table stride < max_blocks");
@@ -353,28 +410,32 @@ extern "C" int lfs_paged_decode(const void* q, const void* k_cache, const void* 
   float* ws_o = (float*)workspace;
   float* ws_ml = ws_o + (size_t)B * max_splits * Hq * D;
   hipStream_t st = (hipStream_t)stream;
+  const int Tmax = D == 64 ? 64 : 32;
   int tile = 16;
-  for (int t = kMaxTile; t >= 16; t >>= 1)
+  for (int t = Tmax; t >= 16; t >>= 1)
     if (BS % t == 0) { tile = t; break; }
   const float sl2 = scale * 1.4426950408889634f;
   if (max_splits > 0) {
-    const dim3 grid((unsigned)max_splits, (unsigned)B);
-    const size_t shmem = sizeof(float) * ((size_t)Hq * kMaxTile + (size_t)Hq * D + 3 * (size_t)Hq);
-    LFS_REQUIRE(shmem <= 64 * 1024, "paged_decode: too many heads for LDS (%d)", Hq);
+    const int wpg = Hkv < 4 ? Hkv : 4;  // waves (kv heads) per workgroup
+    const dim3 grid((unsigned)max_splits, (unsigned)B, (unsigned)((Hkv + wpg - 1) / wpg));
+    LFS_REQUIRE(grid.z < 65536u, "paged_decode: too many kv heads");
+    const dim3 block((unsigned)(64 * wpg));
     const int G = Hq / Hkv;
     const bool ok = D == 64
-        ? dispatch_g<64>(G, grid, shmem, st, (const uint16_t*)q, (const uint16_t*)k_cache,
+        ? dispatch_g<64>(G, grid, block, st, (const uint16_t*)q, (const uint16_t*)k_cache,
                          (const uint16_t*)v_cache, context_lens, block_tables, bt_stride, ws_o,
-                         ws_ml, Hkv, BS, num_blocks, max_blocks, blocks_per_split, tile, sl2, max_splits)
-        : dispatch_g<128>(G, grid, shmem, st, (const uint16_t*)q, (const uint16_t*)k_cache,
+                         ws_ml, (uint16_t*)out, Hkv, BS, num_blocks, max_blocks, blocks_per_split,
+                         tile, sl2, max_splits)
+        : dispatch_g<128>(G, grid, block, st, (const uint16_t*)q, (const uint16_t*)k_cache,
                           (const uint16_t*)v_cache, context_lens, block_tables, bt_stride, ws_o,
-                          ws_ml, Hkv, BS, num_blocks, max_blocks, blocks_per_split, tile, sl2, max_splits);
+                          ws_ml, (uint16_t*)out, Hkv, BS, num_blocks, max_blocks, blocks_per_split,
+                          tile, sl2, max_splits);
     LFS_REQUIRE(ok, "paged_decode: unsupported group size %d", G);
     const int rc = check_launch("paged_decode(split)");
     if (rc) return rc;
   }
-  hipLaunchKernelGGL(paged_decode_merge, dim3((unsigned)B), dim3(256), 0, st, ws_o, ws_ml,
-                     context_lens, (uint16_t*)out, Hq, D, BS, max_blocks, blocks_per_split,
-                     max_splits);
+  hipLaunchKernelGGL(paged_decode_merge, dim3((unsigned)Hq, (unsigned)B), dim3((unsigned)D), 0, st,
+                     ws_o, ws_ml, context_lens, (uint16_t*)out, Hq, D, BS, max_blocks,
+                     blocks_per_split, max_splits);
   return check_launch("paged_decode(merge)");
 }

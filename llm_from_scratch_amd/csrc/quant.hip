@@ -38,13 +38,6 @@ __device__ __forceinline__ float qdiv(float x, float s) {
   return q;
 }
 
-__device__ __forceinline__ void unpack8(const uint4& v, float* f) {
-  f[0] = bf16lo(v.x); f[1] = bf16hi(v.x);
-  f[2] = bf16lo(v.y); f[3] = bf16hi(v.y);
-  f[4] = bf16lo(v.z); f[5] = bf16hi(v.z);
-  f[6] = bf16lo(v.w); f[7] = bf16hi(v.w);
-}
-
 __device__ __forceinline__ uint2 quant8(const float* f, float s) {
   uint2 o;
   o.x = f32x4_to_e4m3(qdiv(f[0], s), qdiv(f[1], s), qdiv(f[2], s), qdiv(f[3], s));

@@ -175,10 +175,17 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
     _lib.check(rc, "store_kvcache")
 
 
-def default_blocks_per_split(batch: int, max_blocks: int, block_size: int) -> int:
-    """KV blocks per split-K chunk: one 256-token block per workgroup at the
-    reference's block size, fewer larger chunks for small blocks."""
-    return max(1, 256 // max(block_size, 1))
+def default_blocks_per_split(batch: int, num_kv_heads: int, max_blocks: int, block_size: int) -> int:
+    """KV blocks per split-K chunk (shapes only, so the choice is capturable).
+
+    The kernel runs one wave per (sequence, kv head, chunk).  Chunks of 256
+    tokens keep the most waves in flight, which is what HBM streaming needs
+    once there are enough (sequence, kv head) pairs (>= 1024); with fewer
+    pairs, 512-token chunks halve the merge work.  Measured on MI355X: cfg4
+    (2048 pairs) is fastest at 256 tokens, cfg3 (256 pairs) at 512."""
+    base = max(1, 256 // max(block_size, 1))
+    bps = base if batch * num_kv_heads >= 1024 else 2 * base
+    return max(1, min(bps, max(max_blocks, 1)))
 
 
 def paged_decode_workspace_bytes(batch: int, num_q_heads: int, head_dim: int, max_blocks: int,
@@ -219,7 +226,7 @@ def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     max_blocks = block_tables.size(1)
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    bps = blocks_per_split or default_blocks_per_split(B, max_blocks, BS)
+    bps = blocks_per_split or default_blocks_per_split(B, Hkv, max_blocks, BS)
     need = paged_decode_workspace_bytes(B, Hq, D, max_blocks, bps)
     if workspace is None:
         workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=q.device)
