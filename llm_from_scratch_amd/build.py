@@ -29,6 +29,9 @@ HIPCC_FLAGS = [
     "-shared",
     # no packed fp32 (v_pk_*_f32) instructions in any generated code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs: the accumulators are scaled by VALU FMAs, which
+    # cannot read AGPRs (an AGPR result costs one v_accvgpr_read per element)
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     # IEEE fp32 divide (act_quant's x / s must be correctly rounded)
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-fno-fast-math",

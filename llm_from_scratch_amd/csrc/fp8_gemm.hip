@@ -8,18 +8,21 @@
 // (4 FMAs per tile per K block).  The scales are arbitrary fp32 values, so the
 // hardware's power-of-two (E8M0) operand scaling cannot carry them.
 //
-// Workgroup tile 128x128, four waves in a 2x2 grid, 64x64 per wave (4x4 MFMA
-// tiles).  A and B K-tiles (16 KB each) are staged through LDS with a double
-// buffer: the next K block's global loads are issued before the current
-// block's MFMAs and written to the other LDS buffer afterwards, so one
-// barrier per K block suffices.  16-byte chunks are XOR-swizzled within each
-// 128-byte LDS row to spread the MFMA operand reads over the banks.
+// Workgroup tile 128x128 (one weight-scale block wide), four waves in a 2x2
+// grid, 64x64 per wave (4x4 MFMA tiles).  A and B K-tiles (16 KB each) are
+// copied global -> LDS by DMA (no register staging) into a ring of NST
+// stages; the activation scales follow in chunks of whole rows.
 //
-// MFMA operand convention: lane l supplies row (l % 16) of A and row (l % 16)
-// of B (= column of C) and the 32 bytes [32*(l/16), 32*(l/16)+32) of the
-// 128-byte K block; A and B use the same K assignment, so the dot products
-// pair the same K indices whatever order the instruction sums them in.  The
-// 16x16 fp32 result in lane l is column (l % 16), rows 4*(l/16) .. +3.
+// MFMA operand convention: lane l supplies row (l % 16) of each operand and
+// the 32 bytes [32*(l/16), 32*(l/16)+32) of the 128-byte K block; both
+// operands use the same K assignment, so the dot products pair the same K
+// indices whatever order the instruction sums them in.  The 16x16 fp32
+// result D = X Y^T in lane l is column (l % 16), rows 4*(l/16) .. +3.
+//
+// Tile order: workgroup ids are dealt round-robin to the 8 XCDs, so the id
+// is remapped to give each XCD a contiguous range of tiles, walked in groups
+// of 8 row-tiles so that concurrently running tiles share A rows and B
+// columns in that XCD's L2.
 #include "common.h"
 
 namespace lfs {
@@ -27,11 +30,15 @@ namespace {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 128, BN = 128, BK = 128;
+constexpr int GROUP_M = 8;
 
-__device__ __forceinline__ int swz(int row, int chunk) {
-  return row * BK + ((chunk ^ (row & 7)) << 4);
+__device__ __forceinline__ v8i frag(const uint8_t* tile, int off_lo, int off_hi) {
+  const u32x4 lo = *reinterpret_cast<const u32x4*>(tile + off_lo);
+  const u32x4 hi = *reinterpret_cast<const u32x4*>(tile + off_hi);
+  return __builtin_bit_cast(v8i, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
 __device__ __forceinline__ v4f mfma_fp8(const v8i& a, const v8i& b) {
@@ -40,49 +47,140 @@ __device__ __forceinline__ v4f mfma_fp8(const v8i& a, const v8i& b) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 0, 0, 0, 0, 0);
 }
 
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+  return (unsigned)(uintptr_t)(const lds_u8*)p;
+}
+
+// Direct global -> LDS loads (no VGPR staging).  Lane i's 16 (or 4) bytes
+// land at LDS address m0 + 16*i (or 4*i).  Issued through inline asm so that
+// the compiler does not pessimise every later LDS read with vmcnt(0); the
+// kernel waits for them explicitly (wait_vm) before its barrier.  m0 is saved
+// and restored around the load.
+__device__ __forceinline__ void dma16(const void* g, unsigned lds) {
+  unsigned tmp;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(tmp) : "s"(lds), "v"(g) : "memory");
+}
+__device__ __forceinline__ void dma4(const void* g, unsigned lds) {
+  unsigned tmp;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dword %2, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(tmp) : "s"(lds), "v"(g) : "memory");
+}
+// s_waitcnt vmcnt(N), other counters unconstrained
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// LDS tile layout: 128-byte rows; 16-byte chunk c of row r is stored in
+// chunk slot c ^ f(r), f(r) = ((r >> 1) & 7) ^ ((r & 1) << 2), which spreads
+// the MFMA operand reads (16 rows x one chunk per 16 lanes) over the banks.
+// Each DMA instruction fills 8 whole rows: lane l writes slot (l & 7) of row
+// 8s + (l >> 3), so it fetches logical chunk (l & 7) ^ f(row) -- 8 complete
+// 128-byte lines per instruction, the access pattern the load path streams
+// at full L2 bandwidth (a permutation inside a line costs nothing, a 16-byte
+// gather over 16 rows costs 3x).
+__device__ __forceinline__ int swz(int r, int c) {
+  return r * BK + ((c ^ (((r >> 1) & 7) ^ ((r & 1) << 2))) << 4);
+}
+
+constexpr int SCK = 16;        // K blocks of scale products held in LDS at a time
+constexpr int SCP = BM + 1;     // padded row of the k-major scale table
+
+// NST-stage pipeline: K blocks kt+1 .. kt+NST-2 are in flight while block kt
+// is multiplied; the buffer refilled at iteration kt is the one consumed at
+// kt-1, which every wave has left once it passes the iteration's barrier.
+// With NST = 2 a workgroup uses 80 KB of LDS and two share a CU, so one
+// workgroup's barrier and LDS waits are covered by the other's MFMAs.
+// Activation scales are staged per chunk of SCK K blocks ([128][SCK] floats,
+// ordinary loads) instead of one strided 4-byte gather per K block.
+template <int NST>
 __global__ __launch_bounds__(256, 2) void fp8_gemm_128x128(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ B,
     const float* __restrict__ Bs, const float* __restrict__ bias, uint16_t* __restrict__ C, int M,
-    int N, int K) {
-  __shared__ __attribute__((aligned(16))) uint8_t sA[2][BM * BK];
-  __shared__ __attribute__((aligned(16))) uint8_t sB[2][BN * BK];
-  __shared__ __attribute__((aligned(16))) float sAs[2][BM];
+    int N, int K, int tiles_m, int tiles_n) {
+  constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK;
+  constexpr int STAGE = A_BYTES + B_BYTES;
+  constexpr int A_PER_WAVE = A_BYTES / 1024 / 4;  // 1 KB (8-row) segments per wave
+  constexpr int B_PER_WAVE = B_BYTES / 1024 / 4;
+  constexpr int LOADS = A_PER_WAVE + B_PER_WAVE;  // DMA instructions per wave per stage
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * STAGE];
+  __shared__ __attribute__((aligned(16))) float ssc[SCK * SCP];
+
+  // ---- tile order (XCD-contiguous ranges, grouped rows)
+  int pid = blockIdx.x;
+  const int ntiles = tiles_m * tiles_n;
+  if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
+  const int group = pid / (GROUP_M * tiles_n);
+  const int first_m = group * GROUP_M;
+  const int gsize = min(tiles_m - first_m, GROUP_M);
+  const int tm = first_m + (pid % gsize);
+  const int tn = (pid % (GROUP_M * tiles_n)) / gsize;
+  const int m0 = tm * BM, n0 = tn * BN;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
   const int KT = K / BK;
+  const int r16 = lane & 15, g = lane >> 4;
 
-  uint4 ra[4], rb[4];
-  float ras = 0.f;
-  auto gload = [&](int kt) {
+  // ---- DMA sources: segment q = wave + 4u covers tile rows 8q .. 8q+7
+  // (rows past M / N are clamped; their results are never stored)
+  const uint8_t* srcA[A_PER_WAVE];
+  const uint8_t* srcB[B_PER_WAVE];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + 256 * i;
-      const int row = c >> 3, ch = c & 7;
-      const int gm = m0 + row, gn = n0 + row;
-      ra[i] = gm < M ? *reinterpret_cast<const uint4*>(A + (size_t)gm * K + kt * BK + ch * 16)
-                     : make_uint4(0, 0, 0, 0);
-      rb[i] = gn < N ? *reinterpret_cast<const uint4*>(B + (size_t)gn * K + kt * BK + ch * 16)
-                     : make_uint4(0, 0, 0, 0);
-    }
-    if (tid < BM) {
-      const int gm = m0 + tid;
-      ras = gm < M ? As[(size_t)gm * KT + kt] : 0.f;
+  for (int u = 0; u < A_PER_WAVE; ++u) {
+    const int r = 8 * (wave + 4 * u) + (lane >> 3);
+    const int c = (lane & 7) ^ (((r >> 1) & 7) ^ ((r & 1) << 2));
+    srcA[u] = A + (size_t)min(m0 + r, M - 1) * K + c * 16;
+  }
+#pragma unroll
+  for (int u = 0; u < B_PER_WAVE; ++u) {
+    const int r = 8 * (wave + 4 * u) + (lane >> 3);
+    const int c = (lane & 7) ^ (((r >> 1) & 7) ^ ((r & 1) << 2));
+    srcB[u] = B + (size_t)min(n0 + r, N - 1) * K + c * 16;
+  }
+  const unsigned lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
+  const float* bs_row = Bs + (size_t)(n0 / 128) * KT;
+
+  auto issue = [&](int kt, int buf) {
+    const unsigned base = lds0 + buf * STAGE;
+#pragma unroll
+    for (int u = 0; u < A_PER_WAVE; ++u) dma16(srcA[u] + kt * BK, base + (wave + 4 * u) * 1024);
+#pragma unroll
+    for (int u = 0; u < B_PER_WAVE; ++u) dma16(srcB[u] + kt * BK, base + A_BYTES + (wave + 4 * u) * 1024);
+  };
+  // scale products a_s[m, kb] * b_s[n0/128, kb] for K blocks kt0 .. +SCK-1,
+  // stored k-major ([SCK][BM+1], conflict-free both ways); ordinary
+  // bounds-checked loads, 16 consecutive K blocks of a row per 16 lanes
+  auto load_scales = [&](int kt0) {
+    const int nk = min(SCK, KT - kt0);
+#pragma unroll
+    for (int v = 0; v < BM * SCK / 256; ++v) {
+      const int idx = tid + 256 * v;
+      const int row = idx / SCK, k = idx % SCK;
+      ssc[k * SCP + row] =
+          k < nk ? As[(size_t)min(m0 + row, M - 1) * KT + kt0 + k] * bs_row[kt0 + k] : 0.f;
     }
   };
-  auto sstore = [&](int buf) {
+
+  // operand read offsets (loop invariant)
+  int offA[4][2], offB[4][2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + 256 * i;
-      const int row = c >> 3, ch = c & 7;
-      *reinterpret_cast<uint4*>(&sA[buf][swz(row, ch)]) = ra[i];
-      *reinterpret_cast<uint4*>(&sB[buf][swz(row, ch)]) = rb[i];
-    }
-    if (tid < BM) sAs[buf][tid] = ras;
-  };
+  for (int i = 0; i < 4; ++i) {
+    offA[i][0] = swz(wm * 64 + i * 16 + r16, 2 * g);
+    offA[i][1] = swz(wm * 64 + i * 16 + r16, 2 * g + 1);
+    offB[i][0] = A_BYTES + swz(wn * 64 + i * 16 + r16, 2 * g);
+    offB[i][1] = A_BYTES + swz(wn * 64 + i * 16 + r16, 2 * g + 1);
+  }
+  // C = A B^T is formed as (B A^T)^T: the MFMA's first operand is the B
+  // fragment, so lane l holds output row 16i + (l % 16), columns
+  // 16j + 4(l / 16) .. +3 -- one activation scale per lane per m-tile, and
+  // 8 contiguous bytes of C per lane in the epilogue
+  const float* scrow = ssc + wm * 64 + r16;
 
   v4f acc[4][4];
 #pragma unroll
@@ -90,61 +188,85 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_128x128(
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  const int r16 = lane & 15, g = lane >> 4;
-  const float* bs_row = Bs + (size_t)(n0 / 128) * KT;
+  load_scales(0);
+#pragma unroll
+  for (int s = 0; s < NST - 1; ++s)
+    if (s < KT) issue(s, s);
 
-  gload(0);
-  sstore(0);
-  __syncthreads();
   for (int kt = 0; kt < KT; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < KT) gload(kt + 1);
-    const float bsv = bs_row[kt];
-
-    v8i fa[4], fb[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = wm * 64 + i * 16 + r16;
-      const uint4 lo = *reinterpret_cast<const uint4*>(&sA[buf][swz(row, 2 * g)]);
-      const uint4 hi = *reinterpret_cast<const uint4*>(&sA[buf][swz(row, 2 * g + 1)]);
-      fa[i] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    if (kt > 0 && kt % SCK == 0) {
+      // next scale chunk: every wave must be done with the old one
+      __syncthreads();
+      load_scales(kt);
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = wn * 64 + j * 16 + r16;
-      const uint4 lo = *reinterpret_cast<const uint4*>(&sB[buf][swz(row, 2 * g)]);
-      const uint4 hi = *reinterpret_cast<const uint4*>(&sB[buf][swz(row, 2 * g + 1)]);
-      fb[j] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    {
+      // stages issued after kt that may stay in flight
+      const int pending = min(NST - 2, KT - 1 - kt);
+      if (pending >= 2) wait_vm<2 * LOADS>();
+      else if (pending == 1) wait_vm<LOADS>();
+      else wait_vm<0>();
     }
-    float sc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float4 a4 = *reinterpret_cast<const float4*>(&sAs[buf][wm * 64 + i * 16 + g * 4]);
-      sc[i][0] = a4.x * bsv; sc[i][1] = a4.y * bsv; sc[i][2] = a4.z * bsv; sc[i][3] = a4.w * bsv;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const v4f t = mfma_fp8(fa[i], fb[j]);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[i][j][r] = fmaf(t[r], sc[i][r], acc[i][j][r]);
-      }
-    if (kt + 1 < KT) sstore(buf ^ 1);
     __syncthreads();
+    if (kt + NST - 1 < KT) issue(kt + NST - 1, (kt + NST - 1) % NST);
+
+    const uint8_t* st = smem + (kt % NST) * STAGE;
+    const int kc = kt % SCK;
+    v8i fa[4], fb[4];
+    float sc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      fa[i] = frag(st, offA[i][0], offA[i][1]);
+      fb[i] = frag(st, offB[i][0], offB[i][1]);
+      sc[i] = scrow[kc * SCP + i * 16];
+    }
+    // software pipeline over tile rows: the 4 MFMAs of row i are issued
+    // before the FMAs that fold row i-1, so the matrix core always has
+    // independent work queued while the wave scales the previous results
+    v4f tp[4], tc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) tp[j] = mfma_fp8(fb[j], fa[0]);
+#pragma unroll
+    for (int i = 1; i <= 4; ++i) {
+      if (i < 4) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) tc[j] = mfma_fp8(fb[j], fa[i]);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i - 1][j][r] = fmaf(tp[j][r], sc[i - 1], acc[i - 1][j][r]);
+      if (i < 4) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) tp[j] = tc[j];
+      }
+    }
   }
 
+  // ---- epilogue: bias, bf16 (RNE), 8-byte stores of 4 consecutive columns
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int col = n0 + wn * 64 + j * 16 + r16;
-    const float bv = (bias != nullptr && col < N) ? bias[col] : 0.f;
+    const int col = n0 + wn * 64 + j * 16 + 4 * g;
+    float bv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (bias != nullptr) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+      for (int r = 0; r < 4; ++r) bv[r] = col + r < N ? bias[col + r] : 0.f;
+    }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = m0 + wm * 64 + i * 16 + g * 4 + r;
-        if (row < M && col < N) C[(size_t)row * N + col] = (uint16_t)f32_to_bf16(acc[i][j][r] + bv);
+    for (int i = 0; i < 4; ++i) {
+      const int row = m0 + wm * 64 + i * 16 + r16;
+      if (row >= M) continue;
+      uint16_t* dst = C + (size_t)row * N + col;
+      if (col + 3 < N && (N & 3) == 0) {
+        uint2 o;
+        o.x = pack_bf16x2(acc[i][j][0] + bv[0], acc[i][j][1] + bv[1]);
+        o.y = pack_bf16x2(acc[i][j][2] + bv[2], acc[i][j][3] + bv[3]);
+        *reinterpret_cast<uint2*>(dst) = o;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (col + r < N) dst[r] = (uint16_t)f32_to_bf16(acc[i][j][r] + bv[r]);
       }
+    }
   }
 }
 
@@ -164,9 +286,10 @@ extern "C" int lfs_fp8_gemm(const void* a, const float* a_s, const void* b, cons
   LFS_REQUIRE(a && a_s && b && b_s && c, "fp8_gemm: null pointer");
   LFS_REQUIRE(K > 0, "fp8_gemm: K must be positive");
   LFS_REQUIRE((((uintptr_t)a | (uintptr_t)b) & 15u) == 0, "fp8_gemm: a and b must be 16-byte aligned");
-  const dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
-  LFS_REQUIRE(grid.y < 65536u, "fp8_gemm: M too large");
-  hipLaunchKernelGGL(fp8_gemm_128x128, grid, dim3(256), 0, (hipStream_t)stream, (const uint8_t*)a,
-                     a_s, (const uint8_t*)b, b_s, bias, (uint16_t*)c, (int)M, (int)N, (int)K);
+  const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  LFS_REQUIRE(tiles_m * tiles_n < (1ll << 31), "fp8_gemm: too many tiles");
+  hipLaunchKernelGGL(fp8_gemm_128x128<2>, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint8_t*)a, a_s, (const uint8_t*)b, b_s, bias,
+                     (uint16_t*)c, (int)M, (int)N, (int)K, (int)tiles_m, (int)tiles_n);
   return check_launch("fp8_gemm");
 }
