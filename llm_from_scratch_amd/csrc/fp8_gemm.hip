@@ -67,6 +67,13 @@ __device__ __forceinline__ void dma4(const void* g, unsigned lds) {
   asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dword %2, off\n\ts_mov_b32 m0, %0"
                : "=&s"(tmp) : "s"(lds), "v"(g) : "memory");
 }
+// LDS writes of this wave visible to its other lanes (no workgroup barrier)
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // s_waitcnt vmcnt(N), other counters unconstrained
 template <int N>
 __device__ __forceinline__ void wait_vm() {
@@ -242,30 +249,47 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_128x128(
     }
   }
 
-  // ---- epilogue: bias, bf16 (RNE), 8-byte stores of 4 consecutive columns
+  // ---- epilogue: bias, bf16 (RNE), then each wave's 64x64 tile goes
+  // through LDS (the idle stage buffers) so that global stores are whole
+  // 128-byte rows: 16-byte chunk c of row r sits at chunk slot c ^ (r & 7)
+  __syncthreads();  // every wave is done with the stage buffers
+  uint8_t* ot = smem + wave * 8192;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int col = n0 + wn * 64 + j * 16 + 4 * g;
+    const int cl = j * 16 + 4 * g;  // first of this lane's 4 columns in the wave tile
     float bv[4] = {0.f, 0.f, 0.f, 0.f};
     if (bias != nullptr) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) bv[r] = col + r < N ? bias[col + r] : 0.f;
+      for (int r = 0; r < 4; ++r) {
+        const int col = n0 + wn * 64 + cl + r;
+        bv[r] = col < N ? bias[col] : 0.f;
+      }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int row = m0 + wm * 64 + i * 16 + r16;
-      if (row >= M) continue;
-      uint16_t* dst = C + (size_t)row * N + col;
-      if (col + 3 < N && (N & 3) == 0) {
-        uint2 o;
-        o.x = pack_bf16x2(acc[i][j][0] + bv[0], acc[i][j][1] + bv[1]);
-        o.y = pack_bf16x2(acc[i][j][2] + bv[2], acc[i][j][3] + bv[3]);
-        *reinterpret_cast<uint2*>(dst) = o;
-      } else {
+      const int rl = i * 16 + r16;
+      uint2 o;
+      o.x = pack_bf16x2(acc[i][j][0] + bv[0], acc[i][j][1] + bv[1]);
+      o.y = pack_bf16x2(acc[i][j][2] + bv[2], acc[i][j][3] + bv[3]);
+      *reinterpret_cast<uint2*>(ot + rl * 128 + (((cl >> 3) ^ (rl & 7)) << 4) + (cl & 7) * 2) = o;
+    }
+  }
+  wave_lds_fence();
+  const int colw = n0 + wn * 64;
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (col + r < N) dst[r] = (uint16_t)f32_to_bf16(acc[i][j][r] + bv[r]);
-      }
+  for (int u = 0; u < 8; ++u) {
+    const int rl = u * 8 + (lane >> 3), c = lane & 7;
+    const int row = m0 + wm * 64 + rl;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(ot + rl * 128 + ((c ^ (rl & 7)) << 4));
+    if (row >= M) continue;
+    uint16_t* dst = C + (size_t)row * N + colw + c * 8;
+    if (colw + c * 8 + 7 < N && (N & 7) == 0) {
+      *reinterpret_cast<u32x4*>(dst) = v;
+    } else {
+      const uint16_t* h = reinterpret_cast<const uint16_t*>(&v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (colw + c * 8 + e < N) dst[e] = h[e];
     }
   }
 }
