@@ -8,8 +8,8 @@
 // (4 FMAs per tile per K block).  The scales are arbitrary fp32 values, so the
 // hardware's power-of-two (E8M0) operand scaling cannot carry them.
 //
-// Workgroup tile 128x128 (one weight-scale block wide), four waves in a 2x2
-// grid, 64x64 per wave (4x4 MFMA tiles).  A and B K-tiles (16 KB each) are
+// Workgroup tile BM x 128 (one weight-scale block wide), 64x64 per wave
+// (4x4 MFMA tiles).  A and B K-tiles (16 KB each) are
 // copied global -> LDS by DMA (no register staging) into a ring of NST
 // stages; the activation scales follow in chunks of whole rows.
 //
@@ -32,7 +32,7 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int BM = 128, BN = 128, BK = 128;
+constexpr int BN = 128, BK = 128;
 constexpr int GROUP_M = 8;
 
 __device__ __forceinline__ v8i frag(const uint8_t* tile, int off_lo, int off_hi) {
@@ -74,6 +74,9 @@ __device__ __forceinline__ void wave_lds_fence() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// s_waitcnt lgkmcnt(0) (LDS reads of this wave complete), vmcnt unconstrained
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
 // s_waitcnt vmcnt(N), other counters unconstrained
 template <int N>
 __device__ __forceinline__ void wait_vm() {
@@ -93,26 +96,31 @@ __device__ __forceinline__ int swz(int r, int c) {
   return r * BK + ((c ^ (((r >> 1) & 7) ^ ((r & 1) << 2))) << 4);
 }
 
-constexpr int SCK = 16;        // K blocks of scale products held in LDS at a time
-constexpr int SCP = BM + 1;     // padded row of the k-major scale table
-
-// NST-stage pipeline: K blocks kt+1 .. kt+NST-2 are in flight while block kt
-// is multiplied; the buffer refilled at iteration kt is the one consumed at
-// kt-1, which every wave has left once it passes the iteration's barrier.
-// With NST = 2 a workgroup uses 80 KB of LDS and two share a CU, so one
-// workgroup's barrier and LDS waits are covered by the other's MFMAs.
-// Activation scales are staged per chunk of SCK K blocks ([128][SCK] floats,
-// ordinary loads) instead of one strided 4-byte gather per K block.
-template <int NST>
-__global__ __launch_bounds__(256, 2) void fp8_gemm_128x128(
+// Tile BM x 128 (BM = 128: 4 waves, BM = 256: 8 waves), 64x64 per wave,
+// waves (wave >> 1, wave & 1) over the tile; 2 waves per SIMD either way.
+// NST LDS stages, NST K blocks in flight during the MFMAs (see the
+// read-then-refill loop below).
+//   BM = 128, NST = 2: 72 KB of LDS, two workgroups per CU, so one
+//     workgroup's barriers and LDS waits are covered by the other's MFMAs;
+//   BM = 256, NST = 3: 152 KB, one workgroup per CU, every B tile shared by
+//     four waves (not dispatched: slower on every benchmark shape).
+// Scale products a_s * b_s are staged per chunk of SCK K blocks in a
+// k-major table ([SCK][BM+1] floats) instead of one strided 4-byte gather
+// per K block.
+template <int BM, int NST, int SCK>
+__global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ B,
     const float* __restrict__ Bs, const float* __restrict__ bias, uint16_t* __restrict__ C, int M,
     int N, int K, int tiles_m, int tiles_n) {
+  constexpr int NW = BM / 32;  // waves
+  constexpr int NT = 64 * NW;  // threads
+  constexpr int SCP = BM + 1;  // padded row of the k-major scale table
   constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK;
   constexpr int STAGE = A_BYTES + B_BYTES;
-  constexpr int A_PER_WAVE = A_BYTES / 1024 / 4;  // 1 KB (8-row) segments per wave
-  constexpr int B_PER_WAVE = B_BYTES / 1024 / 4;
+  constexpr int A_PER_WAVE = A_BYTES / 1024 / NW;  // 1 KB (8-row) segments per wave
+  constexpr int B_PER_WAVE = B_BYTES / 1024 / NW;
   constexpr int LOADS = A_PER_WAVE + B_PER_WAVE;  // DMA instructions per wave per stage
+  static_assert(NW * 8192 <= NST * STAGE, "epilogue staging must fit the stage buffers");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * STAGE];
   __shared__ __attribute__((aligned(16))) float ssc[SCK * SCP];
 
@@ -134,19 +142,19 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_128x128(
   const int KT = K / BK;
   const int r16 = lane & 15, g = lane >> 4;
 
-  // ---- DMA sources: segment q = wave + 4u covers tile rows 8q .. 8q+7
+  // ---- DMA sources: segment q = wave + NW*u covers tile rows 8q .. 8q+7
   // (rows past M / N are clamped; their results are never stored)
   const uint8_t* srcA[A_PER_WAVE];
   const uint8_t* srcB[B_PER_WAVE];
 #pragma unroll
   for (int u = 0; u < A_PER_WAVE; ++u) {
-    const int r = 8 * (wave + 4 * u) + (lane >> 3);
+    const int r = 8 * (wave + NW * u) + (lane >> 3);
     const int c = (lane & 7) ^ (((r >> 1) & 7) ^ ((r & 1) << 2));
     srcA[u] = A + (size_t)min(m0 + r, M - 1) * K + c * 16;
   }
 #pragma unroll
   for (int u = 0; u < B_PER_WAVE; ++u) {
-    const int r = 8 * (wave + 4 * u) + (lane >> 3);
+    const int r = 8 * (wave + NW * u) + (lane >> 3);
     const int c = (lane & 7) ^ (((r >> 1) & 7) ^ ((r & 1) << 2));
     srcB[u] = B + (size_t)min(n0 + r, N - 1) * K + c * 16;
   }
@@ -156,9 +164,9 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_128x128(
   auto issue = [&](int kt, int buf) {
     const unsigned base = lds0 + buf * STAGE;
 #pragma unroll
-    for (int u = 0; u < A_PER_WAVE; ++u) dma16(srcA[u] + kt * BK, base + (wave + 4 * u) * 1024);
+    for (int u = 0; u < A_PER_WAVE; ++u) dma16(srcA[u] + kt * BK, base + (wave + NW * u) * 1024);
 #pragma unroll
-    for (int u = 0; u < B_PER_WAVE; ++u) dma16(srcB[u] + kt * BK, base + A_BYTES + (wave + 4 * u) * 1024);
+    for (int u = 0; u < B_PER_WAVE; ++u) dma16(srcB[u] + kt * BK, base + A_BYTES + (wave + NW * u) * 1024);
   };
   // scale products a_s[m, kb] * b_s[n0/128, kb] for K blocks kt0 .. +SCK-1,
   // stored k-major ([SCK][BM+1], conflict-free both ways); ordinary
@@ -166,8 +174,8 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_128x128(
   auto load_scales = [&](int kt0) {
     const int nk = min(SCK, KT - kt0);
 #pragma unroll
-    for (int v = 0; v < BM * SCK / 256; ++v) {
-      const int idx = tid + 256 * v;
+    for (int v = 0; v < BM * SCK / NT; ++v) {
+      const int idx = tid + NT * v;
       const int row = idx / SCK, k = idx % SCK;
       ssc[k * SCP + row] =
           k < nk ? As[(size_t)min(m0 + row, M - 1) * KT + kt0 + k] * bs_row[kt0 + k] : 0.f;
@@ -195,27 +203,25 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_128x128(
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
+  // Read-then-refill ring: an iteration copies its whole stage into
+  // registers (fragments + scales), passes a second barrier, and only then
+  // refills that same buffer with K block kt + NST, so NST blocks are in
+  // flight while the MFMAs run (the LDS holds only NST stages).
   load_scales(0);
 #pragma unroll
-  for (int s = 0; s < NST - 1; ++s)
+  for (int s = 0; s < NST; ++s)
     if (s < KT) issue(s, s);
 
   for (int kt = 0; kt < KT; ++kt) {
-    if (kt > 0 && kt % SCK == 0) {
-      // next scale chunk: every wave must be done with the old one
-      __syncthreads();
-      load_scales(kt);
-    }
+    if (kt > 0 && kt % SCK == 0) load_scales(kt);  // old chunk last read before the previous B2
     {
-      // stages issued after kt that may stay in flight
-      const int pending = min(NST - 2, KT - 1 - kt);
-      if (pending >= 2) wait_vm<2 * LOADS>();
-      else if (pending == 1) wait_vm<LOADS>();
+      // K blocks issued after kt that may stay in flight
+      const int pending = min(NST - 1, KT - 1 - kt);
+      if (NST > 2 && pending >= 2) wait_vm<2 * LOADS>();
+      else if (pending >= 1) wait_vm<LOADS>();
       else wait_vm<0>();
     }
-    __syncthreads();
-    if (kt + NST - 1 < KT) issue(kt + NST - 1, (kt + NST - 1) % NST);
-
+    __syncthreads();  // B1: block kt (and the scale chunk) visible to every wave
     const uint8_t* st = smem + (kt % NST) * STAGE;
     const int kc = kt % SCK;
     v8i fa[4], fb[4];
@@ -226,26 +232,22 @@ __global__ __launch_bounds__(256, 2) void fp8_gemm_128x128(
       fb[i] = frag(st, offB[i][0], offB[i][1]);
       sc[i] = scrow[kc * SCP + i * 16];
     }
-    // software pipeline over tile rows: the 4 MFMAs of row i are issued
-    // before the FMAs that fold row i-1, so the matrix core always has
-    // independent work queued while the wave scales the previous results
-    v4f tp[4], tc[4];
+    wait_lgkm0();     // this wave's reads of the buffer have completed
+    __syncthreads();  // B2: every wave is done with buffer kt % NST
+    if (kt + NST < KT) issue(kt + NST, kt % NST);
+    // MFMA k is issued, then the FMAs fold the product of MFMA k-2, which
+    // has retired by then; scheduling fences keep the compiler from pulling
+    // a fold up behind its own MFMA (which would idle the matrix core)
+    v4f t[16];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) tp[j] = mfma_fp8(fb[j], fa[0]);
+    for (int k = 0; k < 18; ++k) {
+      if (k < 16) t[k] = mfma_fp8(fb[k & 3], fa[k >> 2]);
+      if (k >= 2) {
+        const int p = k - 2;
 #pragma unroll
-    for (int i = 1; i <= 4; ++i) {
-      if (i < 4) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) tc[j] = mfma_fp8(fb[j], fa[i]);
+        for (int r = 0; r < 4; ++r) acc[p >> 2][p & 3][r] = fmaf(t[p][r], sc[p >> 2], acc[p >> 2][p & 3][r]);
       }
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[i - 1][j][r] = fmaf(tp[j][r], sc[i - 1], acc[i - 1][j][r]);
-      if (i < 4) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) tp[j] = tc[j];
-      }
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
@@ -310,10 +312,15 @@ extern "C" int lfs_fp8_gemm(const void* a, const float* a_s, const void* b, cons
   LFS_REQUIRE(a && a_s && b && b_s && c, "fp8_gemm: null pointer");
   LFS_REQUIRE(K > 0, "fp8_gemm: K must be positive");
   LFS_REQUIRE((((uintptr_t)a | (uintptr_t)b) & 15u) == 0, "fp8_gemm: a and b must be 16-byte aligned");
-  const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-  LFS_REQUIRE(tiles_m * tiles_n < (1ll << 31), "fp8_gemm: too many tiles");
-  hipLaunchKernelGGL(fp8_gemm_128x128<2>, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0,
-                     (hipStream_t)stream, (const uint8_t*)a, a_s, (const uint8_t*)b, b_s, bias,
-                     (uint16_t*)c, (int)M, (int)N, (int)K, (int)tiles_m, (int)tiles_n);
+  LFS_REQUIRE(((uintptr_t)c & 15u) == 0, "fp8_gemm: c must be 16-byte aligned");
+  const int64_t tiles_n = (N + BN - 1) / BN;
+  const int64_t tiles_m128 = (M + 127) / 128;
+  LFS_REQUIRE(tiles_m128 * tiles_n < (1ll << 31), "fp8_gemm: too many tiles");
+  hipStream_t st = (hipStream_t)stream;
+  // 128x128 tiles, two workgroups per CU.  (256x128 tiles with one
+  // 8-wave workgroup per CU measured 10-15% slower on every benchmark shape.)
+  hipLaunchKernelGGL((fp8_gemm_tile<128, 2, 16>), dim3((unsigned)(tiles_m128 * tiles_n)), dim3(256), 0, st,
+                     (const uint8_t*)a, a_s, (const uint8_t*)b, b_s, bias, (uint16_t*)c, (int)M,
+                     (int)N, (int)K, (int)tiles_m128, (int)tiles_n);
   return check_launch("fp8_gemm");
 }
