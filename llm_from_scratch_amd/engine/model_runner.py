@@ -1,0 +1,216 @@
+"""Single-GPU model runner: KV pool, attention metadata, graph-captured decode.
+
+Counterpart of engine/model_runner.py of the reference with the same method
+names and data contract (one MI355X, so no process group or shared-memory
+RPC):
+  allocate_kv_cache   one pool [2, L, NB, BS, Hkv, D]; per-layer k_cache /
+                      v_cache views attached to modules that have them
+                      (:162-190)
+  prepare_prefill     input ids / positions of uncached tokens, cu_seqlens,
+                      slot_mapping over uncached blocks, block tables when a
+                      prefix is cached (:202-249)
+  prepare_decode      last token, position L-1, slot of the newest token,
+                      context_lens (int64), block tables padded with -1
+                      (:253-278)
+  run_model           eager prefill; decode replays the smallest captured
+                      graph whose batch fits, with padding rows given slot -1
+                      and context length 0 (:288-312)
+  capture_cudagraph   graphs for bs in [1,2,4,8] + range(16, max_bs+1, 16)
+                      over static buffers (:339-392)
+The decode slot is bt[-1]*BS + last_block_num_tokens - 1 with the corrected
+last_block_num_tokens (a full last block counts BS tokens).
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from ..context import get_context, reset_context, set_context
+from .sequence import Sequence
+
+
+def prefill_metadata(seqs: list[Sequence], block_size: int) -> dict:
+    """Host lists for a prefill batch (engine/model_runner.py:202-249): ids and
+    positions of the tokens not covered by cached blocks, cu_seqlens over
+    query (uncached) and key (full) lengths, and the slots of every token in
+    the uncached blocks (a full last block contributes block_size slots)."""
+    input_ids, positions, slots = [], [], []
+    cu_q, cu_k = [0], [0]
+    max_q = max_k = 0
+    BS = block_size
+    for seq in seqs:
+        start = seq.num_cached_tokens
+        input_ids.extend(seq.token_ids[start:])
+        positions.extend(range(start, seq.num_tokens))
+        lq, lk = seq.num_tokens - start, seq.num_tokens
+        cu_q.append(cu_q[-1] + lq)
+        cu_k.append(cu_k[-1] + lk)
+        max_q, max_k = max(max_q, lq), max(max_k, lk)
+        for i in range(seq.num_cached_blocks, seq.num_blocks):
+            n = BS if i != seq.num_blocks - 1 else seq.last_block_num_tokens
+            slots.extend(range(seq.block_table[i] * BS, seq.block_table[i] * BS + n))
+    return dict(input_ids=input_ids, positions=positions, cu_seqlens_q=cu_q, cu_seqlens_k=cu_k,
+                max_seqlen_q=max_q, max_seqlen_k=max_k, slot_mapping=slots)
+
+
+def decode_metadata(seqs: list[Sequence], block_size: int) -> dict:
+    """Host lists for a decode batch (engine/model_runner.py:253-278): the
+    newest token of each sequence at position L-1, its slot
+    block_table[-1]*BS + last_block_num_tokens - 1, and L as context length."""
+    return dict(input_ids=[s.last_token for s in seqs],
+                positions=[len(s) - 1 for s in seqs],
+                context_lens=[len(s) for s in seqs],
+                slot_mapping=[s.block_table[-1] * block_size + s.last_block_num_tokens - 1 for s in seqs])
+
+
+class Sampler:
+    """Temperature + Gumbel-max sampling (utils/sampler.py:35-53): argmax of
+    softmax(logits / T) / Exp(1) noise."""
+
+    def __call__(self, logits: torch.Tensor, temperatures: torch.Tensor,
+                 generator: Optional[torch.Generator] = None) -> torch.Tensor:
+        logits = logits.float().div_(temperatures.unsqueeze(1))
+        probs = torch.softmax(logits, dim=-1)
+        noise = torch.empty_like(probs).exponential_(1, generator=generator).clamp_min_(1e-10)
+        return probs.div_(noise).argmax(dim=-1)
+
+
+class ModelRunner:
+    def __init__(self, model: torch.nn.Module, config: dict, device="cuda"):
+        self.model = model
+        self.config = config
+        self.device = torch.device(device)
+        self.block_size = config.get("block_size", 256)
+        self.enforce_eager = config.get("enforce_eager", False)
+        self.sampler = Sampler()
+        self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        self.graph_vars: dict[str, torch.Tensor] = {}
+        self.allocate_kv_cache()
+        if not self.enforce_eager:
+            self.capture_cudagraph()
+
+    # ------------------------------------------------------------ KV pool --
+    def allocate_kv_cache(self) -> None:
+        cfg = self.config
+        num_layers = cfg["num_layers"]
+        num_kv_heads = cfg["num_kv_heads"]
+        head_dim = cfg.get("head_dim", cfg["hidden_size"] // cfg["num_heads"])
+        dtype = cfg.get("kv_dtype", torch.bfloat16)
+        block_bytes = self.block_size * 2 * num_layers * num_kv_heads * head_dim * dtype.itemsize
+        if "num_kv_blocks" in cfg:
+            nb = int(cfg["num_kv_blocks"])
+        else:
+            free, _ = torch.cuda.mem_get_info(self.device)
+            nb = int(free * cfg.get("gpu_memory_utilization", 0.9) // block_bytes)
+        assert nb >= 1, "Not enough memory to hold at least one block of KV cache"
+        self.num_available_kv_blocks = nb
+        self.kv_cache = torch.empty(2, num_layers, nb, self.block_size, num_kv_heads, head_dim,
+                                    device=self.device, dtype=dtype)
+        layer = 0
+        for module in self.model.modules():
+            if hasattr(module, "k_cache") and hasattr(module, "v_cache"):
+                module.k_cache = self.kv_cache[0, layer]
+                module.v_cache = self.kv_cache[1, layer]
+                layer += 1
+        assert layer == num_layers, f"found {layer} attention layers, expected {num_layers}"
+
+    # ----------------------------------------------------------- metadata --
+    def _pad_tables(self, seqs: list[Sequence]) -> torch.Tensor:
+        width = max(len(s.block_table) for s in seqs)
+        rows = [s.block_table + [-1] * (width - len(s.block_table)) for s in seqs]
+        return torch.tensor(rows, dtype=torch.int32, pin_memory=True).to(self.device, non_blocking=True)
+
+    def prepare_prefill(self, seqs: list[Sequence]):
+        m = prefill_metadata(seqs, self.block_size)
+        pin = dict(pin_memory=True)
+
+        def dev(x, dtype):
+            return torch.tensor(x, dtype=dtype, **pin).to(self.device, non_blocking=True)
+
+        block_tables = self._pad_tables(seqs) if m["cu_seqlens_q"][-1] < m["cu_seqlens_k"][-1] else None
+        set_context(True, dev(m["cu_seqlens_q"], torch.int32), dev(m["cu_seqlens_k"], torch.int32),
+                    m["max_seqlen_q"], m["max_seqlen_k"], dev(m["slot_mapping"], torch.int64),
+                    None, block_tables)
+        return dev(m["input_ids"], torch.int64), dev(m["positions"], torch.int64)
+
+    def prepare_decode(self, seqs: list[Sequence]):
+        m = decode_metadata(seqs, self.block_size)
+        pin = dict(pin_memory=True)
+
+        def dev(x, dtype):
+            return torch.tensor(x, dtype=dtype, **pin).to(self.device, non_blocking=True)
+
+        set_context(False, None, None, 0, 0, dev(m["slot_mapping"], torch.int64),
+                    dev(m["context_lens"], torch.int64), self._pad_tables(seqs))
+        return dev(m["input_ids"], torch.int64), dev(m["positions"], torch.int64)
+
+    def prepare_sample(self, seqs: list[Sequence]) -> torch.Tensor:
+        return torch.tensor([s.temperature for s in seqs], dtype=torch.float32,
+                            pin_memory=True).to(self.device, non_blocking=True)
+
+    # --------------------------------------------------------------- run ---
+    @torch.inference_mode()
+    def run_model(self, input_ids: torch.Tensor, positions: torch.Tensor, is_prefill: bool) -> torch.Tensor:
+        bs = input_ids.size(0)
+        if is_prefill or self.enforce_eager or bs > self.max_graph_bs():
+            return self.model.compute_logits(self.model(input_ids, positions))
+        ctx = get_context()
+        graph_bs = next(b for b in sorted(self.graphs) if b >= bs)
+        v = self.graph_vars
+        v["input_ids"][:bs] = input_ids
+        v["positions"][:bs] = positions
+        v["slot_mapping"].fill_(-1)
+        v["slot_mapping"][:bs] = ctx.slot_mapping
+        v["context_lens"].zero_()
+        v["context_lens"][:bs] = ctx.context_lens
+        v["block_tables"].fill_(-1)
+        v["block_tables"][:bs, :ctx.block_tables.size(1)] = ctx.block_tables
+        self.graphs[graph_bs].replay()
+        return self.model.compute_logits(v["outputs"][:bs])
+
+    def run(self, seqs: list[Sequence], is_prefill: bool,
+            generator: Optional[torch.Generator] = None) -> list[int]:
+        input_ids, positions = self.prepare_prefill(seqs) if is_prefill else self.prepare_decode(seqs)
+        logits = self.run_model(input_ids, positions, is_prefill)
+        if is_prefill:
+            # one logit row per sequence: the last prompt token
+            last = get_context().cu_seqlens_q[1:] - 1
+            logits = logits[last]
+        token_ids = self.sampler(logits, self.prepare_sample(seqs), generator).tolist()
+        reset_context()
+        return token_ids
+
+    # ------------------------------------------------------ graph capture --
+    def max_graph_bs(self) -> int:
+        return max(self.graphs) if self.graphs else 0
+
+    @torch.inference_mode()
+    def capture_cudagraph(self) -> None:
+        cfg = self.config
+        max_bs = min(cfg.get("max_num_seqs", 128), 512)
+        max_blocks = math.ceil(cfg.get("max_model_length", 4096) / self.block_size)
+        dev = self.device
+        input_ids = torch.zeros(max_bs, dtype=torch.int64, device=dev)
+        positions = torch.zeros(max_bs, dtype=torch.int64, device=dev)
+        slot_mapping = torch.full((max_bs,), -1, dtype=torch.int64, device=dev)
+        context_lens = torch.zeros(max_bs, dtype=torch.int64, device=dev)
+        block_tables = torch.full((max_bs, max_blocks), -1, dtype=torch.int32, device=dev)
+        outputs = torch.zeros(max_bs, cfg["hidden_size"], dtype=torch.bfloat16, device=dev)
+        sizes = [b for b in [1, 2, 4, 8] + list(range(16, max_bs + 1, 16)) if b <= max_bs]
+        pool = None
+        for bs in reversed(sizes):
+            graph = torch.cuda.CUDAGraph()
+            set_context(False, slot_mapping=slot_mapping[:bs], context_lens=context_lens[:bs],
+                        block_tables=block_tables[:bs])
+            outputs[:bs] = self.model(input_ids[:bs], positions[:bs])  # warm up outside capture
+            with torch.cuda.graph(graph, pool):
+                outputs[:bs] = self.model(input_ids[:bs], positions[:bs])
+            if pool is None:
+                pool = graph.pool()
+            self.graphs[bs] = graph
+            torch.cuda.synchronize()
+            reset_context()
+        self.graph_vars = dict(input_ids=input_ids, positions=positions, slot_mapping=slot_mapping,
+                               context_lens=context_lens, block_tables=block_tables, outputs=outputs)

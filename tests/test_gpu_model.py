@@ -1,0 +1,407 @@
+"""FP8Linear, the paged GQA + MoE decode model and the graph-captured decode
+step, on the GPU.
+
+Decode-step logits are compared with a full causal forward over the same
+tokens written here from the reference's layer math (model/transformer.py:
+162-183, model/attention/GQA.py:65-139, model/utils.py:44-67,
+model/architecture/moe.py:45-90, 288-341) in fp32, with the FP8 linears
+emulated as dequant(act_quant(x)) @ dequant(W)^T + b.
+
+Two tolerances, both relative L2 error per row:
+  * TOL_LAYER = 1e-2 for each op of each layer (FP8 linears, norms, K/V
+    writes, paged attention, SwiGLU, MoE combine) fed the GPU's own input to
+    that op and the GPU-written KV cache (teacher forcing): the single-op
+    bar;
+  * e2e_tol(layers) = 4e-2 * sqrt(layers) for logits after the whole
+    stack, a drift bound rather than a parity bar.  Two valid FP8
+    computations drift apart layer by layer: a bf16 rounding difference in
+    one linear's output flips the e4m3 code of some activations in the next
+    (one e4m3 step is 2^-3 relative), so a 1e-3 difference entering a MoE
+    leaves it as ~1e-2.  Measured on MI355X: 3.5e-2 after 2 layers, 8.2e-2
+    after 12; every single op stays within 2e-3.
+Planted mistakes, checked on the CPU with the kernels emulated, each fail a
+per-op check by 7e-2 or more: interleaved instead of half-split RoPE, head
+map h % Hkv instead of h // G, a dropped linear bias, the newest token left
+out of attention, a dropped residual add, a softmax gate instead of sigmoid,
+top-k weights not renormalised.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from llm_from_scratch_amd.context import reset_context
+from llm_from_scratch_amd.decode_model import DecodeModel, DecodeModelConfig
+from llm_from_scratch_amd.engine import BlockManager, LLMEngine, ModelRunner, SamplingParams, Sequence
+from llm_from_scratch_amd.fp8_linear import FP8Linear
+from llm_from_scratch_amd import workloads
+from oracle import fp8 as ofp8
+
+pytestmark = pytest.mark.gpu
+
+FP32_EPS = torch.finfo(torch.float32).eps
+INV448 = torch.tensor(1.0 / 448.0, dtype=torch.float32)
+
+
+# ---------------------------------------------------------------- helpers --
+def q_act(x: torch.Tensor) -> torch.Tensor:
+    """fp32 value of act_quant's e4m3 codes times their 1x128 scales."""
+    T, K = x.shape
+    xf = x.float().view(T, K // 128, 128)
+    s = xf.abs().amax(-1, keepdim=True).clamp_min(1e-4) * INV448.to(x.device)
+    q = torch.clamp(xf / s, -448, 448).to(torch.float8_e4m3fn).float()
+    return (q * s).view(T, K)
+
+
+def w_deq(m: FP8Linear) -> torch.Tensor:
+    s = m.weight_scale.repeat_interleave(128, 0)[:m.out_features].repeat_interleave(128, 1)
+    return m.weight.float() * s
+
+
+def lin(m: FP8Linear, x: torch.Tensor) -> torch.Tensor:
+    y = q_act(x.to(torch.bfloat16)) @ w_deq(m).t()
+    if m.bias is not None:
+        y = y + m.bias
+    return y.to(torch.bfloat16)
+
+
+def rms(x, w, eps, residual=None):
+    xf = x.float() if residual is None else x.float() + residual.float()
+    out = (w * xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype)
+    return out, xf.to(x.dtype)
+
+
+def rope(x, pos, theta, D):
+    inv = 1.0 / (theta ** (torch.arange(0, D, 2, device=x.device).float() / D))
+    ang = pos.float()[:, None] * inv[None, :]
+    cos, sin = ang.cos()[:, None, :], ang.sin()[:, None, :]
+    x1, x2 = x.float().chunk(2, -1)
+    return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), -1)
+
+
+def gqa(q, k, v, mask=None):
+    """SDPA with query head h reading kv head h // G (model/attention/GQA.py:
+    118-130), fp32.  q [Tq, Hq, D], k/v [Tk, Hkv, D] -> [Tq, Hq*D]."""
+    Tq, Hq, D = q.shape
+    G = Hq // k.shape[1]
+    kh = k.float().repeat_interleave(G, 1).transpose(0, 1)
+    vh = v.float().repeat_interleave(G, 1).transpose(0, 1)
+    s = torch.matmul(q.float().transpose(0, 1), kh.transpose(1, 2).contiguous()) / math.sqrt(D)
+    if mask is not None:
+        s = s.masked_fill(~mask, float("-inf"))
+    return torch.matmul(torch.softmax(s, -1), vh).transpose(0, 1).reshape(Tq, Hq * D)
+
+
+def ref_qkv(a, h, pos, cfg):
+    T, Hq, Hkv, D = h.shape[0], cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
+    q = rms(lin(a.q_proj, h), a.q_norm.weight, FP32_EPS)[0].view(T, Hq, D)
+    k = rms(lin(a.k_proj, h), a.k_norm.weight, FP32_EPS)[0].view(T, Hkv, D)
+    v = lin(a.v_proj, h).view(T, Hkv, D)
+    q = rope(q, pos, cfg.rope_theta, D).to(torch.bfloat16)
+    k = rope(k, pos, cfg.rope_theta, D).to(torch.bfloat16)
+    return q, k, v
+
+
+def ref_moe(f, h, cfg):
+    T = h.shape[0]
+    logits = h.float() @ f.gate_weight.float().t()
+    scores = torch.sigmoid(logits)
+    idx = torch.topk(logits + f.expert_bias, f.top_k, -1).indices
+    w = torch.gather(scores, -1, idx)
+    w = w / (w.sum(-1, keepdim=True) + 1e-10)
+
+    def mlp(e, z):
+        return lin(e.w2, torch.nn.functional.silu(lin(e.w1, z)) * lin(e.w3, z))
+
+    y = torch.zeros(T, cfg.d_model, device=h.device)
+    outs = [mlp(e, h).float() for e in f.experts]
+    for j in range(f.top_k):
+        for e in range(f.n_experts):
+            sel = idx[:, j] == e
+            y[sel] += w[sel, j:j + 1] * outs[e][sel]
+    y += mlp(f.shared_expert, h).float()
+    return y.to(torch.bfloat16)
+
+
+def ref_block(blk, x, residual, pos, cfg, attend):
+    """One decoder block (model/transformer.py:90-118) with fused add & norm;
+    ``attend(q, k, v)`` supplies the attention over the right context."""
+    if residual is None:
+        h, residual = rms(x, blk.att_norm.weight, cfg.rms_eps)[0], x
+    else:
+        h, residual = rms(x, blk.att_norm.weight, cfg.rms_eps, residual)
+    q, k, v = ref_qkv(blk.att, h, pos, cfg)
+    x = lin(blk.att.output_proj, attend(q, k, v).to(torch.bfloat16))
+    h, residual = rms(x, blk.ffn_norm.weight, cfg.rms_eps, residual)
+    return ref_moe(blk.ffn, h, cfg), residual
+
+
+def ref_logits(model: DecodeModel, tokens: list[int]) -> torch.Tensor:
+    """Full causal forward over one sequence (model/transformer.py:162-183);
+    fp32 logits [T, vocab]."""
+    cfg = model.cfg
+    dev = model.embed.device
+    T = len(tokens)
+    pos = torch.arange(T, device=dev)
+    x = model.embed[torch.tensor(tokens, device=dev)]
+    causal = torch.tril(torch.ones(T, T, dtype=torch.bool, device=dev))
+    residual = None
+    for blk in model.layers:
+        x, residual = ref_block(blk, x, residual, pos, cfg, lambda q, k, v: gqa(q, k, v, causal))
+    h, _ = rms(x, model.final_norm.weight, cfg.rms_eps, residual)
+    return lin(model.lm_head, h).float()
+
+
+def rel_err_rows(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    a, b = a.float(), b.float()
+    return (a - b).norm(dim=-1) / b.norm(dim=-1).clamp_min(1e-6)
+
+
+TOL_LAYER = 1e-2
+
+
+def e2e_tol(num_layers: int) -> float:
+    return 4e-2 * math.sqrt(num_layers)
+SMALL = DecodeModelConfig(vocab_size=1024, d_model=256, num_layers=2, num_heads=4, num_kv_heads=2,
+                          d_ff=256, n_routed_experts=4, num_experts_per_tok=2, max_model_length=512)
+
+
+@pytest.fixture
+def block_size():
+    old = Sequence.block_size
+    yield
+    Sequence.block_size = old
+
+
+# ------------------------------------------------------------- FP8Linear --
+def test_fp8_linear_cfg1_matches_oracle():
+    x = workloads.activation(256, 512, seed=0, device="cuda")
+    w = workloads.weight(1344, 512, seed=0, device="cuda")
+    bias = torch.randn(1344, generator=torch.Generator().manual_seed(5)).cuda()
+    m = FP8Linear(512, 1344, device="cuda").load_weight(w, bias)
+    wq, ws = ofp8.weight_quant(w.float().cpu().numpy(), 128)
+    assert np.array_equal(m.weight.view(torch.uint8).cpu().numpy(), wq)
+    assert np.array_equal(m.weight_scale.cpu().numpy(), ws)
+    y = m(x).float().cpu().numpy()
+    aq, asc = ofp8.act_quant(x.float().cpu().numpy(), 128)
+    want = ofp8.fp8_gemm(aq, asc, wq, ws, bias=bias.cpu().numpy())
+    np.testing.assert_allclose(y, want, rtol=1e-2, atol=2e-2)
+
+
+# ------------------------------------------------------- decode model ----
+def _prefill(runner, seqs):
+    ids, pos = runner.prepare_prefill(seqs)
+    logits = runner.run_model(ids, pos, True)
+    from llm_from_scratch_amd.context import get_context
+    last = (get_context().cu_seqlens_q[1:] - 1).long()
+    reset_context()
+    return logits[last].float()
+
+
+def _gather(cache, table, L):
+    t = torch.arange(L, device=cache.device)
+    blocks = torch.tensor(table, device=cache.device)[t // cache.size(1)]
+    return cache[blocks, t % cache.size(1)]
+
+
+def check_layers_teacher_forced(model, runner, seqs):
+    """Eager decode step with hooks on every block, attention, MoE and FP8
+    linear.  Each op must match the reference on the GPU's own input to that
+    op (teacher forcing), so no error is carried from one op to the next:
+      every FP8 linear vs dequant(act_quant(x)) @ dequant(W)^T + b;
+      att_norm / ffn_norm / final_norm (fused add & norm);
+      the newest token's K/V in the pool vs k_norm/RoPE of the GPU's k_proj
+      output and the GPU's v_proj output;
+      attention (GQA over the K/V that the GPU wrote to the pool) vs the
+      output projection's input;
+      each expert's SwiGLU product vs w2's input;
+      MoE combine (gate, top-k, renormalised weights, shared expert) over
+      the GPU's expert outputs vs the MoE output.
+    Returns the largest error per op kind."""
+    rec: dict[str, tuple] = {}
+
+    def hook(name):
+        def f(mod, args, out):
+            rec[name] = (args, out)
+        return f
+
+    hooks = [m.register_forward_hook(hook(n)) for n, m in model.named_modules()
+             if isinstance(m, FP8Linear) or n.count(".") == 1 and n.startswith("layers.")
+             or n.endswith(".att") or n.endswith(".ffn")]
+    try:
+        _decode(runner, seqs, eager=True)
+    finally:
+        for h in hooks:
+            h.remove()
+    cfg = model.cfg
+    worst: dict[str, float] = {}
+
+    def chk(kind, got, want, what):
+        e = rel_err_rows(got, want).max().item()
+        worst[kind] = max(worst.get(kind, 0.0), e)
+        assert e <= TOL_LAYER, f"{what}: {kind} rel err {e:.4f}"
+
+    for name, m in model.named_modules():
+        if isinstance(m, FP8Linear):
+            (x,), y = rec[name]
+            chk("linear", y, lin(m, x), name)
+    T, Hq, Hkv, D = len(seqs), cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
+    for layer, blk in enumerate(model.layers):
+        p = f"layers.{layer}"
+        (x, residual, pos), (y, res_out) = rec[p]
+        (att_in, _), att_out = rec[p + ".att"]
+        (ffn_in,), ffn_out = rec[p + ".ffn"]
+        if residual is None:
+            h, r = rms(x, blk.att_norm.weight, cfg.rms_eps)[0], x
+        else:
+            h, r = rms(x, blk.att_norm.weight, cfg.rms_eps, residual)
+        chk("norm", att_in, h, f"{p} att_norm")
+        h2, r2 = rms(att_out, blk.ffn_norm.weight, cfg.rms_eps, r)
+        chk("norm", ffn_in, h2, f"{p} ffn_norm")
+        chk("norm", res_out, r2, f"{p} residual")
+        a = blk.att
+        q = rms(rec[p + ".att.q_proj"][1], a.q_norm.weight, FP32_EPS)[0].view(T, Hq, D)
+        k = rms(rec[p + ".att.k_proj"][1], a.k_norm.weight, FP32_EPS)[0].view(T, Hkv, D)
+        v = rec[p + ".att.v_proj"][1].view(T, Hkv, D)
+        q = rope(q, pos, cfg.rope_theta, D).to(torch.bfloat16)
+        k = rope(k, pos, cfg.rope_theta, D).to(torch.bfloat16)
+        o = rec[p + ".att.output_proj"][0][0]
+        for i, s in enumerate(seqs):
+            L = len(s)
+            Kc = _gather(a.k_cache, s.block_table, L)
+            Vc = _gather(a.v_cache, s.block_table, L)
+            what = f"{p} seq {i} len {L}"
+            chk("new_k", Kc[-1].reshape(1, -1), k[i].reshape(1, -1), what)
+            chk("new_v", Vc[-1].reshape(1, -1), v[i].reshape(1, -1), what)
+            chk("attention", o[i:i + 1], gqa(q[i:i + 1], Kc, Vc), what)
+        f = blk.ffn
+        experts = [f"{p}.ffn.experts.{e}" for e in range(f.n_experts)] + [f"{p}.ffn.shared_expert"]
+        outs = []
+        for e in experts:
+            act = torch.nn.functional.silu(rec[e + ".w1"][1]) * rec[e + ".w3"][1]
+            chk("swiglu", rec[e + ".w2"][0][0], act, e)
+            outs.append(rec[e + ".w2"][1].float())
+        logits = ffn_in.float() @ f.gate_weight.float().t()
+        idx = torch.topk(logits + f.expert_bias, f.top_k, -1).indices
+        w = torch.gather(torch.sigmoid(logits), -1, idx)
+        w = w / (w.sum(-1, keepdim=True) + 1e-10)
+        want = outs[-1].clone()
+        for j in range(f.top_k):
+            for e in range(f.n_experts):
+                sel = idx[:, j] == e
+                want[sel] += w[sel, j:j + 1] * outs[e][sel]
+        chk("moe_combine", ffn_out, want.to(torch.bfloat16), p)
+        assert y is ffn_out
+    (head_in,), _ = rec["lm_head"]
+    (_, (y, res_out)) = rec[f"layers.{len(model.layers) - 1}"]
+    chk("norm", head_in, rms(y, model.final_norm.weight, cfg.rms_eps, res_out)[0], "final_norm")
+    return worst
+
+
+def _decode(runner, seqs, eager):
+    ids, pos = runner.prepare_decode(seqs)
+    old = runner.enforce_eager
+    runner.enforce_eager = eager
+    try:
+        logits = runner.run_model(ids, pos, False).float()
+    finally:
+        runner.enforce_eager = old
+        reset_context()
+    return logits
+
+
+@torch.inference_mode()
+def test_decode_steps_match_full_forward_small(block_size):
+    """Prefill (with a shared cached prefix), then three decode steps crossing
+    block boundaries (BS=16); graph replay == eager, replays repeatable."""
+    BS = 16
+    Sequence.block_size = BS
+    model = DecodeModel(SMALL, device="cuda", seed=11)
+    runner = ModelRunner(model, SMALL.runner_config(block_size=BS, num_kv_blocks=128, max_num_seqs=8))
+    bm = BlockManager(128, BS)
+    rng = np.random.default_rng(0)
+    prefix = rng.integers(0, SMALL.vocab_size, 2 * BS).tolist()
+    prompts = [rng.integers(0, SMALL.vocab_size, n).tolist() for n in (15, 16, 17, 47)]
+    prompts.append(prefix + rng.integers(0, SMALL.vocab_size, 5).tolist())
+    seqs = [Sequence(p) for p in prompts]
+    for s in seqs:
+        bm.allocate(s)
+    later = Sequence(prefix + rng.integers(0, SMALL.vocab_size, 9).tolist())
+    errs = []
+    got = _prefill(runner, seqs)
+    for i, s in enumerate(seqs):
+        errs.append(rel_err_rows(got[i], ref_logits(model, s.token_ids)[-1]).item())
+        assert errs[-1] <= e2e_tol(SMALL.num_layers), f"prefill seq {i} len {len(s)} rel err {errs[-1]:.4f}"
+    # a second prefill whose first two blocks come from the prefix cache
+    bm.allocate(later)
+    assert later.num_cached_tokens == 2 * BS
+    got = _prefill(runner, [later])
+    errs.append(rel_err_rows(got[0], ref_logits(model, later.token_ids)[-1]).item())
+    assert errs[-1] <= e2e_tol(SMALL.num_layers), f"cached-prefix prefill rel err {errs[-1]:.4f}"
+    seqs.append(later)
+    worst = {}
+    for step in range(3):
+        for s in seqs:
+            s.append_token(int(rng.integers(0, SMALL.vocab_size)))
+            assert bm.can_append(s)
+            bm.append(s)
+        g1 = _decode(runner, seqs, eager=False)
+        e = _decode(runner, seqs, eager=True)
+        g2 = _decode(runner, seqs, eager=False)
+        assert torch.equal(g1, g2), f"graph replays differ at step {step}"
+        assert (rel_err_rows(g1, e) <= 1e-2).all(), f"graph vs eager at step {step}"
+        for i, s in enumerate(seqs):
+            errs.append(rel_err_rows(g1[i], ref_logits(model, s.token_ids)[-1]).item())
+            assert errs[-1] <= e2e_tol(SMALL.num_layers), f"step {step} seq {i} len {len(s)} rel err {errs[-1]:.4f}"
+        for k, v in check_layers_teacher_forced(model, runner, seqs).items():
+            worst[k] = max(worst.get(k, 0.0), v)
+    print(f"\nsmall model: e2e rel err max {max(errs):.4f} median {np.median(errs):.4f}; "
+          f"per-stage max " + ", ".join(f"{k} {v:.2e}" for k, v in worst.items()))
+
+
+@torch.inference_mode()
+def test_decode_step_cfg5_shapes(block_size):
+    """The config-5 model (12 layers, d=768, GQA 12/4, 8 experts top-2 + 1
+    shared, vocab 32000) on 16 sequences with contexts in [256, 2048]."""
+    BS = 256
+    Sequence.block_size = BS
+    cfg = DecodeModelConfig()
+    model = DecodeModel(cfg, device="cuda", seed=4)
+    runner = ModelRunner(model, cfg.runner_config(block_size=BS, num_kv_blocks=160, max_num_seqs=16))
+    bm = BlockManager(160, BS)
+    rng = np.random.default_rng(4)
+    seqs = [Sequence(rng.integers(0, cfg.vocab_size, int(n)).tolist())
+            for n in rng.integers(256, 2048, 16)]
+    seqs[0] = Sequence(rng.integers(0, cfg.vocab_size, 4 * BS - 1).tolist())  # next token fills a block
+    for s in seqs:
+        bm.allocate(s)
+    _prefill(runner, seqs)
+    for s in seqs:
+        s.append_token(int(rng.integers(0, cfg.vocab_size)))
+        bm.append(s)
+    got = _decode(runner, seqs, eager=False)
+    worst = check_layers_teacher_forced(model, runner, seqs)
+    rows = (0, 1, 7, 15)
+    errs = [rel_err_rows(got[i], ref_logits(model, seqs[i].token_ids)[-1]).item() for i in rows]
+    print(f"\ncfg5 model: e2e rel err {['%.4f' % e for e in errs]}; per-stage max "
+          + ", ".join(f"{k} {v:.2e}" for k, v in worst.items()))
+    for i, e in zip(rows, errs):
+        assert e <= e2e_tol(cfg.num_layers), f"seq {i} len {len(seqs[i])} rel err {e:.4f}"
+
+
+@torch.inference_mode()
+def test_engine_generate_runs_to_max_tokens(block_size):
+    BS = 16
+    Sequence.block_size = BS
+    model = DecodeModel(SMALL, device="cuda", seed=3)
+    cfg = SMALL.runner_config(block_size=BS, num_kv_blocks=24, max_num_seqs=4, max_num_sequences=4,
+                              max_num_batched_tokens=256, eos=-1)
+    eng = LLMEngine(model, cfg, generator=torch.Generator(device="cuda").manual_seed(0))
+    rng = np.random.default_rng(5)
+    prompts = [rng.integers(0, SMALL.vocab_size, n).tolist() for n in (3, 30, 17, 40, 9, 16)]
+    out = eng.generate(prompts, SamplingParams(temperature=0.8, max_tokens=20))
+    assert [len(t) for t in out["token_ids"]] == [20] * len(prompts)
+    assert all(0 <= t < SMALL.vocab_size for toks in out["token_ids"] for t in toks)
+    bm = eng.scheduler.block_manager
+    assert len(bm.free_block_ids) == 24 and not bm.used_block_ids
