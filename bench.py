@@ -28,6 +28,13 @@ import torch
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
 METRIC = "FP8 block-GEMM TFLOP/s & paged-decode HBM GB/s (% of MI355X roofline)"
+# Fabric bytes per fp8_gemm launch, averaged over the six headline shapes,
+# from two rocprofv3 --pmc runs of this script (FETCH_SIZE, then WRITE_SIZE;
+# `--no-cpu --extras act_quant,cfg3 --steps 3 --warmup 1 --copy-calibration`),
+# summarised in profiles/fp8_gemm_cfg2_sweep.md.  FETCH_SIZE is scaled by 2.0
+# and WRITE_SIZE by 1.0: a 256 MiB device copy in the same runs reads back
+# 128 MiB fetched and 256 MiB written.  Re-measure after kernel changes.
+GEMM_TRAFFIC_BYTES = 198.1e6
 
 
 def log(*a):
@@ -63,7 +70,8 @@ def gemm_setup(device):
             wq, ws = K.weight_quant(w)
             del x, w
             cases.append(dict(M=M, K=Kd, N=N, a=xq, a_s=xs, b=wq, b_s=ws,
-                              flops=2.0 * M * N * Kd))
+                              flops=2.0 * M * N * Kd,
+                              bytes=M * Kd + N * Kd + 4 * (xs.numel() + ws.numel()) + 2 * M * N))
     return cases
 
 
@@ -129,6 +137,58 @@ def bench_decode(name, device, reps, flush_buf):
     return out
 
 
+def bench_decode_step(device, reps):
+    """cfg5: one graph-captured decode step (12-layer GQA + MoE model, FP8
+    linears, paged KV) for 128 sequences with contexts U{256..2048}, plus
+    lm_head and Gumbel-max sampling.  Synthetic KV (random pool contents),
+    random-init weights."""
+    from llm_from_scratch_amd.decode_model import DecodeModel, DecodeModelConfig
+    from llm_from_scratch_amd.engine import ModelRunner, Sequence
+    from llm_from_scratch_amd.fp8_linear import FP8Linear
+    cfg = DecodeModelConfig()
+    BS, B = 256, 128
+    rng = np.random.default_rng(4)
+    lens = rng.integers(256, 2049, B)
+    nblk = (lens + BS - 1) // BS
+    total = int(nblk.sum())
+    Sequence.block_size = BS
+    model = DecodeModel(cfg, device=device, seed=4)
+    runner = ModelRunner(model, cfg.runner_config(block_size=BS, num_kv_blocks=total, max_num_seqs=B))
+    runner.kv_cache.normal_(generator=torch.Generator(device=device).manual_seed(4))
+    perm = rng.permutation(total)
+    seqs, off = [], 0
+    for L, n in zip(lens, nblk):
+        s = Sequence(rng.integers(0, cfg.vocab_size, int(L)).tolist())
+        s.block_table = perm[off:off + n].tolist()
+        off += n
+        seqs.append(s)
+    ids, pos = runner.prepare_decode(seqs)
+    temps = runner.prepare_sample(seqs)
+    runner.run_model(ids, pos, False)  # fills the static graph inputs
+    graph = runner.graphs[B]
+    hidden = runner.graph_vars["outputs"][:B]
+    gen = torch.Generator(device=device).manual_seed(0)
+
+    def step():
+        graph.replay()
+        return runner.sampler(model.compute_logits(hidden), temps, gen)
+
+    for _ in range(3):
+        step()
+    t = timed_launches([step], reps)[0]
+    w_bytes = sum(m.weight.numel() + 4 * m.weight_scale.numel() + (4 * m.bias.numel() if m.bias is not None else 0)
+                  for m in model.modules() if isinstance(m, FP8Linear))
+    kv = int(lens.sum()) * cfg.num_layers * cfg.num_kv_heads * cfg.head_dim * 2 * 2
+    nbytes = w_bytes + kv
+    out = {"config": "cfg5", "batch": B, "context_tokens": int(lens.sum()), "ms": t * 1e3,
+           "tokens/s": B / t, "bytes": nbytes, "weight_bytes": w_bytes, "kv_bytes": kv,
+           "GB/s": nbytes / t / 1e9, "frac": nbytes / t / 1e9 / HBM_PEAK_GBS,
+           "graph_kernels_note": "decode step captured in one HIP graph; lm_head + sampler eager"}
+    del runner, model
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline():
     """Numpy oracle (blockwise fp32 GEMM, one matmul per 128-wide K block with
     the scale product applied to the partial) on the three M=4096 shapes."""
@@ -160,6 +220,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip decode / act_quant lines")
+    ap.add_argument("--extras", default="act_quant,cfg3,cfg4,cfg5",
+                    help="comma list of extra lines: act_quant, cfg3, cfg4 (paged decode), cfg5 (decode step)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run 4 plain device copies of 256 MiB (a known-traffic kernel for "
+                         "scaling FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -170,6 +235,14 @@ def main():
         sys.exit(1)
     dev = "cuda:0"
     torch.cuda.set_device(0)
+    extras = set() if args.no_extra else set(e for e in args.extras.split(",") if e)
+    if args.copy_calibration:
+        src = torch.empty(256 * 1024 * 1024, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     log("bench: setting up fp8_gemm inputs")
     cases = gemm_setup(dev)
     log("bench: timing fp8_gemm")
@@ -180,6 +253,7 @@ def main():
     shapes = [{"M": c["M"], "K": c["K"], "N": c["N"], "us": t * 1e6,
                "TFLOP/s": c["flops"] / t / 1e12, "frac": c["flops"] / t / 1e12 / FP8_PEAK_TFLOPS}
               for c, t in zip(cases, per)]
+    alg_bytes = sum(c["bytes"] for c in cases) / len(cases)
     del cases
     torch.cuda.empty_cache()
     out = {
@@ -201,21 +275,28 @@ def main():
                    "launches_per_step": len(per)},
         "roofline": {"bound": "mfma", "kernel": "fp8_gemm", "achieved": achieved,
                      "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": achieved / FP8_PEAK_TFLOPS,
-                     "traffic": None},
+                     "traffic": GEMM_TRAFFIC_BYTES,
+                     "algorithmic_bytes": alg_bytes},
         "gemm_shapes": shapes,
     }
-    if not args.no_extra:
-        try:
+    try:
+        if "act_quant" in extras:
             log("bench: act_quant")
             out["act_quant"] = bench_act_quant(dev, 20)
+        decode = [n for n in ("cfg3", "cfg4") if n in extras]
+        if decode:
             flush_buf = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev).zero_()
             out["paged_decode"] = []
-            for name in ("cfg3", "cfg4"):
+            for name in decode:
                 log(f"bench: paged decode {name}")
                 out["paged_decode"].append(bench_decode(name, dev, 20, flush_buf))
             del flush_buf
-        except Exception as e:  # report, keep the headline line
-            out["extra_error"] = repr(e)
+            torch.cuda.empty_cache()
+        if "cfg5" in extras:
+            log("bench: cfg5 decode step")
+            out["decode_step"] = bench_decode_step(dev, 20)
+    except Exception as e:  # report, keep the headline line
+        out["extra_error"] = repr(e)
     if not args.no_cpu:
         log("bench: cpu baseline")
         out["cpu_baseline"] = cpu_baseline()
