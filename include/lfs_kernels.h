@@ -26,6 +26,8 @@
  *                           nn.Linear sites model/attention/GQA.py:34-37,
  *                           model/architecture/mlp.py:56-58); no reference
  *                           counterpart
+ *   lfs_fp8_gemm_splitk     the same GEMM split over K for small M (the
+ *                           decode-step linears)
  *   lfs_store_kvcache       the KV slot write of the attention layer that
  *                           engine/model_runner.py:8 imports (absent from the
  *                           reference); slot contract model_runner.py:226-230,
@@ -34,6 +36,16 @@
  *                           decode call of the same absent layer; math of
  *                           model/attention/GQA.py:118-130, metadata contract
  *                           engine/model_runner.py:253-278 and :288-312
+ * Fused row kernels of the decode step around those calls (each replaces a
+ * chain of torch ops of the reference model):
+ *   lfs_add_rmsnorm         RMSNorm with fused residual add, model/utils.py:53-67
+ *                           (+ act_quant of the output for the next FP8 linear)
+ *   lfs_qk_norm_rope_store  q_norm/k_norm + RoPE + KV slot write,
+ *                           model/attention/GQA.py:80-95,
+ *                           model/attention/utils.py:34-45
+ *   lfs_moe_route           MoE gate, model/architecture/moe.py:45-90
+ *   lfs_swiglu_quant        silu(w1 x) * w3 x, model/architecture/mlp.py:60-67,
+ *                           quantised for the experts' down projection
  */
 #ifndef LFS_KERNELS_H
 #define LFS_KERNELS_H
@@ -44,7 +56,7 @@
 extern "C" {
 #endif
 
-#define LFS_ABI_VERSION 1
+#define LFS_ABI_VERSION 2
 
 /* argument errors (negative); launch errors are positive hipError_t values */
 #define LFS_EINVAL (-1)
@@ -84,15 +96,33 @@ int lfs_weight_dequant(const void* w, const float* s, void* y, int64_t N, int64_
 
 /*
  * fp8_gemm: c[m,n] = bf16_RNE( sum_kb a_s[m,kb] * b_s[n/128,kb] *
- *                              sum_{k in kb} a[m,k] * b[n,k]  (+ bias[n]) )
+ *                              sum_{k in kb} a[m,k] * b[n,k]  (+ bias) )
  * with fp32 accumulation, the per-block scales applied to each 128-wide
- * K-block partial in the fp32 accumulator.
+ * K-block partial in the fp32 accumulator, and the bias added in fp32 before
+ * the single rounding: bias[n] when bias_ld == 0, bias[m * bias_ld + n]
+ * (a per-row bias matrix, bias_ld >= N) otherwise; bias may be NULL.
  * a: e4m3fn [M, K]; a_s: fp32 [M, K/128]; b: e4m3fn [N, K] (nn.Linear
- * weight layout); b_s: fp32 [ceil(N/128), K/128]; bias: fp32 [N] or NULL;
- * c: bf16 [M, N].  All contiguous; K % 128 == 0.
+ * weight layout); b_s: fp32 [ceil(N/128), K/128]; c: bf16 [M, N].
+ * All contiguous; K % 128 == 0.
  */
 int lfs_fp8_gemm(const void* a, const float* a_s, const void* b, const float* b_s,
-                 const float* bias, void* c, int64_t M, int64_t N, int64_t K, void* stream);
+                 const float* bias, int64_t bias_ld, void* c, int64_t M, int64_t N, int64_t K,
+                 void* stream);
+
+/*
+ * fp8_gemm with the K blocks split over `splits` workgroups per output tile
+ * (for small M, where the tiles alone cannot fill the GPU): each split sums
+ * ceil((K/128) / splits) consecutive K blocks into an fp32 partial tile in
+ * `workspace`; a second kernel adds the partials in split order, adds the
+ * bias and rounds to bf16.  Same result contract as lfs_fp8_gemm (fp32
+ * accumulation; the order of the K-block sums differs).  workspace: at least
+ * lfs_fp8_gemm_workspace_bytes(M, N, K, splits) bytes (0 when the split
+ * count reduces to one), 16-byte aligned.
+ */
+int64_t lfs_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t splits);
+int lfs_fp8_gemm_splitk(const void* a, const float* a_s, const void* b, const float* b_s,
+                        const float* bias, int64_t bias_ld, void* c, int64_t M, int64_t N, int64_t K,
+                        int32_t splits, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * store_kvcache: for t < T with slot = slot_mapping[t] != -1,
@@ -131,6 +161,65 @@ int lfs_paged_decode(const void* q, const void* k_cache, const void* v_cache,
                      int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                      int32_t block_size, int64_t num_blocks, int32_t max_blocks, float scale,
                      int32_t blocks_per_split, void* stream);
+
+/*
+ * add_rmsnorm, per row t of x: bf16 [T, d]:
+ *   r = x[t] (+ residual[t])                    fp32 sum of the bf16 inputs
+ *   residual_out[t] = bf16(r)                    (only with a residual)
+ *   out[t] = bf16(weight * r * rsqrt(mean(r^2) + eps))       weight fp32 [d]
+ *   q[t], q_scale[t] = act_quant(out[t], 128)    (optional)
+ * residual and residual_out are both given or both NULL; q and q_scale
+ * likewise (needs d % 128 == 0); out may be NULL when q is given.
+ * d % 8 == 0, d <= 8192; all rows contiguous.
+ */
+int lfs_add_rmsnorm(const void* x, const void* residual, const float* weight, void* out,
+                    void* residual_out, void* q, float* q_scale, int64_t T, int32_t d, float eps,
+                    void* stream);
+
+/*
+ * qk_norm_rope_store, per token t of qkv: bf16 [T, ld], row = [q (Hq*D) |
+ * k (Hkv*D) | v (Hkv*D)]:
+ *   q' = bf16(q_weight * q * rsqrt(mean(q^2) + eps)) over all Hq*D values,
+ *   k' likewise over Hkv*D with k_weight; then per head the half-split
+ *   rotation with c, s = cos_sin[positions[t]][0..D/2), [D/2..D):
+ *   y1 = x1*c - x2*s, y2 = x2*c + x1*s (fp32), rounded to bf16;
+ *   q_out[t] (bf16 [T, Hq, D]) = rotated q'; rotated k' and v are written to
+ *   k_cache / v_cache (bf16 [NB, BS, Hkv, D]) at slot slot_mapping[t] when
+ *   0 <= slot < num_slots (slot_mapping may be NULL: no cache write).
+ * cos_sin: fp32 [max_positions, D]; positions int64 [T] (clamped to the
+ * table).  D % 16 == 0; (Hq + Hkv) * D <= 16384.
+ */
+int lfs_qk_norm_rope_store(const void* qkv, int64_t ld, const float* q_weight, const float* k_weight,
+                           const float* cos_sin, const int64_t* positions,
+                           const int64_t* slot_mapping, void* q_out, void* k_cache, void* v_cache,
+                           int64_t T, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                           int64_t num_slots, int64_t max_positions, float eps, void* stream);
+
+/*
+ * moe_route, per token t of h: bf16 [T, d]:
+ *   logit[e] = h[t] . gate_weight[e] (fp32), gate_weight bf16 [E, d];
+ *   the top_k experts by logit + expert_bias[e] (ties: lower index) get
+ *   weight sigmoid(logit[e]) / (sum over the chosen + 1e-10) (top_k > 1) or
+ *   sigmoid(logit[e]) (top_k == 1), the others 0;
+ *   dense_weights[t] (fp32 [T, E + S]) = those weights, then S ones for the
+ *   shared experts; bias_out[t] (fp32 [T, d]) = sum_e dense_weights[t][e] *
+ *   down_bias[e] (fp32 [E + S, d]).
+ * E + S <= 64; d % 8 == 0.
+ */
+int lfs_moe_route(const void* h, const void* gate_weight, const float* expert_bias,
+                  const float* down_bias, float* dense_weights, float* bias_out, int64_t T,
+                  int32_t d, int32_t num_experts, int32_t num_shared, int32_t top_k, void* stream);
+
+/*
+ * swiglu_quant, for h13: bf16 [T, E, 2, F] (per expert the w1 then the w3
+ * output rows):
+ *   g = bf16(bf16(silu(a)) * b), silu(a) = a / (1 + exp(-a)) in fp32;
+ *   q (e4m3fn [T, E*F]), s = act_quant(g, 128) per row;
+ *   q_scale[t][e*F/128 + i] = s * route_weights[t][e] (fp32 [T, E]).
+ * F % 128 == 0.
+ */
+int lfs_swiglu_quant(const void* h13, const float* route_weights, void* q, float* q_scale, int64_t T,
+                     int32_t num_experts, int32_t d_ff, void* stream);
 
 #ifdef __cplusplus
 }

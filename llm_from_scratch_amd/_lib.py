@@ -11,7 +11,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "liblfs_kernels.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _c_i64, _c_i32, _c_p, _c_f = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p, ctypes.c_float
 
@@ -22,13 +22,23 @@ SIGNATURES = {
     "lfs_act_quant": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_p]),
     "lfs_weight_quant": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_p]),
     "lfs_weight_dequant": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_p]),
-    "lfs_fp8_gemm": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p]),
+    "lfs_fp8_gemm": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
+                                    _c_p]),
+    "lfs_fp8_gemm_workspace_bytes": (ctypes.c_int64, [_c_i64, _c_i64, _c_i64, _c_i32]),
+    "lfs_fp8_gemm_splitk": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
+                                           _c_i32, _c_p, _c_i64, _c_p]),
     "lfs_store_kvcache": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_i32,
                                          _c_i32, _c_i64, _c_p]),
     "lfs_paged_decode_workspace_bytes": (ctypes.c_int64, [_c_i64, _c_i32, _c_i32, _c_i32, _c_i32]),
     "lfs_paged_decode": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64,
                                         _c_i32, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_f, _c_i32,
                                         _c_p]),
+    "lfs_add_rmsnorm": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_f, _c_p]),
+    "lfs_qk_norm_rope_store": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
+                                              _c_i64, _c_i32, _c_i32, _c_i32, _c_i64, _c_i64, _c_f, _c_p]),
+    "lfs_moe_route": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_i32,
+                                     _c_i32, _c_p]),
+    "lfs_swiglu_quant": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_p]),
 }
 
 _LIB = None

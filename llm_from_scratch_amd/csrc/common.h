@@ -69,6 +69,39 @@ __device__ __forceinline__ void e4m3x4_to_f32(uint32_t w, float* o) {
   o[0] = lo[0]; o[1] = lo[1]; o[2] = hi[0]; o[3] = hi[1];
 }
 
+// ------------------------------------------------ e4m3 block quantisation --
+// fp32(1/448): the reference multiplies the fp32 amax by fp8_max_inv
+// (utils.py:101, :135); 1.0f/448.0f is the same correctly rounded constant.
+constexpr float kFp8Max = 448.0f;
+constexpr float kFp8MaxInv = 1.0f / 448.0f;
+constexpr float kAmaxFloor = 1e-4f;  // utils.py:131
+
+__device__ __forceinline__ float scale_from_amax(float amax, bool round_scale) {
+  float s = fmaxf(amax, kAmaxFloor) * kFp8MaxInv;
+  if (round_scale) {
+    // ue8m0: smallest power of two >= s (utils.py:81-94)
+    uint32_t b = __float_as_uint(s);
+    int e = (int)((b >> 23) & 0xFFu) - 127 + ((b & 0x7FFFFFu) != 0u ? 1 : 0);
+    s = __uint_as_float((uint32_t)(e + 127) << 23);
+  }
+  return s;
+}
+
+// clamp(x / s, -448, 448) with an IEEE divide; NaN passes through
+__device__ __forceinline__ float qdiv(float x, float s) {
+  float q = x / s;
+  q = q > kFp8Max ? kFp8Max : q;
+  q = q < -kFp8Max ? -kFp8Max : q;
+  return q;
+}
+
+__device__ __forceinline__ uint2 quant8(const float* f, float s) {
+  uint2 o;
+  o.x = f32x4_to_e4m3(qdiv(f[0], s), qdiv(f[1], s), qdiv(f[2], s), qdiv(f[3], s));
+  o.y = f32x4_to_e4m3(qdiv(f[4], s), qdiv(f[5], s), qdiv(f[6], s), qdiv(f[7], s));
+  return o;
+}
+
 // ------------------------------------------------------- wave reductions --
 // xor-butterfly over groups of W consecutive lanes (W a power of two <= 64)
 template <int W>

@@ -1,6 +1,7 @@
 // Block-scaled FP8 GEMM on gfx950 MFMA.
 //
-//   C[m,n] = bf16( sum_kb a_s[m,kb] * b_s[n/128,kb] * (A[m,kb*128:+128] . B[n,kb*128:+128]) + bias[n] )
+//   C[m,n] = bf16( sum_kb a_s[m,kb] * b_s[n/128,kb] * (A[m,kb*128:+128] . B[n,kb*128:+128]) + bias )
+//   with bias = bias[n] (bias_ld == 0) or bias[m*bias_ld + n] (a per-row bias matrix)
 //
 // One 128-wide K block is exactly one v_mfma_f32_16x16x128_f8f6f4 per 16x16
 // output tile, so every MFMA starts from a zero accumulator and its result is
@@ -110,8 +111,8 @@ __device__ __forceinline__ int swz(int r, int c) {
 template <int BM, int NST, int SCK>
 __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ B,
-    const float* __restrict__ Bs, const float* __restrict__ bias, uint16_t* __restrict__ C, int M,
-    int N, int K, int tiles_m, int tiles_n) {
+    const float* __restrict__ Bs, const float* __restrict__ bias, int64_t bias_ld, uint16_t* __restrict__ C, int M,
+    int N, int K, int tiles_m, int tiles_n, float* __restrict__ ws, int kps) {
   constexpr int NW = BM / 32;  // waves
   constexpr int NT = 64 * NW;  // threads
   constexpr int SCP = BM + 1;  // padded row of the k-major scale table
@@ -139,7 +140,12 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int wm = wave >> 1, wn = wave & 1;
-  const int KT = K / BK;
+  const int KTA = K / BK;                  // K blocks of a row (scale row stride)
+  // split-K: this workgroup sums K blocks kb0 .. kb0+KT-1 (blockIdx.y-th
+  // split of kps blocks) and, with more than one split, writes its fp32
+  // partial tile to ws[split] instead of C
+  const int kb0 = blockIdx.y * kps;
+  const int KT = min(kps, KTA - kb0);
   const int r16 = lane & 15, g = lane >> 4;
 
   // ---- DMA sources: segment q = wave + NW*u covers tile rows 8q .. 8q+7
@@ -150,16 +156,17 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
   for (int u = 0; u < A_PER_WAVE; ++u) {
     const int r = 8 * (wave + NW * u) + (lane >> 3);
     const int c = (lane & 7) ^ (((r >> 1) & 7) ^ ((r & 1) << 2));
-    srcA[u] = A + (size_t)min(m0 + r, M - 1) * K + c * 16;
+    srcA[u] = A + (size_t)min(m0 + r, M - 1) * K + (size_t)kb0 * BK + c * 16;
   }
 #pragma unroll
   for (int u = 0; u < B_PER_WAVE; ++u) {
     const int r = 8 * (wave + NW * u) + (lane >> 3);
     const int c = (lane & 7) ^ (((r >> 1) & 7) ^ ((r & 1) << 2));
-    srcB[u] = B + (size_t)min(n0 + r, N - 1) * K + c * 16;
+    srcB[u] = B + (size_t)min(n0 + r, N - 1) * K + (size_t)kb0 * BK + c * 16;
   }
   const unsigned lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
-  const float* bs_row = Bs + (size_t)(n0 / 128) * KT;
+  const float* bs_row = Bs + (size_t)(n0 / 128) * KTA + kb0;
+  const float* as_base = As + kb0;
 
   auto issue = [&](int kt, int buf) {
     const unsigned base = lds0 + buf * STAGE;
@@ -178,7 +185,7 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
       const int idx = tid + NT * v;
       const int row = idx / SCK, k = idx % SCK;
       ssc[k * SCP + row] =
-          k < nk ? As[(size_t)min(m0 + row, M - 1) * KT + kt0 + k] * bs_row[kt0 + k] : 0.f;
+          k < nk ? as_base[(size_t)min(m0 + row, M - 1) * KTA + kt0 + k] * bs_row[kt0 + k] : 0.f;
     }
   };
 
@@ -251,6 +258,30 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
     }
   }
 
+  if (ws != nullptr) {
+    // split-K partial: fp32, no bias; lane holds rows 16i + r16, columns
+    // 16j + 4g .. +3 of its wave's 64x64 tile
+    float* wsp = ws + (size_t)blockIdx.y * M * N;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = m0 + wm * 64 + i * 16 + r16;
+      if (row >= M) continue;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int col = n0 + wn * 64 + j * 16 + 4 * g;
+        float* dst = wsp + (size_t)row * N + col;
+        if (col + 3 < N && (N & 3) == 0) {
+          *reinterpret_cast<float4*>(dst) = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (col + r < N) dst[r] = acc[i][j][r];
+        }
+      }
+    }
+    return;
+  }
+
   // ---- epilogue: bias, bf16 (RNE), then each wave's 64x64 tile goes
   // through LDS (the idle stage buffers) so that global stores are whole
   // 128-byte rows: 16-byte chunk c of row r sits at chunk slot c ^ (r & 7)
@@ -260,7 +291,7 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
   for (int j = 0; j < 4; ++j) {
     const int cl = j * 16 + 4 * g;  // first of this lane's 4 columns in the wave tile
     float bv[4] = {0.f, 0.f, 0.f, 0.f};
-    if (bias != nullptr) {
+    if (bias != nullptr && bias_ld == 0) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int col = n0 + wn * 64 + cl + r;
@@ -270,6 +301,14 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int rl = i * 16 + r16;
+      if (bias != nullptr && bias_ld != 0) {
+        const int row = m0 + wm * 64 + rl;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int col = n0 + wn * 64 + cl + r;
+          bv[r] = (row < M && col < N) ? bias[(int64_t)row * bias_ld + col] : 0.f;
+        }
+      }
       uint2 o;
       o.x = pack_bf16x2(acc[i][j][0] + bv[0], acc[i][j][1] + bv[1]);
       o.y = pack_bf16x2(acc[i][j][2] + bv[2], acc[i][j][3] + bv[3]);
@@ -296,31 +335,100 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
   }
 }
 
+// out[m, n] = bf16(sum_s ws[s, m, n] + bias), four columns per thread
+__global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ ws, int splits,
+                                                     const float* __restrict__ bias, int64_t bias_ld,
+                                                     uint16_t* __restrict__ C, int64_t M, int64_t N) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;  // float4 index
+  const int64_t nq = (N + 3) / 4;
+  if (q >= M * nq) return;
+  const int64_t m = q / nq, n = (q - m * nq) * 4;
+  const int64_t MN = M * N;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < splits; ++s) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (n + r < N) v[r] += ws[s * MN + m * N + n + r];
+  }
+  if (bias != nullptr) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (n + r < N) v[r] += bias[(bias_ld ? m * bias_ld : 0) + n + r];
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    if (n + r < N) C[m * N + n + r] = (uint16_t)f32_to_bf16(v[r]);
+}
+
 }  // namespace
 }  // namespace lfs
 
 using namespace lfs;
 
-extern "C" int lfs_fp8_gemm(const void* a, const float* a_s, const void* b, const float* b_s,
-                            const float* bias, void* c, int64_t M, int64_t N, int64_t K,
-                            void* stream) {
+extern "C" int64_t lfs_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t splits) {
+  if (M <= 0 || N <= 0 || K <= 0 || splits <= 1) return 0;
+  const int64_t KT = K / 128;
+  const int64_t kps = (KT + splits - 1) / splits;
+  const int64_t used = (KT + kps - 1) / kps;
+  return used > 1 ? used * M * N * 4 : 0;
+}
+
+namespace {
+int fp8_gemm_impl(const void* a, const float* a_s, const void* b, const float* b_s, const float* bias,
+                  int64_t bias_ld, void* c, int64_t M, int64_t N, int64_t K, int32_t splits,
+                  void* workspace, int64_t workspace_bytes, void* stream) {
   LFS_REQUIRE(M >= 0 && N >= 0 && K >= 0, "fp8_gemm: negative shape");
   LFS_REQUIRE(K % 128 == 0, "fp8_gemm: K=%lld must be a multiple of 128", (long long)K);
   LFS_REQUIRE(M < (1ll << 31) && N < (1ll << 31) && K < (1ll << 31) && M * K < (1ll << 40),
               "fp8_gemm: shape too large");
+  LFS_REQUIRE(splits >= 1, "fp8_gemm: splits must be >= 1");
   if (M == 0 || N == 0) return 0;
   LFS_REQUIRE(a && a_s && b && b_s && c, "fp8_gemm: null pointer");
   LFS_REQUIRE(K > 0, "fp8_gemm: K must be positive");
   LFS_REQUIRE((((uintptr_t)a | (uintptr_t)b) & 15u) == 0, "fp8_gemm: a and b must be 16-byte aligned");
   LFS_REQUIRE(((uintptr_t)c & 15u) == 0, "fp8_gemm: c must be 16-byte aligned");
+  LFS_REQUIRE(bias_ld == 0 || (bias != nullptr && bias_ld >= N), "fp8_gemm: bias_ld must be 0 or >= N");
   const int64_t tiles_n = (N + BN - 1) / BN;
   const int64_t tiles_m128 = (M + 127) / 128;
   LFS_REQUIRE(tiles_m128 * tiles_n < (1ll << 31), "fp8_gemm: too many tiles");
+  const int KT = (int)(K / 128);
+  int kps = (KT + splits - 1) / splits;
+  const int used = (KT + kps - 1) / kps;
+  float* ws = nullptr;
+  if (used > 1) {
+    const int64_t need = (int64_t)used * M * N * 4;
+    LFS_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+                "fp8_gemm: split-K needs a workspace of %lld bytes", (long long)need);
+    LFS_REQUIRE(((uintptr_t)workspace & 15u) == 0, "fp8_gemm: workspace must be 16-byte aligned");
+    ws = (float*)workspace;
+  } else {
+    kps = KT;
+  }
   hipStream_t st = (hipStream_t)stream;
   // 128x128 tiles, two workgroups per CU.  (256x128 tiles with one
   // 8-wave workgroup per CU measured 10-15% slower on every benchmark shape.)
-  hipLaunchKernelGGL((fp8_gemm_tile<128, 2, 16>), dim3((unsigned)(tiles_m128 * tiles_n)), dim3(256), 0, st,
-                     (const uint8_t*)a, a_s, (const uint8_t*)b, b_s, bias, (uint16_t*)c, (int)M,
-                     (int)N, (int)K, (int)tiles_m128, (int)tiles_n);
-  return check_launch("fp8_gemm");
+  hipLaunchKernelGGL((fp8_gemm_tile<128, 2, 16>), dim3((unsigned)(tiles_m128 * tiles_n), (unsigned)(used > 1 ? used : 1)),
+                     dim3(256), 0, st, (const uint8_t*)a, a_s, (const uint8_t*)b, b_s, bias, bias_ld,
+                     (uint16_t*)c, (int)M, (int)N, (int)K, (int)tiles_m128, (int)tiles_n, ws, kps);
+  int rc = check_launch("fp8_gemm");
+  if (rc != 0 || ws == nullptr) return rc;
+  const int64_t quads = M * ((N + 3) / 4);
+  hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st, ws, used, bias,
+                     bias_ld, (uint16_t*)c, M, N);
+  return check_launch("fp8_gemm split-K reduce");
+}
+}  // namespace
+
+extern "C" int lfs_fp8_gemm(const void* a, const float* a_s, const void* b, const float* b_s,
+                            const float* bias, int64_t bias_ld, void* c, int64_t M, int64_t N,
+                            int64_t K, void* stream) {
+  return fp8_gemm_impl(a, a_s, b, b_s, bias, bias_ld, c, M, N, K, 1, nullptr, 0, stream);
+}
+
+extern "C" int lfs_fp8_gemm_splitk(const void* a, const float* a_s, const void* b, const float* b_s,
+                                   const float* bias, int64_t bias_ld, void* c, int64_t M, int64_t N,
+                                   int64_t K, int32_t splits, void* workspace, int64_t workspace_bytes,
+                                   void* stream) {
+  return fp8_gemm_impl(a, a_s, b, b_s, bias, bias_ld, c, M, N, K, splits, workspace, workspace_bytes,
+                       stream);
 }

@@ -1,0 +1,425 @@
+// Row-wise fused kernels of the paged GQA + MoE decode step (gfx950).
+//
+// Each replaces a chain of small elementwise / reduction launches around the
+// FP8 GEMMs with one launch that reads its rows once:
+//
+//  add_rmsnorm        fused residual add + RMSNorm (model/utils.py:53-67),
+//                     optionally also act_quant of the normalised row
+//                     (model/attention/utils.py:129-139) for the next FP8
+//                     linear.
+//  qk_norm_rope_store q_norm over d_model and k_norm over Hkv*D (fp32, as
+//                     torch.nn.RMSNorm, model/attention/GQA.py:39-40, 80-81),
+//                     half-split RoPE (model/attention/utils.py:34-45) of q
+//                     and k, q to its own buffer, k and v to the paged cache
+//                     slot (engine/model_runner.py:226-230, :261).
+//  moe_route          sigmoid gate, top-k of the biased logits, weights
+//                     renormalised over the chosen experts
+//                     (model/architecture/moe.py:45-90) as a dense [T, E+S]
+//                     matrix (shared experts weight 1), and the routed bias
+//                     sum_e w[t,e] * b2[e,:] of the experts' down projections.
+//  swiglu_quant       silu(w1 x) * (w3 x) with the reference's bf16 roundings
+//                     (model/architecture/mlp.py:60-67), act_quant of the
+//                     result per 128 group, each group's scale multiplied by
+//                     the token's routing weight for that expert.
+//
+// Rounding follows the torch ops they replace: fp32 math, products and sums
+// as separate correctly rounded operations (no contraction into FMAs where
+// torch computes two ops), bf16 round-to-nearest-even where torch stores
+// bf16.  Row reductions (the RMS mean, the gate dot products) are summed in a
+// different order than torch's reduction kernels, so their results can differ
+// in the last fp32 bit.
+#include "common.h"
+
+namespace lfs {
+namespace {
+
+// Sum over a workgroup of NW waves; every thread gets the total.
+template <int NW>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = group_sum<64>(v);
+  if (NW == 1) return v;
+  const int wave = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) t += red[w];
+  return t;
+}
+
+__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
+__device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, b); }
+
+// ------------------------------------------------------------ add_rmsnorm --
+// One workgroup of 128 threads per row; thread c handles 16-byte chunks
+// c, c + 128, ... (CPT of them).  With quantisation, a 128-element group is
+// 16 consecutive chunks, which sit in 16 consecutive lanes of one wave.
+template <int CPT, bool QUANT>
+__global__ __launch_bounds__(128) void add_rmsnorm_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ residual,
+    const float* __restrict__ w, uint16_t* __restrict__ out, uint16_t* __restrict__ res_out,
+    uint8_t* __restrict__ q, float* __restrict__ qs, int d, float eps) {
+  __shared__ float red[2];
+  const int64_t row = blockIdx.x;
+  const int cpr = d / 8;
+  float f[CPT][8];
+  float4 wq[CPT][2];  // weights, loaded before the reduction
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = threadIdx.x + 128 * i;
+    if (c < cpr) {
+      wq[i][0] = *reinterpret_cast<const float4*>(w + c * 8);
+      wq[i][1] = *reinterpret_cast<const float4*>(w + c * 8 + 4);
+      unpack8(*reinterpret_cast<const uint4*>(x + row * d + c * 8), f[i]);
+      if (residual != nullptr) {
+        float r[8];
+        unpack8(*reinterpret_cast<const uint4*>(residual + row * d + c * 8), r);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[i][e] = add_rn(f[i][e], r[e]);
+        uint4 o;
+        o.x = pack_bf16x2(f[i][0], f[i][1]);
+        o.y = pack_bf16x2(f[i][2], f[i][3]);
+        o.z = pack_bf16x2(f[i][4], f[i][5]);
+        o.w = pack_bf16x2(f[i][6], f[i][7]);
+        *reinterpret_cast<uint4*>(res_out + row * d + c * 8) = o;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = add_rn(ss, mul_rn(f[i][e], f[i][e]));
+    }
+  }
+  const float total = block_sum<2>(ss, red);
+  const float inv = rsqrtf(add_rn(mul_rn(total, 1.0f / (float)d), eps));
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = threadIdx.x + 128 * i;
+    const bool ok = c < cpr;
+    float y[8];
+    if (ok) {
+      const float4 w0 = wq[i][0], w1 = wq[i][1];
+      const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = bf16_to_f32(f32_to_bf16(mul_rn(mul_rn(wv[e], f[i][e]), inv)));
+      uint4 o;
+      o.x = pack_bf16x2(y[0], y[1]);
+      o.y = pack_bf16x2(y[2], y[3]);
+      o.z = pack_bf16x2(y[4], y[5]);
+      o.w = pack_bf16x2(y[6], y[7]);
+      if (out != nullptr) *reinterpret_cast<uint4*>(out + row * d + c * 8) = o;
+    }
+    if (QUANT) {
+      float amax = 0.f;
+      if (ok) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(y[e]));
+      }
+      amax = group_max<16>(amax);
+      if (ok) {
+        const float sc = scale_from_amax(amax, false);
+        *reinterpret_cast<uint2*>(q + row * d + c * 8) = quant8(y, sc);
+        if ((c & 15) == 0) qs[row * (d / 128) + c / 16] = sc;
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------- qk_norm_rope_store --
+// One workgroup of 256 threads per token.  A "unit" is one head's pair of
+// 8-element chunks (d0..d0+7, D/2+d0..D/2+d0+7) that RoPE combines; q has
+// Hq*D/16 units, k has Hkv*D/16.  Each thread keeps up to UPT units in
+// registers between the norm reduction and the rotation.
+constexpr int kRopeUPT = 4;
+
+__global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(
+    const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ qw,
+    const float* __restrict__ kw, const float* __restrict__ cos_sin, const int64_t* __restrict__ pos,
+    const int64_t* __restrict__ slots, uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc,
+    uint16_t* __restrict__ vc, int Hq, int Hkv, int D, int64_t num_slots, int64_t max_pos,
+    float eps) {
+  __shared__ float red[4];
+  const int64_t t = blockIdx.x;
+  const uint16_t* row = qkv + t * ld;
+  const int half = D / 2, upr = D / 16;  // units per head
+  const int uq = Hq * upr, uk = Hkv * upr;
+  int64_t p = pos[t];
+  p = p < 0 ? 0 : (p >= max_pos ? max_pos - 1 : p);
+  const float* cs = cos_sin + p * D;  // [cos(0..D/2) | sin(0..D/2)]
+  const int64_t slot = slots != nullptr ? slots[t] : -1;
+  const bool store = slot >= 0 && slot < num_slots;
+
+  float a[kRopeUPT][8], b[kRopeUPT][8];
+  float ssq = 0.f, ssk = 0.f;
+#pragma unroll
+  for (int i = 0; i < kRopeUPT; ++i) {
+    const int u = threadIdx.x + 256 * i;
+    if (u < uq + uk) {
+      const bool isq = u < uq;
+      const int uu = isq ? u : u - uq;
+      const int h = uu / upr, d0 = (uu % upr) * 8;
+      const uint16_t* src = row + (isq ? 0 : Hq * D) + h * D;
+      unpack8(*reinterpret_cast<const uint4*>(src + d0), a[i]);
+      unpack8(*reinterpret_cast<const uint4*>(src + half + d0), b[i]);
+      float s = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s = add_rn(s, add_rn(mul_rn(a[i][e], a[i][e]), mul_rn(b[i][e], b[i][e])));
+      if (isq) ssq = add_rn(ssq, s); else ssk = add_rn(ssk, s);
+    }
+  }
+  // v: straight copy into the cache slot (Hkv*D/8 chunks)
+  if (store) {
+    const int64_t dst = slot * (int64_t)Hkv * D;
+    for (int c = threadIdx.x; c < Hkv * D / 8; c += 256)
+      *reinterpret_cast<uint4*>(vc + dst + c * 8) =
+          *reinterpret_cast<const uint4*>(row + (Hq + Hkv) * D + c * 8);
+  }
+  // two block sums at once
+  ssq = group_sum<64>(ssq);
+  ssk = group_sum<64>(ssk);
+  const int wave = threadIdx.x >> 6;
+  __shared__ float redk[4];
+  if ((threadIdx.x & 63) == 0) { red[wave] = ssq; redk[wave] = ssk; }
+  __syncthreads();
+  const float tq = add_rn(add_rn(red[0], red[1]), add_rn(red[2], red[3]));
+  const float tk = add_rn(add_rn(redk[0], redk[1]), add_rn(redk[2], redk[3]));
+  const float invq = rsqrtf(add_rn(mul_rn(tq, 1.0f / (float)(Hq * D)), eps));
+  const float invk = rsqrtf(add_rn(mul_rn(tk, 1.0f / (float)(Hkv * D)), eps));
+#pragma unroll
+  for (int i = 0; i < kRopeUPT; ++i) {
+    const int u = threadIdx.x + 256 * i;
+    if (u < uq + uk) {
+      const bool isq = u < uq;
+      const int uu = isq ? u : u - uq;
+      const int h = uu / upr, d0 = (uu % upr) * 8;
+      const float* wt = (isq ? qw : kw) + h * D;
+      const float inv = isq ? invq : invk;
+      float y1[8], y2[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        // norm output rounded to bf16 (the norm returns the input dtype)
+        const float x1 = bf16_to_f32(f32_to_bf16(mul_rn(mul_rn(wt[d0 + e], a[i][e]), inv)));
+        const float x2 = bf16_to_f32(f32_to_bf16(mul_rn(mul_rn(wt[half + d0 + e], b[i][e]), inv)));
+        const float c = cs[d0 + e], s = cs[half + d0 + e];
+        y1[e] = sub_rn(mul_rn(x1, c), mul_rn(x2, s));
+        y2[e] = add_rn(mul_rn(x2, c), mul_rn(x1, s));
+      }
+      uint4 o1, o2;
+      o1.x = pack_bf16x2(y1[0], y1[1]); o1.y = pack_bf16x2(y1[2], y1[3]);
+      o1.z = pack_bf16x2(y1[4], y1[5]); o1.w = pack_bf16x2(y1[6], y1[7]);
+      o2.x = pack_bf16x2(y2[0], y2[1]); o2.y = pack_bf16x2(y2[2], y2[3]);
+      o2.z = pack_bf16x2(y2[4], y2[5]); o2.w = pack_bf16x2(y2[6], y2[7]);
+      uint16_t* dst;
+      if (isq) {
+        dst = q_out + (t * Hq + h) * D;
+      } else {
+        if (!store) continue;
+        dst = kc + (slot * Hkv + h) * D;
+      }
+      *reinterpret_cast<uint4*>(dst + d0) = o1;
+      *reinterpret_cast<uint4*>(dst + half + d0) = o2;
+    }
+  }
+}
+
+// --------------------------------------------------------------- moe_route --
+// One workgroup of 4 waves per token.  Wave w computes the gate logits of
+// experts w, w+4, ... (lane l sums chunks l, l+64, ... then a butterfly);
+// wave 0 picks the top k; all 256 threads form the routed bias.
+constexpr int kMaxExperts = 64;
+
+__global__ __launch_bounds__(256) void moe_route_kernel(
+    const uint16_t* __restrict__ h, const uint16_t* __restrict__ gw, const float* __restrict__ ebias,
+    const float* __restrict__ b2, float* __restrict__ dense, float* __restrict__ bias_out, int d,
+    int E, int S, int top_k) {
+  __shared__ float logits[kMaxExperts];
+  __shared__ float wsel[kMaxExperts];
+  const int64_t t = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int cpr = d / 8;
+  for (int e = wave; e < E; e += 4) {
+    float acc = 0.f;
+    for (int c = lane; c < cpr; c += 64) {
+      float hv[8], gv[8];
+      unpack8(*reinterpret_cast<const uint4*>(h + t * d + c * 8), hv);
+      unpack8(*reinterpret_cast<const uint4*>(gw + (int64_t)e * d + c * 8), gv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc = add_rn(acc, mul_rn(hv[i], gv[i]));
+    }
+    acc = group_sum<64>(acc);
+    if (lane == 0) logits[e] = acc;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const bool valid = lane < E;
+    const float logit = valid ? logits[lane] : 0.f;
+    // sigmoid score and biased logit of expert `lane`
+    const float score = valid ? 1.0f / (1.0f + expf(-logit)) : 0.f;
+    const float key = valid ? add_rn(logit, ebias[lane]) : -INFINITY;
+    // top-k by repeated wave argmax (ties: lowest expert index)
+    bool chosen = false;
+    float wsum = 0.f;
+    for (int k = 0; k < top_k; ++k) {
+      float best = chosen ? -INFINITY : key;
+      int bi = valid && !chosen ? lane : kMaxExperts;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const float ob = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (ob > best || (ob == best && oi < bi)) { best = ob; bi = oi; }
+      }
+      if (lane == bi) chosen = true;
+      wsum = add_rn(wsum, __shfl(score, bi < 64 ? bi : 0, 64) * (bi < 64 ? 1.f : 0.f));
+    }
+    float wgt = chosen ? score : 0.f;
+    if (top_k > 1) wgt = chosen ? wgt / add_rn(wsum, 1e-10f) : 0.f;
+    if (lane < E + S) {
+      const float v = lane < E ? wgt : 1.0f;
+      dense[t * (E + S) + lane] = v;
+      wsel[lane] = v;
+    }
+  }
+  __syncthreads();
+  // routed bias: sum_e w[e] * b2[e, n], experts in index order
+  for (int n = threadIdx.x; n < d; n += 256) {
+    float acc = 0.f;
+    for (int e = 0; e < E + S; ++e) acc = add_rn(acc, mul_rn(wsel[e], b2[(int64_t)e * d + n]));
+    bias_out[t * d + n] = acc;
+  }
+}
+
+// ------------------------------------------------------------ swiglu_quant --
+// One wave per (token, expert), workgroup index t * E + e; lane l handles
+// chunks l, l+64, ... of the expert's F outputs (a 128 group = 16
+// consecutive lanes).
+__global__ __launch_bounds__(64) void swiglu_quant_kernel(
+    const uint16_t* __restrict__ h13, const float* __restrict__ route, uint8_t* __restrict__ q,
+    float* __restrict__ qs, int E, int F) {
+  const int64_t t = blockIdx.x / E;
+  const int e = (int)(blockIdx.x - t * E);
+  const int lane = threadIdx.x;
+  const uint16_t* a = h13 + (t * E + e) * 2 * (int64_t)F;
+  const uint16_t* b = a + F;
+  const float r = route[t * E + e];
+  const int64_t orow = t * (int64_t)E * F + (int64_t)e * F;
+  for (int c = lane; c < F / 8; c += 64) {
+    float av[8], bv[8], g[8];
+    unpack8(*reinterpret_cast<const uint4*>(a + c * 8), av);
+    unpack8(*reinterpret_cast<const uint4*>(b + c * 8), bv);
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float sl = bf16_to_f32(f32_to_bf16(av[i] / add_rn(1.0f, expf(-av[i]))));
+      g[i] = bf16_to_f32(f32_to_bf16(mul_rn(sl, bv[i])));
+      amax = fmaxf(amax, fabsf(g[i]));
+    }
+    amax = group_max<16>(amax);
+    const float sc = scale_from_amax(amax, false);
+    *reinterpret_cast<uint2*>(q + orow + c * 8) = quant8(g, sc);
+    if ((c & 15) == 0) qs[(orow + c * 8) / 128] = mul_rn(sc, r);
+  }
+}
+
+template <int CPT>
+int launch_add_rmsnorm(bool quant, const void* x, const void* residual, const float* w, void* out,
+                       void* res_out, void* q, float* qs, int64_t T, int d, float eps,
+                       hipStream_t st) {
+  if (quant)
+    hipLaunchKernelGGL((add_rmsnorm_kernel<CPT, true>), dim3((unsigned)T), dim3(128), 0, st,
+                       (const uint16_t*)x, (const uint16_t*)residual, w, (uint16_t*)out,
+                       (uint16_t*)res_out, (uint8_t*)q, qs, d, eps);
+  else
+    hipLaunchKernelGGL((add_rmsnorm_kernel<CPT, false>), dim3((unsigned)T), dim3(128), 0, st,
+                       (const uint16_t*)x, (const uint16_t*)residual, w, (uint16_t*)out,
+                       (uint16_t*)res_out, (uint8_t*)q, qs, d, eps);
+  return check_launch("add_rmsnorm");
+}
+
+}  // namespace
+}  // namespace lfs
+
+using namespace lfs;
+
+extern "C" int lfs_add_rmsnorm(const void* x, const void* residual, const float* weight, void* out,
+                               void* residual_out, void* q, float* q_scale, int64_t T, int32_t d,
+                               float eps, void* stream) {
+  LFS_REQUIRE(T >= 0 && d > 0, "add_rmsnorm: bad shape");
+  LFS_REQUIRE(d % 8 == 0 && d <= 128 * 8 * 8, "add_rmsnorm: d=%d must be a multiple of 8 and <= 8192", d);
+  LFS_REQUIRE((residual == nullptr) == (residual_out == nullptr),
+              "add_rmsnorm: residual and residual_out go together");
+  LFS_REQUIRE((q == nullptr) == (q_scale == nullptr), "add_rmsnorm: q and q_scale go together");
+  LFS_REQUIRE(q == nullptr || d % 128 == 0, "add_rmsnorm: quantised output needs d %% 128 == 0");
+  LFS_REQUIRE(out != nullptr || q != nullptr, "add_rmsnorm: no output");
+  if (T == 0) return 0;
+  LFS_REQUIRE(x && weight, "add_rmsnorm: null pointer");
+  LFS_REQUIRE(((uintptr_t)x | (uintptr_t)residual | (uintptr_t)out | (uintptr_t)residual_out |
+               (uintptr_t)weight | (uintptr_t)q) % 16 == 0,
+              "add_rmsnorm: buffers must be 16-byte aligned");
+  LFS_REQUIRE(T < (1ll << 31), "add_rmsnorm: too many rows");
+  hipStream_t st = (hipStream_t)stream;
+  const int cpr = d / 8;
+  const bool quant = q != nullptr;
+  if (cpr <= 128) return launch_add_rmsnorm<1>(quant, x, residual, weight, out, residual_out, q, q_scale, T, d, eps, st);
+  if (cpr <= 256) return launch_add_rmsnorm<2>(quant, x, residual, weight, out, residual_out, q, q_scale, T, d, eps, st);
+  if (cpr <= 512) return launch_add_rmsnorm<4>(quant, x, residual, weight, out, residual_out, q, q_scale, T, d, eps, st);
+  return launch_add_rmsnorm<8>(quant, x, residual, weight, out, residual_out, q, q_scale, T, d, eps, st);
+}
+
+extern "C" int lfs_qk_norm_rope_store(const void* qkv, int64_t ld, const float* q_weight,
+                                      const float* k_weight, const float* cos_sin,
+                                      const int64_t* positions, const int64_t* slot_mapping,
+                                      void* q_out, void* k_cache, void* v_cache, int64_t T,
+                                      int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                      int64_t num_slots, int64_t max_positions, float eps,
+                                      void* stream) {
+  const int Hq = num_q_heads, Hkv = num_kv_heads, D = head_dim;
+  LFS_REQUIRE(T >= 0 && Hq > 0 && Hkv > 0, "qk_norm_rope_store: bad shape");
+  LFS_REQUIRE(D % 16 == 0 && D > 0 && D <= 512, "qk_norm_rope_store: head_dim=%d must be a multiple of 16", D);
+  LFS_REQUIRE((int64_t)(Hq + Hkv) * D / 16 <= 256 * kRopeUPT,
+              "qk_norm_rope_store: (Hq+Hkv)*D/16 must be <= %d", 256 * kRopeUPT);
+  LFS_REQUIRE(ld >= (int64_t)(Hq + 2 * Hkv) * D && ld % 8 == 0, "qk_norm_rope_store: bad row stride");
+  LFS_REQUIRE(max_positions > 0, "qk_norm_rope_store: empty RoPE table");
+  if (T == 0) return 0;
+  LFS_REQUIRE(qkv && q_weight && k_weight && cos_sin && positions && q_out,
+              "qk_norm_rope_store: null pointer");
+  LFS_REQUIRE(slot_mapping == nullptr || (k_cache && v_cache), "qk_norm_rope_store: null cache");
+  LFS_REQUIRE(((uintptr_t)qkv | (uintptr_t)q_out | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16 == 0,
+              "qk_norm_rope_store: buffers must be 16-byte aligned");
+  hipLaunchKernelGGL(qk_norm_rope_store_kernel, dim3((unsigned)T), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)qkv, ld, q_weight, k_weight, cos_sin, positions, slot_mapping,
+                     (uint16_t*)q_out, (uint16_t*)k_cache, (uint16_t*)v_cache, Hq, Hkv, D, num_slots,
+                     max_positions, eps);
+  return check_launch("qk_norm_rope_store");
+}
+
+extern "C" int lfs_moe_route(const void* h, const void* gate_weight, const float* expert_bias,
+                             const float* down_bias, float* dense_weights, float* bias_out, int64_t T,
+                             int32_t d, int32_t num_experts, int32_t num_shared, int32_t top_k,
+                             void* stream) {
+  LFS_REQUIRE(T >= 0 && d > 0 && d % 8 == 0, "moe_route: d=%d must be a positive multiple of 8", d);
+  LFS_REQUIRE(num_experts > 0 && num_shared >= 0 && num_experts + num_shared <= kMaxExperts,
+              "moe_route: at most %d experts", kMaxExperts);
+  LFS_REQUIRE(top_k >= 1 && top_k <= num_experts, "moe_route: bad top_k");
+  if (T == 0) return 0;
+  LFS_REQUIRE(h && gate_weight && expert_bias && down_bias && dense_weights && bias_out,
+              "moe_route: null pointer");
+  LFS_REQUIRE(((uintptr_t)h | (uintptr_t)gate_weight) % 16 == 0, "moe_route: h and gate_weight must be 16-byte aligned");
+  hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)T), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)h, (const uint16_t*)gate_weight, expert_bias, down_bias,
+                     dense_weights, bias_out, d, num_experts, num_shared, top_k);
+  return check_launch("moe_route");
+}
+
+extern "C" int lfs_swiglu_quant(const void* h13, const float* route_weights, void* q, float* q_scale,
+                                int64_t T, int32_t num_experts, int32_t d_ff, void* stream) {
+  LFS_REQUIRE(T >= 0 && num_experts > 0, "swiglu_quant: bad shape");
+  LFS_REQUIRE(d_ff > 0 && d_ff % 128 == 0, "swiglu_quant: d_ff=%d must be a multiple of 128", d_ff);
+  if (T == 0) return 0;
+  LFS_REQUIRE(h13 && route_weights && q && q_scale, "swiglu_quant: null pointer");
+  LFS_REQUIRE(((uintptr_t)h13 | (uintptr_t)q) % 16 == 0, "swiglu_quant: buffers must be 16-byte aligned");
+  LFS_REQUIRE(T * num_experts < (1ll << 31), "swiglu_quant: too many rows");
+  hipLaunchKernelGGL(swiglu_quant_kernel, dim3((unsigned)(T * num_experts)), dim3(64), 0,
+                     (hipStream_t)stream, (const uint16_t*)h13, route_weights, (uint8_t*)q, q_scale,
+                     num_experts, d_ff);
+  return check_launch("swiglu_quant");
+}

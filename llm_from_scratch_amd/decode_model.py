@@ -18,6 +18,12 @@ Interface (nano-vLLM style, as the runner expects):
     hidden = model(input_ids [T], positions [T])      # bf16 [T, d_model]
     logits = model.compute_logits(hidden)             # bf16 [T, vocab]
 
+Kernels per layer: add_rmsnorm (+act_quant) -> qkv FP8 GEMM ->
+qk_norm_rope_store -> paged decode (split + merge) -> act_quant -> output
+FP8 GEMM -> add_rmsnorm (+act_quant) -> moe_route -> gate/up FP8 GEMM ->
+swiglu_quant -> down FP8 GEMM.  Setting ``model.trace = {}`` makes an
+eager forward record every intermediate (per layer) for parity tests.
+
 MoE in the decode step: every expert runs over the whole batch and is
 weighted by the routing weight (0 for experts a token did not pick).  Each
 output row depends only on its own input row (act_quant is per row, the
@@ -25,7 +31,7 @@ GEMM rows are independent), so this equals the reference's per-expert
 gather/scatter (moe_infer, moe.py:288-341) while needing no host sync --
 the decode step can be captured in a HIP graph -- and, since a batch of
 decode tokens touches every expert anyway, it streams the same weight
-bytes.  Expert outputs are accumulated in fp32 and rounded once.
+bytes.  All experts together take two FP8 GEMMs (see MoE).
 """
 from __future__ import annotations
 
@@ -68,38 +74,30 @@ class DecodeModelConfig:
 
 
 class RMSNorm(nn.Module):
-    """model/utils.py:44-67: fp32 compute, optional fused residual add."""
+    """model/utils.py:44-67: fp32 compute, optional fused residual add; runs
+    as one add_rmsnorm launch (optionally also quantising its output)."""
 
     def __init__(self, d: int, eps: float = 1e-5, device=None):
         super().__init__()
         self.eps = eps
         self.weight = nn.Parameter(torch.ones(d, dtype=torch.float32, device=device))
 
-    def forward(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None):
-        dtype = x.dtype
-        if residual is None:
-            x = x.float()
-            return (self.weight * x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.eps)).to(dtype)
-        x = x.float().add_(residual.float())
-        residual = x
-        out = self.weight * x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.eps)
-        return out.to(dtype), residual.to(dtype)
+    def forward(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None, out: bool = True,
+                quant: bool = False):
+        """-> (out, residual_out, q, q_scale); residual_out is x without a
+        residual (the reference returns (norm(x), x) in that case)."""
+        return kernels.add_rmsnorm(x, self.weight, self.eps, residual, out=out, quant=quant)
 
 
 class Rotary(nn.Module):
-    """Half-split RoPE with a cat(cos, sin) table (model/attention/utils.py:18-45)."""
+    """Half-split RoPE table cat(cos, sin) [max_seq_len, D]
+    (model/attention/utils.py:18-31); applied inside qk_norm_rope_store."""
 
     def __init__(self, theta: float, d_k: int, max_seq_len: int, device=None):
         super().__init__()
         inv_freq = 1.0 / (theta ** (torch.arange(0, d_k, 2, device=device).float() / d_k))
         ang = torch.outer(torch.arange(max_seq_len, device=device).float(), inv_freq)
         self.register_buffer("cos_sin_cached", torch.cat([ang.cos(), ang.sin()], -1), persistent=False)
-
-    def forward(self, x: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
-        # x [T, H, D], positions [T]
-        cos, sin = self.cos_sin_cached[positions].unsqueeze(1).chunk(2, dim=-1)
-        x1, x2 = x.float().chunk(2, dim=-1)
-        return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1)
 
 
 class PagedGQAAttention(nn.Module):
@@ -108,9 +106,12 @@ class PagedGQAAttention(nn.Module):
         d, D = cfg.d_model, cfg.head_dim
         self.num_heads, self.num_kv_heads, self.head_dim = cfg.num_heads, cfg.num_kv_heads, D
         self.scale = 1.0 / math.sqrt(D)
-        self.q_proj = FP8Linear(d, d, device=device)
-        self.k_proj = FP8Linear(d, cfg.num_kv_heads * D, device=device)
-        self.v_proj = FP8Linear(d, cfg.num_kv_heads * D, device=device)
+        # q_proj, k_proj and v_proj (GQA.py:34-36) as one FP8 linear: their
+        # row blocks start at multiples of 128, so quantising the stacked
+        # weight gives the same codes and scales as quantising each one, and
+        # every output column of the GEMM is independent of the others
+        self.q_dim, self.kv_dim = d, cfg.num_kv_heads * D
+        self.qkv_proj = FP8Linear(d, d + 2 * self.kv_dim, device=device)
         self.output_proj = FP8Linear(d, d, device=device)
         # torch.nn.RMSNorm default eps (machine epsilon of the fp32 compute)
         self.q_norm = RMSNorm(d, eps=torch.finfo(torch.float32).eps, device=device)
@@ -119,26 +120,30 @@ class PagedGQAAttention(nn.Module):
         self.k_cache = torch.empty(0)  # pool views attached by the model runner
         self.v_cache = torch.empty(0)
 
-    def qkv(self, x: torch.Tensor, positions: torch.Tensor):
-        T = x.size(0)
-        q = self.q_norm(self.q_proj(x)).view(T, self.num_heads, self.head_dim)
-        k = self.k_norm(self.k_proj(x)).view(T, self.num_kv_heads, self.head_dim)
-        v = self.v_proj(x).view(T, self.num_kv_heads, self.head_dim)
-        q = self.rope(q, positions).to(torch.bfloat16)
-        k = self.rope(k, positions).to(torch.bfloat16)
-        return q, k, v
-
-    def forward(self, x: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
+    def forward(self, xq: torch.Tensor, xs: torch.Tensor, positions: torch.Tensor,
+                trace: Optional[dict] = None) -> torch.Tensor:
+        """xq, xs: the attention input already quantised (act_quant codes and
+        1x128 scales of the att_norm output)."""
         ctx = get_context()
-        q, k, v = self.qkv(x, positions)
-        if self.k_cache.numel():
-            kernels.store_kvcache(k, v, self.k_cache, self.v_cache, ctx.slot_mapping)
+        T = xq.size(0)
+        assert self.k_cache.numel(), "PagedGQAAttention needs the KV pool (ModelRunner.allocate_kv_cache)"
+        qkv = self.qkv_proj.gemm(xq, xs)
+        q = kernels.qk_norm_rope_store(qkv, self.q_norm.weight, self.k_norm.weight, self.rope.cos_sin_cached,
+                                       positions, self.num_heads, self.num_kv_heads, self.q_norm.eps,
+                                       self.k_cache, self.v_cache, ctx.slot_mapping)
         if ctx.is_prefill:
+            flat = (-1, self.num_kv_heads, self.head_dim)
+            k = self.k_cache.view(flat)[ctx.slot_mapping]
+            v = self.v_cache.view(flat)[ctx.slot_mapping]
             o = self._prefill_attention(q, k, v, ctx)
         else:
-            o = kernels.paged_attention_decode(q.contiguous(), self.k_cache, self.v_cache,
-                                               ctx.context_lens, ctx.block_tables, self.scale)
-        return self.output_proj(o.reshape(x.size(0), -1))
+            o = kernels.paged_attention_decode(q, self.k_cache, self.v_cache, ctx.context_lens,
+                                               ctx.block_tables, self.scale)
+        o = o.reshape(T, -1)
+        out = self.output_proj(o)
+        if trace is not None:
+            trace.update(qkv=qkv, q=q, att_o=o, att_out=out)
+        return out
 
     def _prefill_attention(self, q, k, v, ctx) -> torch.Tensor:
         """Causal attention of each prompt over its full context (cached
@@ -147,7 +152,7 @@ class PagedGQAAttention(nn.Module):
         cu_q = ctx.cu_seqlens_q.tolist()
         cu_k = ctx.cu_seqlens_k.tolist()
         out = torch.empty_like(q)
-        BS = self.k_cache.size(1) if self.k_cache.numel() else 1
+        BS = self.k_cache.size(1)
         for i in range(len(cu_q) - 1):
             qs, qe, lk = cu_q[i], cu_q[i + 1], cu_k[i + 1] - cu_k[i]
             lq = qe - qs
@@ -169,49 +174,64 @@ class PagedGQAAttention(nn.Module):
         return out
 
 
-class MLP(nn.Module):
-    """SwiGLU: w2(silu(w1 x) * w3 x) (model/architecture/mlp.py:48-67)."""
-
-    def __init__(self, d: int, d_ff: int, device=None):
-        super().__init__()
-        self.w1 = FP8Linear(d, d_ff, device=device)
-        self.w3 = FP8Linear(d, d_ff, device=device)
-        self.w2 = FP8Linear(d_ff, d, device=device)
-
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return self.w2(torch.nn.functional.silu(self.w1(x)) * self.w3(x))
-
-
 class MoE(nn.Module):
+    """Routed experts + one shared expert (model/architecture/moe.py:160-260),
+    each a SwiGLU MLP w2(silu(w1 x) * w3 x) with biases
+    (model/architecture/mlp.py:48-67), computed densely over experts:
+      * moe_route: sigmoid gate, top-k of the biased logits, renormalised
+        weights as a dense [T, E+1] matrix (shared expert 1, unpicked 0) and
+        the bias matrix sum_e w_e * b2_e;
+      * one FP8 GEMM with every expert's w1 and w3 stacked along N (rows
+        [e][w1 | w3], blocks aligned to 128, so the codes and scales equal
+        per-expert quantisation);
+      * swiglu_quant: SwiGLU in bf16 as the reference rounds it, act_quant of
+        all the experts' hidden rows at once (128-groups never straddle
+        experts, d_ff % 128 == 0), each group's scale multiplied by the
+        token's routing weight for that expert;
+      * one FP8 GEMM with every expert's w2 stacked along K, so the fp32
+        accumulator sums sum_e w_e * (w2_e h_e) directly, plus the bias
+        matrix.
+    The reference rounds each expert's output to bf16 and scatter-adds in
+    bf16 (moe.py:288-341); here the weighted sum is rounded once."""
+
     def __init__(self, cfg: DecodeModelConfig, device=None):
         super().__init__()
         self.top_k = cfg.num_experts_per_tok
         self.n_experts = cfg.n_routed_experts
+        self.n_shared = 1 if cfg.n_shared_experts > 0 else 0
+        self.d_ff = cfg.d_ff
+        assert cfg.d_ff % 128 == 0, "d_ff must be a multiple of 128"
+        E = self.n_experts + self.n_shared
         self.gate_weight = nn.Parameter(torch.empty(cfg.n_routed_experts, cfg.d_model, device=device,
                                                     dtype=torch.bfloat16))
         self.register_buffer("expert_bias", torch.zeros(cfg.n_routed_experts, device=device))
-        self.experts = nn.ModuleList([MLP(cfg.d_model, cfg.d_ff, device) for _ in range(cfg.n_routed_experts)])
-        self.shared_expert = MLP(cfg.d_model, cfg.d_ff, device) if cfg.n_shared_experts > 0 else None
+        self.w13 = FP8Linear(cfg.d_model, E * 2 * cfg.d_ff, device=device)
+        self.w2 = FP8Linear(E * cfg.d_ff, cfg.d_model, bias=False, device=device)
+        self.register_buffer("w2_bias", torch.zeros(E, cfg.d_model, device=device))
 
-    def route(self, x: torch.Tensor):
-        """Gate (moe.py:45-90): sigmoid scores, top-k of the biased logits,
-        weights renormalised over the chosen experts; dense [T, E] weights."""
-        logits = x.float() @ self.gate_weight.float().t()
-        scores = torch.sigmoid(logits)
-        idx = torch.topk(logits + self.expert_bias, self.top_k, dim=-1, sorted=False).indices
-        w = torch.gather(scores, -1, idx)
-        if self.top_k > 1:
-            w = w / (w.sum(-1, keepdim=True) + 1e-10)
-        return torch.zeros_like(scores).scatter_(1, idx, w), idx
+    @torch.no_grad()
+    def load_experts(self, experts: list[tuple]) -> None:
+        """experts: (w1 [F, d], b1, w3 [F, d], b3, w2 [d, F], b2) per routed
+        expert, then the shared expert."""
+        w13 = torch.cat([torch.cat([w1, w3]) for w1, _, w3, _, _, _ in experts])
+        b13 = torch.cat([torch.cat([b1, b3]) for _, b1, _, b3, _, _ in experts])
+        self.w13.load_weight(w13, b13)
+        self.w2.load_weight(torch.cat([e[4] for e in experts], dim=1))
+        self.w2_bias.copy_(torch.stack([e[5] for e in experts]).float())
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        dense_w, _ = self.route(x)
-        y = torch.zeros(x.shape, dtype=torch.float32, device=x.device)
-        for e, expert in enumerate(self.experts):
-            y += dense_w[:, e:e + 1] * expert(x).float()
-        if self.shared_expert is not None:
-            y += self.shared_expert(x).float()
-        return y.to(x.dtype)
+    def forward(self, h: torch.Tensor, hq: torch.Tensor, hs: torch.Tensor,
+                trace: Optional[dict] = None) -> torch.Tensor:
+        """h: the ffn_norm output (bf16, for the gate); hq, hs: the same
+        quantised (for the experts)."""
+        T, F = h.size(0), self.d_ff
+        w, bias = kernels.moe_route(h, self.gate_weight, self.expert_bias, self.w2_bias, self.top_k,
+                                    self.n_shared)
+        h13 = self.w13.gemm(hq, hs)
+        gq, gs = kernels.swiglu_quant(h13.view(T, -1, 2, F), w)
+        y = kernels.fp8_gemm(gq, gs, self.w2.weight, self.w2.weight_scale, bias)
+        if trace is not None:
+            trace.update(route_w=w, route_bias=bias, h13=h13, ffn_out=y)
+        return y
 
 
 class Block(nn.Module):
@@ -222,14 +242,17 @@ class Block(nn.Module):
         self.att_norm = RMSNorm(cfg.d_model, cfg.rms_eps, device)
         self.ffn_norm = RMSNorm(cfg.d_model, cfg.rms_eps, device)
 
-    def forward(self, x, residual, positions):
-        if residual is None:
-            x, residual = self.att_norm(x), x
-        else:
-            x, residual = self.att_norm(x, residual)
-        x = self.att(x, positions)
-        x, residual = self.ffn_norm(x, residual)
-        return self.ffn(x), residual
+    def forward(self, x, residual, positions, trace: Optional[dict] = None):
+        """Fused add & norm before attention and before the MoE
+        (model/transformer.py:90-118)."""
+        if trace is not None:
+            trace.update(x=x, residual=residual)
+        h, residual, hq, hs = self.att_norm(x, residual, out=trace is not None, quant=True)
+        x = self.att(hq, hs, positions, trace)
+        h2, residual, hq, hs = self.ffn_norm(x, residual, out=True, quant=True)
+        if trace is not None:
+            trace.update(att_h=h, ffn_h=h2, res_mid=residual)
+        return self.ffn(h2, hq, hs, trace), residual
 
 
 class DecodeModel(nn.Module):
@@ -241,12 +264,13 @@ class DecodeModel(nn.Module):
         self.layers = nn.ModuleList([Block(cfg, self.rope, device) for _ in range(cfg.num_layers)])
         self.final_norm = RMSNorm(cfg.d_model, cfg.rms_eps, device)
         self.lm_head = FP8Linear(cfg.d_model, cfg.vocab_size, device=device)
+        self.trace: Optional[dict] = None
         self.init_weights(seed)
 
     @torch.no_grad()
     def init_weights(self, seed: int) -> None:
         """nn.Linear's default init (uniform +-1/sqrt(fan_in) for weight and
-        bias), truncated-normal embedding, from one seeded generator."""
+        bias), clamped-normal embedding, from one seeded generator."""
         g = torch.Generator(device=self.embed.device)
         g.manual_seed(seed)
         dev = self.embed.device
@@ -255,21 +279,33 @@ class DecodeModel(nn.Module):
             return (torch.rand(shape, generator=g, device=dev) * 2 - 1) * bound
 
         self.embed.copy_(torch.randn(self.embed.shape, generator=g, device=dev).clamp_(-3, 3))
+        experts = {id(lin) for layer in self.layers for lin in (layer.ffn.w13, layer.ffn.w2)}
         for m in self.modules():
-            if isinstance(m, FP8Linear):
+            if isinstance(m, MoE):
+                m.gate_weight.copy_(uniform(m.gate_weight.shape, 1.0 / math.sqrt(m.gate_weight.shape[1])))
+                d, F = m.gate_weight.shape[1], m.d_ff
+                bd, bf = 1.0 / math.sqrt(d), 1.0 / math.sqrt(F)
+                m.load_experts([(uniform((F, d), bd), uniform((F,), bd), uniform((F, d), bd), uniform((F,), bd),
+                                 uniform((d, F), bf), uniform((d,), bf))
+                                for _ in range(m.n_experts + m.n_shared)])
+            elif isinstance(m, FP8Linear) and id(m) not in experts:
                 b = 1.0 / math.sqrt(m.in_features)
                 m.load_weight(uniform((m.out_features, m.in_features), b),
                               uniform((m.out_features,), b) if m.bias is not None else None)
-            elif isinstance(m, MoE):
-                m.gate_weight.copy_(uniform(m.gate_weight.shape, 1.0 / math.sqrt(m.gate_weight.shape[1])))
 
     def forward(self, input_ids: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
         x = self.embed[input_ids]
         residual = None
-        for layer in self.layers:
-            x, residual = layer(x, residual, positions)
-        x, _ = self.final_norm(x, residual)
-        return x
+        tr = self.trace
+        for i, layer in enumerate(self.layers):
+            x, residual = layer(x, residual, positions, None if tr is None else tr.setdefault(i, {}))
+        h, _, _, _ = self.final_norm(x, residual)
+        if tr is not None:
+            tr["final"] = dict(x=x, residual=residual, h=h)
+        return h
 
     def compute_logits(self, hidden: torch.Tensor) -> torch.Tensor:
-        return self.lm_head(hidden)
+        logits = self.lm_head(hidden)
+        if self.trace is not None:
+            self.trace["final"].update(head_in=hidden, logits=logits)
+        return logits

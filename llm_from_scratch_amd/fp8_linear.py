@@ -60,6 +60,11 @@ class FP8Linear(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         x = x.to(torch.bfloat16).contiguous()
         xq, xs = kernels.act_quant(x, 128)
+        return self.gemm(xq, xs)
+
+    def gemm(self, xq: torch.Tensor, xs: torch.Tensor) -> torch.Tensor:
+        """The linear on an input already quantised by act_quant (codes and
+        1x128 scales), e.g. by a fused norm."""
         return kernels.fp8_gemm(xq, xs, self.weight, self.weight_scale, self.bias)
 
     def extra_repr(self) -> str:

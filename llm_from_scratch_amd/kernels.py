@@ -113,14 +113,30 @@ def weight_dequant(x: torch.Tensor, s: torch.Tensor, block_size: int = 128) -> t
     return y
 
 
+def default_gemm_splits(M: int, N: int, K: int) -> int:
+    """K splits for fp8_gemm: 1 when the 128x128 output tiles alone give
+    >= 192 workgroups; otherwise enough splits to reach ~256 workgroups,
+    keeping >= 2 K blocks per split and the fp32 partials <= 8 MB."""
+    tiles = -(-M // 128) * -(-N // 128)
+    kt = K // 128
+    if tiles >= 192 or kt < 4:
+        return 1
+    splits = min(kt // 2, max(1, 256 // tiles), max(1, (8 << 20) // max(1, 4 * M * N)))
+    return max(1, splits)
+
+
 def fp8_gemm(a: torch.Tensor, a_s: torch.Tensor, b: torch.Tensor, b_s: torch.Tensor,
-             bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+             bias: Optional[torch.Tensor] = None, splits: Optional[int] = None) -> torch.Tensor:
     """c = a @ b^T with 1x128 activation scales and 128x128 weight scales.
 
     a: e4m3fn [..., K], a_s: fp32 [..., K/128]; b: e4m3fn [N, K] (nn.Linear
-    weight layout), b_s: fp32 [ceil(N/128), K/128]; bias: fp32 [N] or None.
+    weight layout), b_s: fp32 [ceil(N/128), K/128]; bias: None, fp32 [N], or
+    an fp32 per-row bias matrix [..., N] (rows with unit stride in N).
     The scale products are applied to each 128-wide K-block partial in an
-    fp32 accumulator; the result is rounded once to bf16 [..., N].
+    fp32 accumulator, the bias is added in fp32, and the result is rounded
+    once to bf16 [..., N].  ``splits`` > 1 splits the K blocks over that many
+    workgroups per output tile (fp32 partials, then one reduction); by
+    default only small-M shapes that cannot fill the GPU are split.
     """
     assert a.is_contiguous() and b.is_contiguous(), "Input tensors must be contiguous"
     assert a_s.is_contiguous() and b_s.is_contiguous(), "Scaling factor tensors must be contiguous"
@@ -136,13 +152,28 @@ def fp8_gemm(a: torch.Tensor, a_s: torch.Tensor, b: torch.Tensor, b_s: torch.Ten
     assert K % 128 == 0, "K must be a multiple of 128"
     assert a_s.shape == (*a.shape[:-1], K // 128), "a_s must be [..., K/128]"
     assert b_s.shape == (math.ceil(N / 128), K // 128), "b_s must be [ceil(N/128), K/128]"
+    bias_ld = 0
     if bias is not None:
         _on_gpu(a, bias)
         _dtype(bias, torch.float32, "bias")
-        assert bias.is_contiguous() and bias.shape == (N,), "bias must be fp32 [N]"
+        if bias.dim() == 1:
+            assert bias.is_contiguous() and bias.shape == (N,), "bias must be fp32 [N]"
+        else:
+            bias = bias.reshape(-1, bias.size(-1)) if bias.dim() > 2 else bias
+            assert bias.shape == (M, N) and bias.stride(1) == 1, "bias matrix must be fp32 [..., N]"
+            bias_ld = bias.stride(0) if M > 1 else N
     c = a.new_empty(*a.shape[:-1], N, dtype=torch.bfloat16)
-    rc = _lib.load().lfs_fp8_gemm(_ptr(a), _ptr(a_s), _ptr(b), _ptr(b_s), _ptr(bias), _ptr(c),
-                                  M, N, K, _stream(a))
+    if splits is None:
+        splits = default_gemm_splits(M, N, K)
+    L = _lib.load()
+    need = int(L.lfs_fp8_gemm_workspace_bytes(M, N, K, splits)) if splits > 1 else 0
+    if need:
+        ws = torch.empty(need // 4, dtype=torch.float32, device=a.device)
+        rc = L.lfs_fp8_gemm_splitk(_ptr(a), _ptr(a_s), _ptr(b), _ptr(b_s), _ptr(bias), bias_ld, _ptr(c),
+                                   M, N, K, splits, _ptr(ws), need, _stream(a))
+    else:
+        rc = L.lfs_fp8_gemm(_ptr(a), _ptr(a_s), _ptr(b), _ptr(b_s), _ptr(bias), bias_ld, _ptr(c),
+                            M, N, K, _stream(a))
     _lib.check(rc, "fp8_gemm")
     return c
 
@@ -238,3 +269,129 @@ def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
                                       _stream(q))
     _lib.check(rc, "paged_attention_decode")
     return o
+
+
+# ------------------------------------------------- fused decode-step rows --
+def add_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+                residual: Optional[torch.Tensor] = None, out: bool = True, quant: bool = False):
+    """RMSNorm with fused residual add (model/utils.py:53-67) in one launch.
+
+    x (and residual): bf16 [T, d] contiguous; weight fp32 [d].  Returns
+    (out, residual_out, q, q_scale): out = bf16(weight * r * rsqrt(mean(r^2)
+    + eps)) with r = x (+ residual); residual_out = bf16(r) when a residual
+    is given, else x; q, q_scale = act_quant(out, 128) when ``quant``.
+    """
+    assert x.dim() == 2 and x.is_contiguous(), "x must be contiguous [T, d]"
+    T, d = x.shape
+    _on_gpu(x, weight)
+    _dtype(x, torch.bfloat16, "x")
+    _dtype(weight, torch.float32, "weight")
+    assert weight.is_contiguous() and weight.shape == (d,)
+    res_out = None
+    if residual is not None:
+        _on_gpu(x, residual)
+        _dtype(residual, torch.bfloat16, "residual")
+        assert residual.shape == x.shape and residual.is_contiguous()
+        res_out = torch.empty_like(x)
+    y = torch.empty_like(x) if out else None
+    q = qs = None
+    if quant:
+        q = torch.empty(T, d, dtype=FP8, device=x.device)
+        qs = torch.empty(T, d // 128, dtype=torch.float32, device=x.device)
+    rc = _lib.load().lfs_add_rmsnorm(_ptr(x), _ptr(residual), _ptr(weight), _ptr(y), _ptr(res_out),
+                                     _ptr(q), _ptr(qs), T, d, float(eps), _stream(x))
+    _lib.check(rc, "add_rmsnorm")
+    return y, (res_out if residual is not None else x), q, qs
+
+
+def qk_norm_rope_store(qkv: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor,
+                       cos_sin: torch.Tensor, positions: torch.Tensor, num_q_heads: int,
+                       num_kv_heads: int, eps: float, k_cache: Optional[torch.Tensor] = None,
+                       v_cache: Optional[torch.Tensor] = None,
+                       slot_mapping: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """q_norm / k_norm (fp32 RMSNorm over Hq*D and Hkv*D), half-split RoPE
+    (model/attention/utils.py:34-45) and the KV slot write, one launch.
+
+    qkv: bf16 [T, (Hq + 2 Hkv) * D] (rows may be strided); cos_sin: fp32
+    [max_pos, D] = cat(cos, sin); positions int64 [T]; caches bf16
+    [NB, BS, Hkv, D] and slot_mapping int64 [T] (-1 = skip), or None.
+    Returns q: bf16 [T, Hq, D].
+    """
+    assert qkv.dim() == 2 and qkv.stride(1) == 1
+    T = qkv.size(0)
+    D = cos_sin.size(1)
+    assert qkv.size(1) == (num_q_heads + 2 * num_kv_heads) * D, "qkv width mismatch"
+    _on_gpu(qkv, q_weight, k_weight, cos_sin, positions)
+    _dtype(qkv, torch.bfloat16, "qkv")
+    for t, n in ((q_weight, "q_weight"), (k_weight, "k_weight"), (cos_sin, "cos_sin")):
+        _dtype(t, torch.float32, n)
+        assert t.is_contiguous(), f"{n} must be contiguous"
+    _dtype(positions, torch.int64, "positions")
+    assert q_weight.numel() == num_q_heads * D and k_weight.numel() == num_kv_heads * D
+    num_slots = 0
+    if slot_mapping is not None:
+        _on_gpu(qkv, k_cache, v_cache, slot_mapping)
+        _dtype(slot_mapping, torch.int64, "slot_mapping")
+        for t, n in ((k_cache, "k_cache"), (v_cache, "v_cache")):
+            _dtype(t, torch.bfloat16, n)
+            assert t.is_contiguous() and t.dim() == 4 and t.shape[2:] == (num_kv_heads, D), \
+                f"{n} must be [NB, BS, Hkv, D]"
+        assert slot_mapping.numel() == T and slot_mapping.is_contiguous()
+        num_slots = k_cache.shape[0] * k_cache.shape[1]
+    q = torch.empty(T, num_q_heads, D, dtype=torch.bfloat16, device=qkv.device)
+    rc = _lib.load().lfs_qk_norm_rope_store(
+        _ptr(qkv), qkv.stride(0), _ptr(q_weight), _ptr(k_weight), _ptr(cos_sin), _ptr(positions),
+        _ptr(slot_mapping), _ptr(q), _ptr(k_cache), _ptr(v_cache), T, num_q_heads, num_kv_heads, D,
+        num_slots, cos_sin.size(0), float(eps), _stream(qkv))
+    _lib.check(rc, "qk_norm_rope_store")
+    return q
+
+
+def moe_route(h: torch.Tensor, gate_weight: torch.Tensor, expert_bias: torch.Tensor,
+              down_bias: torch.Tensor, top_k: int, num_shared: int):
+    """MoE gate (model/architecture/moe.py:45-90) as dense weights.
+
+    h: bf16 [T, d]; gate_weight bf16 [E, d]; expert_bias fp32 [E];
+    down_bias fp32 [E + S, d].  Returns (weights fp32 [T, E + S] -- the
+    renormalised top-k sigmoid scores, 0 for unpicked experts, 1 for the S
+    shared experts -- and bias fp32 [T, d] = weights @ down_bias).
+    """
+    assert h.dim() == 2 and h.is_contiguous() and gate_weight.is_contiguous()
+    T, d = h.shape
+    E = gate_weight.size(0)
+    _on_gpu(h, gate_weight, expert_bias, down_bias)
+    _dtype(h, torch.bfloat16, "h")
+    _dtype(gate_weight, torch.bfloat16, "gate_weight")
+    _dtype(expert_bias, torch.float32, "expert_bias")
+    _dtype(down_bias, torch.float32, "down_bias")
+    assert gate_weight.shape == (E, d) and expert_bias.shape == (E,)
+    assert down_bias.shape == (E + num_shared, d) and down_bias.is_contiguous()
+    w = torch.empty(T, E + num_shared, dtype=torch.float32, device=h.device)
+    bias = torch.empty(T, d, dtype=torch.float32, device=h.device)
+    rc = _lib.load().lfs_moe_route(_ptr(h), _ptr(gate_weight), _ptr(expert_bias), _ptr(down_bias),
+                                   _ptr(w), _ptr(bias), T, d, E, num_shared, top_k, _stream(h))
+    _lib.check(rc, "moe_route")
+    return w, bias
+
+
+def swiglu_quant(h13: torch.Tensor, route_weights: torch.Tensor):
+    """silu(w1 x) * (w3 x) with bf16 roundings (model/architecture/mlp.py:
+    60-67), quantised per 128 group with each group's scale multiplied by the
+    routing weight of its expert.
+
+    h13: bf16 [T, E, 2, F] (w1 rows then w3 rows per expert); route_weights
+    fp32 [T, E].  Returns (q e4m3fn [T, E*F], scales fp32 [T, E*F/128]).
+    """
+    assert h13.dim() == 4 and h13.size(2) == 2 and h13.is_contiguous()
+    T, E, _, F = h13.shape
+    _on_gpu(h13, route_weights)
+    _dtype(h13, torch.bfloat16, "h13")
+    _dtype(route_weights, torch.float32, "route_weights")
+    assert route_weights.shape == (T, E) and route_weights.is_contiguous()
+    assert F % 128 == 0, "d_ff must be a multiple of 128"
+    q = torch.empty(T, E * F, dtype=FP8, device=h13.device)
+    qs = torch.empty(T, E * F // 128, dtype=torch.float32, device=h13.device)
+    rc = _lib.load().lfs_swiglu_quant(_ptr(h13), _ptr(route_weights), _ptr(q), _ptr(qs), T, E, F,
+                                      _stream(h13))
+    _lib.check(rc, "swiglu_quant")
+    return q, qs

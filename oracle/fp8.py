@@ -219,5 +219,6 @@ def fp8_gemm(a, a_s, b, b_s, bias=None, block_size: int = 128, accum=np.float64)
             sc = sc.astype(np.float32)
         acc += part * sc
     if bias is not None:
-        acc = acc + np.asarray(bias, dtype=accum)[None, :]
+        bias = np.asarray(bias, dtype=accum)
+        acc = acc + (bias[None, :] if bias.ndim == 1 else bias)
     return bf16_round(acc.astype(np.float32))

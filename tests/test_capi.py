@@ -42,7 +42,7 @@ def test_argument_errors_are_reported_without_launch(lib):
     assert rc == -1 and b"block_size" in lib.lfs_last_error()
     rc = lib.lfs_act_quant(None, 256, None, None, 4, 200, 128, 0, None)
     assert rc == -1 and b"divisible" in lib.lfs_last_error()
-    rc = lib.lfs_fp8_gemm(None, None, None, None, None, None, 4, 4, 100, None)
+    rc = lib.lfs_fp8_gemm(None, None, None, None, None, 0, None, 4, 4, 100, None)
     assert rc == -1 and b"multiple of 128" in lib.lfs_last_error()
     rc = lib.lfs_paged_decode(None, None, None, None, None, 4, None, None, 0, 2, 16, 4, 96, 256, 8, 4,
                               0.1, 1, None)
@@ -52,11 +52,36 @@ def test_argument_errors_are_reported_without_launch(lib):
     assert rc == -1 and b"multiple of num_kv_heads" in lib.lfs_last_error()
     with pytest.raises(ValueError, match="block_size"):
         _lib.check(lib.lfs_weight_quant(None, None, None, 8, 8, 7, None), "weight_quant")
+    # split-K needs its workspace (non-null dummy pointers: the check comes first)
+    rc = lib.lfs_fp8_gemm_splitk(16, 16, 16, 16, None, 0, 16, 8, 8, 512, 4, None, 0, None)
+    assert rc == -1 and b"workspace" in lib.lfs_last_error()
+    rc = lib.lfs_fp8_gemm(16, 16, 16, 16, 16, 4, 16, 8, 8, 128, None)
+    assert rc == -1 and b"bias_ld" in lib.lfs_last_error()
+    rc = lib.lfs_add_rmsnorm(None, None, None, None, None, None, None, 4, 100, 1e-5, None)
+    assert rc == -1 and b"multiple of 8" in lib.lfs_last_error()
+    rc = lib.lfs_add_rmsnorm(None, None, None, None, None, 16, 16, 4, 200, 1e-5, None)
+    assert rc == -1 and b"128" in lib.lfs_last_error()
+    rc = lib.lfs_qk_norm_rope_store(None, 1280, None, None, None, None, None, None, None, None, 4, 12, 4, 72,
+                                    0, 4096, 1e-6, None)
+    assert rc == -1 and b"head_dim" in lib.lfs_last_error()
+    rc = lib.lfs_moe_route(None, None, None, None, None, None, 4, 768, 8, 1, 9, None)
+    assert rc == -1 and b"top_k" in lib.lfs_last_error()
+    rc = lib.lfs_swiglu_quant(None, None, None, None, 4, 9, 500, None)
+    assert rc == -1 and b"d_ff" in lib.lfs_last_error()
+
+
+def test_gemm_workspace_bytes(lib):
+    # K = 5 blocks over 3 splits -> 2 blocks per split -> 3 partial tiles
+    assert lib.lfs_fp8_gemm_workspace_bytes(10, 20, 640, 3) == 3 * 10 * 20 * 4
+    # 4 blocks over 3 splits -> 2 per split -> 2 partials
+    assert lib.lfs_fp8_gemm_workspace_bytes(10, 20, 512, 3) == 2 * 10 * 20 * 4
+    assert lib.lfs_fp8_gemm_workspace_bytes(10, 20, 128, 8) == 0
+    assert lib.lfs_fp8_gemm_workspace_bytes(10, 20, 512, 1) == 0
 
 
 def test_empty_shapes_are_no_ops(lib):
     assert lib.lfs_act_quant(None, 128, None, None, 0, 128, 128, 0, None) == 0
-    assert lib.lfs_fp8_gemm(None, None, None, None, None, None, 0, 64, 128, None) == 0
+    assert lib.lfs_fp8_gemm(None, None, None, None, None, 0, None, 0, 64, 128, None) == 0
     assert lib.lfs_store_kvcache(None, 0, None, 0, None, None, None, 0, 4, 64, 0, None) == 0
 
 

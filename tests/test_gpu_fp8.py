@@ -45,6 +45,30 @@ def test_act_quant_cfg1():
     check_act_quant(W.activation(256, 512, seed=0, outliers=False).to(DEV))
 
 
+@pytest.mark.parametrize("splits", [2, 3, 5, 7])
+def test_fp8_gemm_split_k(splits):
+    """K split over workgroups (fp32 partials + reduction): same oracle,
+    ragged M/N, a K count that does not divide evenly, bias vector and
+    per-row bias matrix."""
+    rng = np.random.default_rng(40 + splits)
+    M, N, Kd = 300, 400, 640
+    ac = rng.integers(0, 256, (M, Kd), dtype=np.uint8)
+    bc = rng.integers(0, 256, (N, Kd), dtype=np.uint8)
+    ac[(ac & 0x7F) == 0x7F] = 0
+    bc[(bc & 0x7F) == 0x7F] = 0
+    a = torch.from_numpy(ac).view(torch.float8_e4m3fn).to(DEV)
+    b = torch.from_numpy(bc).view(torch.float8_e4m3fn).to(DEV)
+    a_s = torch.from_numpy(rng.uniform(1e-3, 1e-2, (M, Kd // 128)).astype(np.float32)).to(DEV)
+    b_s = torch.from_numpy(rng.uniform(1e-3, 1e-2, (-(-N // 128), Kd // 128)).astype(np.float32)).to(DEV)
+    bias = torch.from_numpy(rng.standard_normal(N).astype(np.float32)).to(DEV)
+    bm = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32)).to(DEV)
+    for bb, what in ((None, "nobias"), (bias, "bias"), (bm, "bias matrix")):
+        got = K.fp8_gemm(a, a_s, b, b_s, bb, splits=splits)
+        assert_close(f32(got), gemm_oracle(a, a_s, b, b_s, bb), f"splits={splits} {what}")
+        one = K.fp8_gemm(a, a_s, b, b_s, bb, splits=1)
+        assert np.abs(f32(got) - f32(one)).max() <= 2e-2 + 1e-2 * np.abs(f32(one)).max()
+
+
 @pytest.mark.parametrize("M", [1, 16, 128, 4096])
 @pytest.mark.parametrize("Kd", [1024, 4096, 2048])
 def test_act_quant_cfg2_outliers(M, Kd):
@@ -185,6 +209,34 @@ def test_fp8_gemm_random_codes_and_scales():
     bias = torch.from_numpy(rng.standard_normal(N).astype(np.float32)).to(DEV)
     assert_close(f32(K.fp8_gemm(a, a_s, b, b_s)), gemm_oracle(a, a_s, b, b_s), "nobias")
     assert_close(f32(K.fp8_gemm(a, a_s, b, b_s, bias)), gemm_oracle(a, a_s, b, b_s, bias), "bias")
+    # per-row bias matrix, given as a strided view: a distinct value per (m, n)
+    # catches a bias indexed by column only or with the wrong row stride
+    bm = torch.from_numpy(rng.standard_normal((M, N + 24)).astype(np.float32)).to(DEV)[:, 5:5 + N]
+    assert_close(f32(K.fp8_gemm(a, a_s, b, b_s, bm)), gemm_oracle(a, a_s, b, b_s, bm), "bias matrix")
+
+
+@pytest.mark.parametrize("splits", [2, 3, 5, 7])
+def test_fp8_gemm_split_k(splits):
+    """K split over workgroups (fp32 partials + reduction): same oracle,
+    ragged M/N, a K count that does not divide evenly, bias vector and
+    per-row bias matrix."""
+    rng = np.random.default_rng(40 + splits)
+    M, N, Kd = 300, 400, 640
+    ac = rng.integers(0, 256, (M, Kd), dtype=np.uint8)
+    bc = rng.integers(0, 256, (N, Kd), dtype=np.uint8)
+    ac[(ac & 0x7F) == 0x7F] = 0
+    bc[(bc & 0x7F) == 0x7F] = 0
+    a = torch.from_numpy(ac).view(torch.float8_e4m3fn).to(DEV)
+    b = torch.from_numpy(bc).view(torch.float8_e4m3fn).to(DEV)
+    a_s = torch.from_numpy(rng.uniform(1e-3, 1e-2, (M, Kd // 128)).astype(np.float32)).to(DEV)
+    b_s = torch.from_numpy(rng.uniform(1e-3, 1e-2, (-(-N // 128), Kd // 128)).astype(np.float32)).to(DEV)
+    bias = torch.from_numpy(rng.standard_normal(N).astype(np.float32)).to(DEV)
+    bm = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32)).to(DEV)
+    for bb, what in ((None, "nobias"), (bias, "bias"), (bm, "bias matrix")):
+        got = K.fp8_gemm(a, a_s, b, b_s, bb, splits=splits)
+        assert_close(f32(got), gemm_oracle(a, a_s, b, b_s, bb), f"splits={splits} {what}")
+        one = K.fp8_gemm(a, a_s, b, b_s, bb, splits=1)
+        assert np.abs(f32(got) - f32(one)).max() <= 2e-2 + 1e-2 * np.abs(f32(one)).max()
 
 
 @pytest.mark.parametrize("M", [1, 16, 128, 4096])

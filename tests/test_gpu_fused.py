@@ -1,0 +1,140 @@
+"""Fused row kernels of the decode step vs the torch ops they replace.
+
+Each kernel is compared with the reference formulation in torch on the
+same device (model/utils.py:53-67 RMSNorm, model/attention/utils.py:34-45
+RoPE, model/architecture/moe.py:45-90 gate, model/architecture/mlp.py:60-67
+SwiGLU).  Row reductions are summed in a different order than torch's, so
+norm outputs may differ by one bf16 step in rare elements; everything that
+does not depend on a reduction (residual sums, slot writes, the
+quantisation of the kernel's own output) is compared bit for bit.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from llm_from_scratch_amd import kernels as K
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def bf16_steps(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """|a - b| in units of the bf16 spacing at b."""
+    a, b = a.float(), b.float()
+    spacing = torch.where(b == 0, torch.full_like(b, 2.0 ** -133),
+                          2.0 ** (torch.floor(torch.log2(b.abs())) - 7))
+    return (a - b).abs() / spacing
+
+
+def rms_ref(x, w, eps, residual=None):
+    xf = x.float() if residual is None else x.float() + residual.float()
+    return (w * xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(torch.bfloat16), xf.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("T,d", [(1, 768), (128, 768), (37, 256), (5, 4096), (3, 8192), (4, 200)])
+def test_add_rmsnorm(T, d):
+    g = torch.Generator(device=DEV).manual_seed(T * 7 + d)
+    x = (torch.randn(T, d, generator=g, device=DEV) * 3).to(torch.bfloat16)
+    r = torch.randn(T, d, generator=g, device=DEV).to(torch.bfloat16)
+    w = torch.rand(d, generator=g, device=DEV) + 0.5
+    quant = d % 128 == 0
+    for residual in (None, r):
+        out, res_out, q, qs = K.add_rmsnorm(x, w, 1e-5, residual, out=True, quant=quant)
+        want, want_res = rms_ref(x, w, 1e-5, residual)
+        steps = bf16_steps(out, want)
+        assert steps.max() <= 1 and (steps > 0).float().mean() < 1e-3, f"max {steps.max()}"
+        if residual is None:
+            assert res_out is x
+        else:
+            assert torch.equal(res_out, want_res)
+        if quant:
+            q2, qs2 = K.act_quant(out, 128)
+            assert torch.equal(q.view(torch.uint8), q2.view(torch.uint8)) and torch.equal(qs, qs2)
+    if quant:  # quantised output only
+        none, _, q3, qs3 = K.add_rmsnorm(x, w, 1e-5, r, out=False, quant=True)
+        assert none is None and torch.equal(q3.view(torch.uint8), q.view(torch.uint8)) and torch.equal(qs3, qs)
+
+
+def rope_ref(x, cos_sin, pos):
+    cos, sin = cos_sin[pos].unsqueeze(1).chunk(2, -1)
+    x1, x2 = x.float().chunk(2, -1)
+    return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), -1).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("T,Hq,Hkv,D", [(128, 12, 4, 64), (7, 32, 8, 128), (3, 4, 4, 64), (2, 64, 8, 128)])
+def test_qk_norm_rope_store(T, Hq, Hkv, D):
+    g = torch.Generator(device=DEV).manual_seed(T + Hq + D)
+    W = (Hq + 2 * Hkv) * D
+    qkv_full = torch.randn(T, W + 16, generator=g, device=DEV).to(torch.bfloat16)
+    qkv = qkv_full[:, :W]  # strided rows
+    qw = torch.rand(Hq * D, generator=g, device=DEV) + 0.5
+    kw = torch.rand(Hkv * D, generator=g, device=DEV) + 0.5
+    inv = 1.0 / (10000.0 ** (torch.arange(0, D, 2, device=DEV).float() / D))
+    ang = torch.outer(torch.arange(4096, device=DEV).float(), inv)
+    cos_sin = torch.cat([ang.cos(), ang.sin()], -1)
+    pos = torch.randint(0, 4096, (T,), generator=g, device=DEV)
+    NB, BS = 8, 16
+    kc = torch.full((NB, BS, Hkv, D), -7.0, device=DEV, dtype=torch.bfloat16)
+    vc = torch.full_like(kc, -7.0)
+    slots = torch.randperm(NB * BS, generator=g, device=DEV)[:T]
+    slots[0] = -1  # skipped
+    eps = torch.finfo(torch.float32).eps
+    q = K.qk_norm_rope_store(qkv, qw, kw, cos_sin, pos, Hq, Hkv, eps, kc, vc, slots)
+    qr, kr, vr = qkv.split([Hq * D, Hkv * D, Hkv * D], -1)
+    qn, _ = rms_ref(qr, qw, eps)
+    kn, _ = rms_ref(kr, kw, eps)
+    want_q = rope_ref(qn.view(T, Hq, D), cos_sin, pos)
+    want_k = rope_ref(kn.view(T, Hkv, D), cos_sin, pos)
+    steps = bf16_steps(q, want_q)
+    # a one-step difference in the norm output can move the rotated value by
+    # a few bf16 steps where the rotation cancels; bound by the row scale
+    err = (q.float() - want_q.float()).abs().amax() / want_q.float().abs().amax()
+    assert err < 1e-2 and (steps > 0).float().mean() < 1e-2
+    flat_k = kc.view(-1, Hkv, D)
+    flat_v = vc.view(-1, Hkv, D)
+    written = torch.zeros(NB * BS, dtype=torch.bool, device=DEV)
+    for t in range(1, T):
+        s = int(slots[t])
+        written[s] = True
+        assert torch.equal(flat_v[s], vr[t].reshape(Hkv, D)), f"v slot of token {t}"
+        e = (flat_k[s].float() - want_k[t].float()).abs().amax() / want_k[t].float().abs().amax()
+        assert e < 1e-2, f"k slot of token {t}: {e}"
+    assert (flat_k[~written] == -7.0).all() and (flat_v[~written] == -7.0).all()
+
+
+@pytest.mark.parametrize("T,d,E,S,k", [(128, 768, 8, 1, 2), (33, 256, 4, 0, 1), (5, 1024, 16, 2, 4)])
+def test_moe_route(T, d, E, S, k):
+    g = torch.Generator(device=DEV).manual_seed(T + E)
+    h = torch.randn(T, d, generator=g, device=DEV).to(torch.bfloat16)
+    gw = (torch.randn(E, d, generator=g, device=DEV) / math.sqrt(d)).to(torch.bfloat16)
+    eb = torch.randn(E, generator=g, device=DEV) * 0.1
+    b2 = torch.randn(E + S, d, generator=g, device=DEV)
+    w, bias = K.moe_route(h, gw, eb, b2, k, S)
+    logits = h.float() @ gw.float().t()
+    scores = torch.sigmoid(logits)
+    idx = torch.topk(logits + eb, k, -1).indices
+    sel = torch.gather(scores, -1, idx)
+    if k > 1:
+        sel = sel / (sel.sum(-1, keepdim=True) + 1e-10)
+    dense = torch.zeros(T, E + S, device=DEV).scatter_(1, idx, sel)
+    dense[:, E:] = 1.0
+    assert torch.equal(w > 0, dense > 0), "different experts chosen"
+    torch.testing.assert_close(w, dense, rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(bias, dense @ b2, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("T,E,F", [(128, 9, 512), (3, 2, 128), (17, 4, 1024)])
+def test_swiglu_quant(T, E, F):
+    g = torch.Generator(device=DEV).manual_seed(T + F)
+    h13 = (torch.randn(T, E, 2, F, generator=g, device=DEV) * 2).to(torch.bfloat16)
+    route = torch.rand(T, E, generator=g, device=DEV)
+    route[:, 0] = 0.0
+    q, qs = K.swiglu_quant(h13, route)
+    gg = torch.nn.functional.silu(h13[:, :, 0]) * h13[:, :, 1]
+    q2, qs2 = K.act_quant(gg.reshape(T, E * F), 128)
+    same = (q.view(torch.uint8) == q2.view(torch.uint8)).float().mean().item()
+    assert same > 0.999, f"codes equal for {same:.5f} of elements"
+    want_s = (qs2.view(T, E, F // 128) * route.unsqueeze(-1)).view(T, -1)
+    torch.testing.assert_close(qs, want_s, rtol=2e-7, atol=0)

@@ -9,9 +9,9 @@ emulated as dequant(act_quant(x)) @ dequant(W)^T + b.
 
 Two tolerances, both relative L2 error per row:
   * TOL_LAYER = 1e-2 for each op of each layer (FP8 linears, norms, K/V
-    writes, paged attention, SwiGLU, MoE combine) fed the GPU's own input to
-    that op and the GPU-written KV cache (teacher forcing): the single-op
-    bar;
+    writes, paged attention, the MoE's SwiGLU + down projection + weighted
+    combine) fed the GPU's own input to that op and the GPU-written KV cache
+    (teacher forcing): the single-op bar;
   * e2e_tol(layers) = 4e-2 * sqrt(layers) for logits after the whole
     stack, a drift bound rather than a parity bar.  Two valid FP8
     computations drift apart layer by layer: a bf16 rounding difference in
@@ -60,9 +60,14 @@ def w_deq(m: FP8Linear) -> torch.Tensor:
 
 
 def lin(m: FP8Linear, x: torch.Tensor) -> torch.Tensor:
-    y = q_act(x.to(torch.bfloat16)) @ w_deq(m).t()
-    if m.bias is not None:
-        y = y + m.bias
+    return lin_w(w_deq(m), m.bias, x)
+
+
+def lin_w(w: torch.Tensor, bias, x: torch.Tensor) -> torch.Tensor:
+    """dequant(act_quant(x)) @ w^T (+ bias), rounded to bf16."""
+    y = q_act(x.to(torch.bfloat16)) @ w.t()
+    if bias is not None:
+        y = y + bias
     return y.to(torch.bfloat16)
 
 
@@ -93,35 +98,70 @@ def gqa(q, k, v, mask=None):
     return torch.matmul(torch.softmax(s, -1), vh).transpose(0, 1).reshape(Tq, Hq * D)
 
 
+def split_qkv(y, cfg):
+    T, Hq, Hkv, D = y.shape[0], cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
+    q, k, v = y.split([Hq * D, Hkv * D, Hkv * D], dim=-1)
+    return q, k, v.reshape(T, Hkv, D)
+
+
+def norm_rope(a, q, k, pos, cfg):
+    T, Hq, Hkv, D = q.shape[0], cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
+    q = rms(q, a.q_norm.weight, FP32_EPS)[0].view(T, Hq, D)
+    k = rms(k, a.k_norm.weight, FP32_EPS)[0].view(T, Hkv, D)
+    return (rope(q, pos, cfg.rope_theta, D).to(torch.bfloat16),
+            rope(k, pos, cfg.rope_theta, D).to(torch.bfloat16))
+
+
 def ref_qkv(a, h, pos, cfg):
-    T, Hq, Hkv, D = h.shape[0], cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
-    q = rms(lin(a.q_proj, h), a.q_norm.weight, FP32_EPS)[0].view(T, Hq, D)
-    k = rms(lin(a.k_proj, h), a.k_norm.weight, FP32_EPS)[0].view(T, Hkv, D)
-    v = lin(a.v_proj, h).view(T, Hkv, D)
-    q = rope(q, pos, cfg.rope_theta, D).to(torch.bfloat16)
-    k = rope(k, pos, cfg.rope_theta, D).to(torch.bfloat16)
+    """q_proj/k_proj/v_proj (GQA.py:80-82) -- rows of the fused weight --
+    then q_norm over d_model, k_norm over Hkv*D, half-split RoPE."""
+    q, k, v = split_qkv(lin(a.qkv_proj, h), cfg)
+    q, k = norm_rope(a, q, k, pos, cfg)
     return q, k, v
 
 
-def ref_moe(f, h, cfg):
-    T = h.shape[0]
+def expert_weights(f, e):
+    """(w1, b1, w3, b3, w2, b2) of expert e (the last one is the shared
+    expert), dequantised from the stacked FP8 weights."""
+    F = f.d_ff
+    w13, b13 = w_deq(f.w13), f.w13.bias
+    w2 = w_deq(f.w2)
+    r = 2 * F * e
+    return (w13[r:r + F], b13[r:r + F], w13[r + F:r + 2 * F], b13[r + F:r + 2 * F],
+            w2[:, e * F:(e + 1) * F], f.w2_bias[e])
+
+
+def ref_route(f, h):
     logits = h.float() @ f.gate_weight.float().t()
     scores = torch.sigmoid(logits)
     idx = torch.topk(logits + f.expert_bias, f.top_k, -1).indices
     w = torch.gather(scores, -1, idx)
-    w = w / (w.sum(-1, keepdim=True) + 1e-10)
+    return idx, w / (w.sum(-1, keepdim=True) + 1e-10)
 
-    def mlp(e, z):
-        return lin(e.w2, torch.nn.functional.silu(lin(e.w1, z)) * lin(e.w3, z))
 
-    y = torch.zeros(T, cfg.d_model, device=h.device)
-    outs = [mlp(e, h).float() for e in f.experts]
+def ref_combine(f, h, outs, d_model):
+    """sum of the chosen experts' outputs weighted by the renormalised gate
+    scores, plus the shared expert (moe.py:196-260, 288-341), in fp32."""
+    idx, w = ref_route(f, h)
+    y = outs[-1].float().clone()
     for j in range(f.top_k):
         for e in range(f.n_experts):
             sel = idx[:, j] == e
-            y[sel] += w[sel, j:j + 1] * outs[e][sel]
-    y += mlp(f.shared_expert, h).float()
+            y[sel] += w[sel, j:j + 1] * outs[e][sel].float()
     return y.to(torch.bfloat16)
+
+
+def swiglu(a, b):
+    """silu(w1 x) * (w3 x) with the reference's bf16 roundings."""
+    return torch.nn.functional.silu(a.to(torch.bfloat16)) * b.to(torch.bfloat16)
+
+
+def ref_moe(f, h, cfg):
+    outs = []
+    for e in range(f.n_experts + f.n_shared):
+        w1, b1, w3, b3, w2, b2 = expert_weights(f, e)
+        outs.append(lin_w(w2, b2, swiglu(lin_w(w1, b1, h), lin_w(w3, b3, h))))
+    return ref_combine(f, h, outs, cfg.d_model)
 
 
 def ref_block(blk, x, residual, pos, cfg, attend):
@@ -206,96 +246,76 @@ def _gather(cache, table, L):
 
 
 def check_layers_teacher_forced(model, runner, seqs):
-    """Eager decode step with hooks on every block, attention, MoE and FP8
-    linear.  Each op must match the reference on the GPU's own input to that
-    op (teacher forcing), so no error is carried from one op to the next:
-      every FP8 linear vs dequant(act_quant(x)) @ dequant(W)^T + b;
-      att_norm / ffn_norm / final_norm (fused add & norm);
-      the newest token's K/V in the pool vs k_norm/RoPE of the GPU's k_proj
-      output and the GPU's v_proj output;
-      attention (GQA over the K/V that the GPU wrote to the pool) vs the
-      output projection's input;
-      each expert's SwiGLU product vs w2's input;
-      MoE combine (gate, top-k, renormalised weights, shared expert) over
-      the GPU's expert outputs vs the MoE output.
+    """Eager decode step with the model's trace on; each op must match the
+    reference on the GPU's own input to that op (teacher forcing), so no
+    error is carried from one op to the next:
+      every FP8 linear (qkv, output, experts' w1/w3, lm_head) vs
+      dequant(act_quant(x)) @ dequant(W)^T + b;
+      att_norm / ffn_norm / final_norm (fused add & norm, residual out);
+      q after q_norm + RoPE, and the newest token's K/V in the pool after
+      k_norm + RoPE, vs the same from the GPU's qkv output;
+      attention (GQA over the K/V the GPU wrote to the pool) vs its output;
+      gate weights and routed bias vs the reference gate;
+      MoE down projection from the GPU's w1/w3 output: per-expert SwiGLU and
+      w2 (+ bias), combined with the gate weights and the shared expert, vs
+      the MoE output.
     Returns the largest error per op kind."""
-    rec: dict[str, tuple] = {}
-
-    def hook(name):
-        def f(mod, args, out):
-            rec[name] = (args, out)
-        return f
-
-    hooks = [m.register_forward_hook(hook(n)) for n, m in model.named_modules()
-             if isinstance(m, FP8Linear) or n.count(".") == 1 and n.startswith("layers.")
-             or n.endswith(".att") or n.endswith(".ffn")]
+    model.trace = {}
     try:
         _decode(runner, seqs, eager=True)
+        tr = model.trace
     finally:
-        for h in hooks:
-            h.remove()
+        model.trace = None
     cfg = model.cfg
     worst: dict[str, float] = {}
 
     def chk(kind, got, want, what):
-        e = rel_err_rows(got, want).max().item()
+        e = rel_err_rows(got.reshape(got.shape[0], -1), want.reshape(want.shape[0], -1)).max().item()
         worst[kind] = max(worst.get(kind, 0.0), e)
         assert e <= TOL_LAYER, f"{what}: {kind} rel err {e:.4f}"
 
-    for name, m in model.named_modules():
-        if isinstance(m, FP8Linear):
-            (x,), y = rec[name]
-            chk("linear", y, lin(m, x), name)
-    T, Hq, Hkv, D = len(seqs), cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
+    pos = torch.tensor([len(s) - 1 for s in seqs], device=model.embed.device)
     for layer, blk in enumerate(model.layers):
-        p = f"layers.{layer}"
-        (x, residual, pos), (y, res_out) = rec[p]
-        (att_in, _), att_out = rec[p + ".att"]
-        (ffn_in,), ffn_out = rec[p + ".ffn"]
-        if residual is None:
-            h, r = rms(x, blk.att_norm.weight, cfg.rms_eps)[0], x
+        t, p = tr[layer], f"layer {layer}"
+        if t["residual"] is None:
+            h, r = rms(t["x"], blk.att_norm.weight, cfg.rms_eps)[0], t["x"]
         else:
-            h, r = rms(x, blk.att_norm.weight, cfg.rms_eps, residual)
-        chk("norm", att_in, h, f"{p} att_norm")
-        h2, r2 = rms(att_out, blk.ffn_norm.weight, cfg.rms_eps, r)
-        chk("norm", ffn_in, h2, f"{p} ffn_norm")
-        chk("norm", res_out, r2, f"{p} residual")
+            h, r = rms(t["x"], blk.att_norm.weight, cfg.rms_eps, t["residual"])
+        chk("norm", t["att_h"], h, f"{p} att_norm")
         a = blk.att
-        q = rms(rec[p + ".att.q_proj"][1], a.q_norm.weight, FP32_EPS)[0].view(T, Hq, D)
-        k = rms(rec[p + ".att.k_proj"][1], a.k_norm.weight, FP32_EPS)[0].view(T, Hkv, D)
-        v = rec[p + ".att.v_proj"][1].view(T, Hkv, D)
-        q = rope(q, pos, cfg.rope_theta, D).to(torch.bfloat16)
-        k = rope(k, pos, cfg.rope_theta, D).to(torch.bfloat16)
-        o = rec[p + ".att.output_proj"][0][0]
+        chk("linear", t["qkv"], lin(a.qkv_proj, t["att_h"]), f"{p} qkv_proj")
+        q, k, v = split_qkv(t["qkv"], cfg)
+        q, k = norm_rope(a, q, k, pos, cfg)
+        chk("q_norm_rope", t["q"], q, p)
         for i, s in enumerate(seqs):
             L = len(s)
             Kc = _gather(a.k_cache, s.block_table, L)
             Vc = _gather(a.v_cache, s.block_table, L)
             what = f"{p} seq {i} len {L}"
-            chk("new_k", Kc[-1].reshape(1, -1), k[i].reshape(1, -1), what)
-            chk("new_v", Vc[-1].reshape(1, -1), v[i].reshape(1, -1), what)
-            chk("attention", o[i:i + 1], gqa(q[i:i + 1], Kc, Vc), what)
+            chk("new_k", Kc[-1:], k[i:i + 1], what)
+            chk("new_v", Vc[-1:], v[i:i + 1], what)
+            chk("attention", t["att_o"][i:i + 1], gqa(t["q"][i:i + 1], Kc, Vc), what)
+        chk("linear", t["att_out"], lin(a.output_proj, t["att_o"]), f"{p} output_proj")
+        h2, r2 = rms(t["att_out"], blk.ffn_norm.weight, cfg.rms_eps, r)
+        chk("norm", t["ffn_h"], h2, f"{p} ffn_norm")
+        chk("norm", t["res_mid"], r2, f"{p} residual")
         f = blk.ffn
-        experts = [f"{p}.ffn.experts.{e}" for e in range(f.n_experts)] + [f"{p}.ffn.shared_expert"]
+        idx, w = ref_route(f, t["ffn_h"])
+        dense = torch.zeros(len(seqs), f.n_experts + f.n_shared, device=w.device)
+        dense.scatter_(1, idx, w)
+        dense[:, f.n_experts:] = 1.0
+        chk("route", t["route_w"], dense, p)
+        chk("route", t["route_bias"], dense @ f.w2_bias, p)
+        chk("linear", t["h13"], lin(f.w13, t["ffn_h"]), f"{p} w13")
         outs = []
-        for e in experts:
-            act = torch.nn.functional.silu(rec[e + ".w1"][1]) * rec[e + ".w3"][1]
-            chk("swiglu", rec[e + ".w2"][0][0], act, e)
-            outs.append(rec[e + ".w2"][1].float())
-        logits = ffn_in.float() @ f.gate_weight.float().t()
-        idx = torch.topk(logits + f.expert_bias, f.top_k, -1).indices
-        w = torch.gather(torch.sigmoid(logits), -1, idx)
-        w = w / (w.sum(-1, keepdim=True) + 1e-10)
-        want = outs[-1].clone()
-        for j in range(f.top_k):
-            for e in range(f.n_experts):
-                sel = idx[:, j] == e
-                want[sel] += w[sel, j:j + 1] * outs[e][sel]
-        chk("moe_combine", ffn_out, want.to(torch.bfloat16), p)
-        assert y is ffn_out
-    (head_in,), _ = rec["lm_head"]
-    (_, (y, res_out)) = rec[f"layers.{len(model.layers) - 1}"]
-    chk("norm", head_in, rms(y, model.final_norm.weight, cfg.rms_eps, res_out)[0], "final_norm")
+        for e in range(f.n_experts + f.n_shared):
+            _, _, _, _, w2, b2 = expert_weights(f, e)
+            r0 = 2 * f.d_ff * e
+            outs.append(lin_w(w2, b2, swiglu(t["h13"][:, r0:r0 + f.d_ff], t["h13"][:, r0 + f.d_ff:r0 + 2 * f.d_ff])))
+        chk("moe_down_combine", t["ffn_out"], ref_combine(f, t["ffn_h"], outs, cfg.d_model), p)
+    fin = tr["final"]
+    chk("norm", fin["h"], rms(fin["x"], model.final_norm.weight, cfg.rms_eps, fin["residual"])[0], "final_norm")
+    chk("linear", fin["logits"], lin(model.lm_head, fin["head_in"]), "lm_head")
     return worst
 
 
