@@ -66,8 +66,8 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 //   V  : lane l owns token (l / (D/8)) + (64/(D/8))*i and dims
 //        (l % (D/8))*8 .. +7 (coalesced 16-byte loads), fp32 FMAs into
 //        acc[G][8], rescaled by exp2(m_old - m_new) read from lane g.
-// Loads are software-pipelined one tile ahead (K of the next tile behind the
-// QK MFMAs, V of the next tile behind the P.V) with nontemporal 16-byte
+// Loads are software-pipelined two tiles ahead (two K and two V buffers,
+// each refilled as soon as its tile is consumed) with nontemporal 16-byte
 // loads, since every KV row is read exactly once.  There is no workgroup
 // barrier: waves exit independently.  A chunk that covers
 // the whole context writes the normalised bf16 output directly; otherwise
@@ -136,48 +136,67 @@ __global__ __launch_bounds__(256) void paged_decode_split(
   float* pw = p_lds[wave];
   const int32_t* btrow = bt + (int64_t)b * bt_stride;
 
-  // tile descriptor: valid token count (0 = masked) and element offset
-  auto tile_at = [&](int64_t t0, int& n, int64_t& off) {
+  const int ntiles = (int)((t_end - t_begin + tile - 1) / tile);
+  // tile i of the chunk: valid row count (0 for a skipped block) and the
+  // element offset of its first row.  Tiles at or past `last` are
+  // look-ahead fillers: n = 0 and row 0 of block 0, so their loads all hit
+  // one line (they only keep the per-step load count constant).
+  int last = 0;
+  auto tile_at = [&](int i, int& n, int64_t& off) {
+    if (i >= last) {
+      n = 0;
+      off = (int64_t)kh * D;
+      return;
+    }
+    const int64_t t0 = t_begin + (int64_t)i * tile;
     n = (int)min((int64_t)tile, t_end - t0);
     const int32_t blk = btrow[t0 / BS];
-    if (blk < 0 || (int64_t)blk >= NB) n = 0;  // invalid block: contributes nothing
-    off = ((int64_t)(n > 0 ? blk : 0) * BS + (t0 % BS)) * row + (int64_t)kh * D;
+    const bool ok = blk >= 0 && (int64_t)blk < NB;
+    if (!ok) n = 0;  // invalid block: contributes nothing
+    off = ((int64_t)(ok ? blk : 0) * BS + (t0 % BS)) * row + (int64_t)kh * D;
   };
-  uint4 ka[Geo::NG][Geo::NDC];
-  uint4 va[Geo::UV];
-  auto load_k = [&](int n, int64_t off) {
+  // Every load is issued unconditionally: rows past the valid count n read
+  // row n-1 (row 0 of block 0 for a skipped block), whose scores are masked
+  // and whose P is 0 (a skipped block's P.V is not run).  Offsets inside a
+  // tile are 32-bit from a wave-uniform base.
+  auto load_k = [&](uint4 (&ka)[Geo::NG][Geo::NDC], int n, int64_t off) {
     const uint16_t* kb = kc + off;
+    const int nn = max(n, 1);
 #pragma unroll
     for (int g16 = 0; g16 < Geo::NG; ++g16) {
-      const int tok = g16 * 16 + j;
+      const int tr = min(g16 * 16 + j, nn - 1);
 #pragma unroll
       for (int c = 0; c < Geo::NDC; ++c)
-        ka[g16][c] = tok < n ? nt_load16(kb + tok * row + c * 32 + kq * 8) : make_uint4(0, 0, 0, 0);
+        ka[g16][c] = nt_load16(kb + (uint32_t)(tr * (int)row + c * 32 + kq * 8));
     }
   };
-  auto load_v = [&](int n, int64_t off) {
+  auto load_v = [&](uint4 (&va)[Geo::UV], int n, int64_t off) {
     const uint16_t* vb = vc + off;
+    const int nn = max(n, 1);
 #pragma unroll
-    for (int i = 0; i < Geo::UV; ++i) {
-      const int tok = ts + Geo::TPI * i;
-      va[i] = tok < n ? nt_load16(vb + tok * row + dc * 8) : make_uint4(0, 0, 0, 0);
-    }
+    for (int i = 0; i < Geo::UV; ++i)
+      va[i] = nt_load16(vb + (uint32_t)(min(ts + Geo::TPI * i, nn - 1) * (int)row + dc * 8));
   };
 
-  // Software pipeline without extra registers: K of tile i+1 is requested as
-  // soon as the QK MFMAs of tile i have consumed ka, V of tile i+1 as soon as
-  // the P.V of tile i has consumed va, so one tile is always in flight.
-  int n_cur;
-  int64_t off_cur;
-  tile_at(t_begin, n_cur, off_cur);
-  load_k(n_cur, off_cur);
-  load_v(n_cur, off_cur);
-  for (int64_t t0 = t_begin; t0 < t_end; t0 += tile) {
-    const int n = n_cur;
-    const bool has_next = t0 + tile < t_end;
-    int n_nxt = 0;
-    int64_t off_nxt = 0;
-    if (has_next) tile_at(t0 + tile, n_nxt, off_nxt);
+  // Software pipeline two tiles deep, two K and two V buffers.  Issue order:
+  //   prologue K0 V0 K1 V1;  tile i: [QK_i] K_{i+2} [softmax, P.V_i] V_{i+2}
+  // Each buffer is refilled with tile i+2 as soon as tile i has consumed it,
+  // so up to two tiles of K and V are in flight while a tile is computed.
+  // The tiles of a chunk are processed in straight-line code (MAXT steps
+  // unrolled, with early exits), every step issuing the same loads, so the
+  // compiler's in-order wait counts are exact: QK_i waits only for K_i and
+  // P.V_i only for V_i.  (In a loop, its conservative merge at the loop
+  // header drains every load in flight once per iteration.)  Chunks longer
+  // than MAXT tiles are walked MAXT tiles at a time.
+  constexpr int MAXT = 8;
+  uint4 ka0[Geo::NG][Geo::NDC], ka1[Geo::NG][Geo::NDC];
+  uint4 va0[Geo::UV], va1[Geo::UV];
+  int nb0 = 0, nb1 = 0;
+  auto step = [&](int i, uint4 (&ka)[Geo::NG][Geo::NDC], uint4 (&va)[Geo::UV], int& nb) {
+    const int n = nb;
+    int n2;
+    int64_t o2;
+    tile_at(i + 2, n2, o2);
 
     // ---- scores (log2 domain) and online-softmax update for head j
     float s[Geo::NG][4];
@@ -195,7 +214,9 @@ __global__ __launch_bounds__(256) void paged_decode_split(
         tmax = fmaxf(tmax, s[g16][r]);
       }
     }
-    if (has_next) load_k(n_nxt, off_nxt);
+    __builtin_amdgcn_sched_barrier(0);  // keep the issue order the wait counts assume
+    load_k(ka, n2, o2);
+    __builtin_amdgcn_sched_barrier(0);
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
     const float m_new = fmaxf(m_run, tmax);
@@ -216,35 +237,56 @@ __global__ __launch_bounds__(256) void paged_decode_split(
     m_run = m_new;
     wave_lds_sync();
 
-    // ---- P.V
+    // ---- P.V (rows past n have P = 0; a skipped block adds nothing)
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), g));
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[g][e] *= a;
     }
+    if (n > 0) {
 #pragma unroll
-    for (int i = 0; i < Geo::UV; ++i) {
-      const int tok = ts + Geo::TPI * i;
-      if (tok < n) {
-        float vf[8];
-        unpack8(va[i], vf);
+      for (int iv = 0; iv < Geo::UV; ++iv) {
+        const int tok = ts + Geo::TPI * iv;
         float pg[GP];
 #pragma unroll
         for (int g4 = 0; g4 < GP; g4 += 4) {
           const float4 p4 = *reinterpret_cast<const float4*>(&pw[tok * GP + g4]);
           pg[g4] = p4.x; pg[g4 + 1] = p4.y; pg[g4 + 2] = p4.z; pg[g4 + 3] = p4.w;
         }
+        float vf[8];
+        unpack8(va[iv], vf);
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
           for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pg[g], vf[e], acc[g][e]);
       }
     }
-    if (has_next) load_v(n_nxt, off_nxt);
+    __builtin_amdgcn_sched_barrier(0);
+    load_v(va, n2, o2);
+    __builtin_amdgcn_sched_barrier(0);
     wave_lds_sync();
-    n_cur = n_nxt;
-    off_cur = off_nxt;
+    nb = n2;
+  };
+  for (int base = 0; base < ntiles; base += MAXT) {
+    last = min(ntiles, base + MAXT);
+    {
+      int64_t o0, o1;
+      tile_at(base, nb0, o0);
+      tile_at(base + 1, nb1, o1);
+      load_k(ka0, nb0, o0);
+      load_v(va0, nb0, o0);
+      load_k(ka1, nb1, o1);
+      load_v(va1, nb1, o1);
+    }
+#pragma unroll
+    for (int u = 0; u < MAXT; u += 2) {
+      if (base + u >= last) break;
+      step(base + u, ka0, va0, nb0);
+      if (base + u + 1 >= last) break;
+      step(base + u + 1, ka1, va1, nb1);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // drain the look-ahead loads
   }
 
   // ---- reduce the token subgroups (lanes with the same dc)
@@ -396,6 +438,7 @@ extern "C" int lfs_paged_decode(const void* q, const void* k_cache, const void* 
   LFS_REQUIRE(BS % 16 == 0, "paged_decode: block_size must be a multiple of 16 (got %d)", BS);
   LFS_REQUIRE(blocks_per_split > 0, "paged_decode: blocks_per_split must be positive");
   LFS_REQUIRE(bt_stride >= max_blocks, "paged_decode: block table stride < max_blocks");
+  LFS_REQUIRE(num_blocks >= 1 || max_blocks == 0, "paged_decode: empty KV pool");
   if (B == 0) return 0;
   LFS_REQUIRE(q && k_cache && v_cache && context_lens && out, "paged_decode: null pointer");
   LFS_REQUIRE(max_blocks == 0 || block_tables, "paged_decode: null block table");
