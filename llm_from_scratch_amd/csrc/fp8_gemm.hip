@@ -9,21 +9,27 @@
 // (4 FMAs per tile per K block).  The scales are arbitrary fp32 values, so the
 // hardware's power-of-two (E8M0) operand scaling cannot carry them.
 //
-// Workgroup tile BM x 128 (one weight-scale block wide), 64x64 per wave
-// (4x4 MFMA tiles).  A and B K-tiles (16 KB each) are
-// copied global -> LDS by DMA (no register staging) into a ring of NST
-// stages; the activation scales follow in chunks of whole rows.
+// Two kernels: fp8_gemm_tile, a 128 x 128 tile (64x64 per wave, two
+// workgroups per CU, optional split-K), and fp8_gemm_big, a 256 x 256 tile
+// (128x64 per wave, one workgroup per CU) for shapes that fill the chip.
+// A and B K-tiles are copied global -> LDS by DMA (no register staging);
+// the activation scales follow in chunks of whole rows.
 //
 // MFMA operand convention: lane l supplies row (l % 16) of each operand and
-// the 32 bytes [32*(l/16), 32*(l/16)+32) of the 128-byte K block; both
-// operands use the same K assignment, so the dot products pair the same K
-// indices whatever order the instruction sums them in.  The 16x16 fp32
-// result D = X Y^T in lane l is column (l % 16), rows 4*(l/16) .. +3.
+// 32 bytes of the 128-byte K block: 16-byte chunks (l/16) and (l/16)+4.
+// Both operands use the same K assignment, so the dot products pair the
+// same K indices whatever order the instruction sums them in.  (Chunks g and
+// g+4 rather than 2g and 2g+1 make the sixteen rows of one read touch every
+// LDS bank once with the swizzle below: full LDS read bandwidth on gfx950,
+// against half of it for the adjacent pair.)  The 16x16 fp32 result
+// D = X Y^T in lane l is column (l % 16), rows 4*(l/16) .. +3.
 //
 // Tile order: workgroup ids are dealt round-robin to the 8 XCDs, so the id
 // is remapped to give each XCD a contiguous range of tiles, walked in groups
-// of 8 row-tiles so that concurrently running tiles share A rows and B
+// of row-tiles so that concurrently running tiles share A rows and B
 // columns in that XCD's L2.
+#include <algorithm>
+
 #include "common.h"
 
 namespace lfs {
@@ -68,6 +74,20 @@ __device__ __forceinline__ void dma4(const void* g, unsigned lds) {
   asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dword %2, off\n\ts_mov_b32 m0, %0"
                : "=&s"(tmp) : "s"(lds), "v"(g) : "memory");
 }
+// Same copy with a wave-uniform base address (SGPR pair) and a 32-bit
+// per-lane byte offset, so that per-lane addresses cost one VGPR.
+__device__ __forceinline__ void dma16s(const void* base_any, unsigned off, unsigned lds) {
+  // uniform by construction; make it an SGPR pair (readfirstlane returns
+  // int: each half goes through uint32_t so that the low word is not
+  // sign-extended into the high one)
+  const uint64_t b = (uint64_t)(uintptr_t)base_any;
+  const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+  const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+  const void* base = (const void*)(uintptr_t)((hi << 32) | lo);
+  unsigned tmp;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %2, %3\n\ts_mov_b32 m0, %0"
+               : "=&s"(tmp) : "s"(lds), "v"(off), "s"(base) : "memory");
+}
 // LDS writes of this wave visible to its other lanes (no workgroup barrier)
 __device__ __forceinline__ void wave_lds_fence() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -87,7 +107,8 @@ __device__ __forceinline__ void wait_vm() {
 
 // LDS tile layout: 128-byte rows; 16-byte chunk c of row r is stored in
 // chunk slot c ^ f(r), f(r) = ((r >> 1) & 7) ^ ((r & 1) << 2), which spreads
-// the MFMA operand reads (16 rows x one chunk per 16 lanes) over the banks.
+// the MFMA operand reads (16 rows x chunk g or g+4 per 16 lanes) over the
+// banks.
 // Each DMA instruction fills 8 whole rows: lane l writes slot (l & 7) of row
 // 8s + (l >> 3), so it fetches logical chunk (l & 7) ^ f(row) -- 8 complete
 // 128-byte lines per instruction, the access pattern the load path streams
@@ -193,10 +214,10 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
   int offA[4][2], offB[4][2];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    offA[i][0] = swz(wm * 64 + i * 16 + r16, 2 * g);
-    offA[i][1] = swz(wm * 64 + i * 16 + r16, 2 * g + 1);
-    offB[i][0] = A_BYTES + swz(wn * 64 + i * 16 + r16, 2 * g);
-    offB[i][1] = A_BYTES + swz(wn * 64 + i * 16 + r16, 2 * g + 1);
+    offA[i][0] = swz(wm * 64 + i * 16 + r16, g);
+    offA[i][1] = swz(wm * 64 + i * 16 + r16, g + 4);
+    offB[i][0] = A_BYTES + swz(wn * 64 + i * 16 + r16, g);
+    offB[i][1] = A_BYTES + swz(wn * 64 + i * 16 + r16, g + 4);
   }
   // C = A B^T is formed as (B A^T)^T: the MFMA's first operand is the B
   // fragment, so lane l holds output row 16i + (l % 16), columns
@@ -335,6 +356,205 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
   }
 }
 
+// ---------------------------------------------------------------------------
+// 256x256 tile, 8 waves (2 x 4), 128 x 64 per wave (8 x 4 MFMA tiles).
+//
+// Half the global->LDS bytes per flop of the 128x128 tile and 3/4 of its LDS
+// reads per MFMA.  Two 64 KB stages and one barrier per K block: after the
+// barrier of block kt every wave has finished block kt-1, so block kt+1 is
+// copied into that stage while block kt is multiplied.  The activation
+// scales (k-major [SCKB][256] floats per chunk of SCKB K blocks, double
+// buffered) and the tile's two weight-scale columns ([SCKB][2]) come through
+// the same DMA path, so everything an iteration copies is one group that the
+// wave waits for with vmcnt(0) before the barrier.  The eight 1 KB copies of
+// a wave are spread over its MFMA sequence (one per four MFMAs) so that no
+// wave waits behind a full load queue before its MFMAs.
+//
+// Per K block a wave reads its four B fragments, then streams its eight A
+// fragments one 16-row m-tile ahead of the MFMAs; the fold of MFMA k into
+// the fp32 accumulator runs two MFMAs behind it.
+constexpr int BIG = 256, SCKB = 8, GROUP_M_BIG = 4;
+
+__global__ __launch_bounds__(512, 1) void fp8_gemm_big(
+    const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ B,
+    const float* __restrict__ Bs, const float* __restrict__ bias, int64_t bias_ld, uint16_t* __restrict__ C, int M,
+    int N, int K, int tiles_m, int tiles_n) {
+  constexpr int A_BYTES = BIG * BK;    // 32 KB (B tile the same)
+  constexpr int STAGE = 2 * A_BYTES;   // 64 KB
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+  __shared__ __attribute__((aligned(1024))) float sas[2][SCKB][BIG];
+  __shared__ __attribute__((aligned(64))) float sbs[2][SCKB][2];
+
+  // ---- tile order (XCD-contiguous ranges, groups of GROUP_M_BIG row-tiles)
+  int pid = blockIdx.x;
+  const int ntiles = tiles_m * tiles_n;
+  if ((ntiles & 7) == 0) pid = (pid & 7) * (ntiles >> 3) + (pid >> 3);
+  const int group = pid / (GROUP_M_BIG * tiles_n);
+  const int first_m = group * GROUP_M_BIG;
+  const int gsize = min(tiles_m - first_m, GROUP_M_BIG);
+  const int tm = first_m + (pid % gsize);
+  const int tn = (pid % (GROUP_M_BIG * tiles_n)) / gsize;
+  const int m0 = tm * BIG, n0 = tn * BIG;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 2, wn = wave & 3;
+  const int KT = K / BK;
+  const int nbs = (N + 127) / 128;  // weight-scale rows
+  const int r16 = lane & 15, g = lane >> 4;
+
+  // ---- DMA sources: segment q = wave + 8u (u = 0..3) is tile rows 8q .. 8q+7,
+  // addressed as a uniform tile base plus a per-lane offset (rows past M / N
+  // are clamped; their results are never stored).  The host guarantees
+  // 256 * K < 2^31.
+  unsigned offA[4], offB[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int r = 8 * (wave + 8 * u) + (lane >> 3);
+    const int c = (lane & 7) ^ (((r >> 1) & 7) ^ ((r & 1) << 2));
+    offA[u] = (unsigned)(min(m0 + r, M - 1) - m0) * (unsigned)K + c * 16;
+    offB[u] = (unsigned)(min(n0 + r, N - 1) - n0) * (unsigned)K + c * 16;
+  }
+  const uint8_t* tileA = A + (size_t)m0 * K;
+  const uint8_t* tileB = B + (size_t)n0 * K;
+  const unsigned lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
+  const unsigned lsas = __builtin_amdgcn_readfirstlane(lds_addr(&sas[0][0][0]));
+  const unsigned lsbs = __builtin_amdgcn_readfirstlane(lds_addr(&sbs[0][0][0]));
+
+  auto issue = [&](int kt, int buf) {
+    const unsigned base = lds0 + buf * STAGE;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) dma16s(tileA + (size_t)kt * BK, offA[u], base + (wave + 8 * u) * 1024);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) dma16s(tileB + (size_t)kt * BK, offB[u], base + A_BYTES + (wave + 8 * u) * 1024);
+  };
+  // scale chunk for K blocks kb0 .. kb0+SCKB-1: wave w copies K block
+  // kb0 + w for 256 rows (four 64-row dword copies); lanes 0-15 of wave 0
+  // copy b_s[n0/128 + h][kb0 + k] to sbs[buf][k][h] (k = lane/2, h = lane%2).
+  // Rows, weight-scale rows and K blocks past the end are clamped (unused).
+  auto issue_scales = [&](int kb0, int buf) {
+    const int kb = min(kb0 + wave, KT - 1);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float* src = As + (size_t)min(m0 + 64 * u + lane, M - 1) * KT + kb;
+      dma4(src, lsas + ((buf * SCKB + wave) * BIG + 64 * u) * 4);
+    }
+    if (wave == 0 && lane < 16) {
+      const float* src = Bs + (size_t)min(n0 / 128 + (lane & 1), nbs - 1) * KT + min(kb0 + (lane >> 1), KT - 1);
+      dma4(src, lsbs + buf * SCKB * 2 * 4);
+    }
+  };
+
+  // operand read offsets: rows base + 16 i + r16 sit at i * 2048 plus a
+  // per-lane offset (the swizzle depends only on r16)
+  const int fsw = ((r16 >> 1) & 7) ^ ((r16 & 1) << 2);
+  const int la0 = (wm * 128 + r16) * BK + ((g ^ fsw) << 4);
+  const int la1 = (wm * 128 + r16) * BK + (((g + 4) ^ fsw) << 4);
+  const int lb0 = A_BYTES + (wn * 64 + r16) * BK + ((g ^ fsw) << 4);
+  const int lb1 = A_BYTES + (wn * 64 + r16) * BK + (((g + 4) ^ fsw) << 4);
+
+  v4f acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  issue_scales(0, 0);
+  issue(0, 0);
+  for (int kt = 0; kt < KT; ++kt) {
+    wait_vm<0>();     // this wave's copies of block kt (and its scale chunk) landed
+    __syncthreads();  // everyone's copies landed; everyone is done with block kt-1
+    if (kt + 1 < KT && (kt + 1) % SCKB == 0) issue_scales(kt + 1, ((kt + 1) / SCKB) & 1);
+    const unsigned nbase = lds0 + ((kt + 1) & 1) * STAGE;
+    const int kn = min(kt + 1, KT - 1);  // the last block re-copies itself into the free stage
+    const uint8_t* st = smem + (kt & 1) * STAGE;
+    const int sbuf = (kt / SCKB) & 1, kc = kt % SCKB;
+    const float* sa = &sas[sbuf][kc][wm * 128 + r16];
+    const float bsv = sbs[sbuf][kc][wn >> 1];
+    v8i fb[4], fa[8];
+    float sc[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) fb[j] = frag(st + j * 2048, lb0, lb1);
+    fa[0] = frag(st, la0, la1);
+    sc[0] = sa[0] * bsv;
+    v4f t[32];
+#pragma unroll
+    for (int k = 0; k < 34; ++k) {
+      if (k < 32) t[k] = mfma_fp8(fb[k & 3], fa[k >> 2]);
+      if ((k & 3) == 1 && (k >> 2) < 8) {
+        const int u = (k >> 2) & 3;
+        if (k < 16) dma16s(tileA + (size_t)kn * BK, offA[u], nbase + (wave + 8 * u) * 1024);
+        else dma16s(tileB + (size_t)kn * BK, offB[u], nbase + A_BYTES + (wave + 8 * u) * 1024);
+      }
+      if ((k & 3) == 0 && (k >> 2) + 1 < 8) {
+        const int i1 = (k >> 2) + 1;
+        fa[i1] = frag(st + i1 * 2048, la0, la1);
+        sc[i1] = sa[16 * i1] * bsv;
+      }
+      if (k >= 2) {
+        const int p = k - 2;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[p >> 2][p & 3][r] = fmaf(t[p][r], sc[p >> 2], acc[p >> 2][p & 3][r]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // ---- epilogue: bias, bf16 (RNE), each wave's 128x64 tile staged in LDS
+  // (16 KB per wave, chunk c of row r at slot c ^ (r & 7)) so that global
+  // stores are whole 128-byte rows
+  wait_vm<0>();  // the last iteration's copy must land before the stages are reused
+  __syncthreads();
+  uint8_t* ot = smem + wave * 16384;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int cl = j * 16 + 4 * g;
+    float bv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (bias != nullptr && bias_ld == 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int col = n0 + wn * 64 + cl + r;
+        bv[r] = col < N ? bias[col] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int rl = i * 16 + r16;
+      if (bias != nullptr && bias_ld != 0) {
+        const int row = m0 + wm * 128 + rl;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int col = n0 + wn * 64 + cl + r;
+          bv[r] = (row < M && col < N) ? bias[(int64_t)row * bias_ld + col] : 0.f;
+        }
+      }
+      uint2 o;
+      o.x = pack_bf16x2(acc[i][j][0] + bv[0], acc[i][j][1] + bv[1]);
+      o.y = pack_bf16x2(acc[i][j][2] + bv[2], acc[i][j][3] + bv[3]);
+      *reinterpret_cast<uint2*>(ot + rl * 128 + (((cl >> 3) ^ (rl & 7)) << 4) + (cl & 7) * 2) = o;
+    }
+  }
+  wave_lds_fence();
+  const int colw = n0 + wn * 64;
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const int rl = u * 8 + (lane >> 3), c = lane & 7;
+    const int row = m0 + wm * 128 + rl;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(ot + rl * 128 + ((c ^ (rl & 7)) << 4));
+    if (row >= M) continue;
+    uint16_t* dst = C + (size_t)row * N + colw + c * 8;
+    if (colw + c * 8 + 7 < N && (N & 7) == 0) {
+      *reinterpret_cast<u32x4*>(dst) = v;
+    } else {
+      const uint16_t* h = reinterpret_cast<const uint16_t*>(&v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (colw + c * 8 + e < N) dst[e] = h[e];
+    }
+  }
+}
+
 // out[m, n] = bf16(sum_s ws[s, m, n] + bias), four columns per thread
 __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ ws, int splits,
                                                      const float* __restrict__ bias, int64_t bias_ld,
@@ -374,6 +594,29 @@ extern "C" int64_t lfs_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K,
 }
 
 namespace {
+// compute units of the current device (the persistent kernel's grid)
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// 256x256 tiles (one workgroup per CU) when they fill the chip with at most
+// 15% of the last round idle, K is long enough to amortise the 64 KB
+// prologue copy, and the per-lane 32-bit copy offsets fit (256 rows of K bytes)
+bool use_big_tiles(int64_t M, int64_t N, int64_t K) {
+  const int64_t t = ((M + BIG - 1) / BIG) * ((N + BIG - 1) / BIG);
+  const int64_t cus = cu_count();
+  const int64_t rounds = (t + cus - 1) / cus;
+  return t >= cus && t * 100 >= rounds * cus * 85 && K >= 512 && 256 * K < (1ll << 31);
+}
+
 int fp8_gemm_impl(const void* a, const float* a_s, const void* b, const float* b_s, const float* bias,
                   int64_t bias_ld, void* c, int64_t M, int64_t N, int64_t K, int32_t splits,
                   void* workspace, int64_t workspace_bytes, void* stream) {
@@ -405,6 +648,13 @@ int fp8_gemm_impl(const void* a, const float* a_s, const void* b, const float* b
     kps = KT;
   }
   hipStream_t st = (hipStream_t)stream;
+  if (ws == nullptr && use_big_tiles(M, N, K)) {
+    const int64_t bm = (M + BIG - 1) / BIG, bn = (N + BIG - 1) / BIG;
+    hipLaunchKernelGGL(fp8_gemm_big, dim3((unsigned)(bm * bn)), dim3(512), 0, st, (const uint8_t*)a, a_s,
+                       (const uint8_t*)b, b_s, bias, bias_ld, (uint16_t*)c, (int)M, (int)N, (int)K, (int)bm,
+                       (int)bn);
+    return check_launch("fp8_gemm");
+  }
   // 128x128 tiles, two workgroups per CU.  (256x128 tiles with one
   // 8-wave workgroup per CU measured 10-15% slower on every benchmark shape.)
   hipLaunchKernelGGL((fp8_gemm_tile<128, 2, 16>), dim3((unsigned)(tiles_m128 * tiles_n), (unsigned)(used > 1 ? used : 1)),

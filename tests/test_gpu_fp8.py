@@ -153,9 +153,12 @@ def test_weight_dequant_bitexact(shape):
 # ---------------------------------------------------------------- fp8_gemm --
 def gemm_oracle(a, a_s, b, b_s, bias=None, rows=None):
     an, asn = codes(a), f32(a_s)
+    bn = None if bias is None else f32(bias)
     if rows is not None:
         an, asn = an[rows], asn[rows]
-    return F.fp8_gemm(an, asn, codes(b), f32(b_s), None if bias is None else f32(bias))
+        if bn is not None and bn.ndim == 2:
+            bn = bn[rows]
+    return F.fp8_gemm(an, asn, codes(b), f32(b_s), bn)
 
 
 def assert_close(got, ref, what=""):
@@ -237,6 +240,31 @@ def test_fp8_gemm_split_k(splits):
         assert_close(f32(got), gemm_oracle(a, a_s, b, b_s, bb), f"splits={splits} {what}")
         one = K.fp8_gemm(a, a_s, b, b_s, bb, splits=1)
         assert np.abs(f32(got) - f32(one)).max() <= 2e-2 + 1e-2 * np.abs(f32(one)).max()
+
+
+@pytest.mark.parametrize("M,N,Kd", [(4000, 4042, 1152), (4096, 4040, 640)])
+def test_fp8_gemm_big_tiles_ragged(M, N, Kd):
+    """Shapes with 256 tiles of 256x256 (the one-workgroup-per-CU kernel):
+    partial last row and column tiles, N not a multiple of 8 (element-wise
+    stores), 9 and 5 K blocks (a partial second scale chunk, a single
+    partial chunk), bias vector and per-row bias matrix; sampled rows
+    include both sides of every tile boundary near the edges."""
+    rng = np.random.default_rng(M + N + Kd)
+    ac = rng.integers(0, 256, (M, Kd), dtype=np.uint8)
+    bc = rng.integers(0, 256, (N, Kd), dtype=np.uint8)
+    ac[(ac & 0x7F) == 0x7F] = 0
+    bc[(bc & 0x7F) == 0x7F] = 0
+    a = torch.from_numpy(ac).view(torch.float8_e4m3fn).to(DEV)
+    b = torch.from_numpy(bc).view(torch.float8_e4m3fn).to(DEV)
+    a_s = torch.from_numpy(rng.uniform(1e-3, 1e-2, (M, Kd // 128)).astype(np.float32)).to(DEV)
+    b_s = torch.from_numpy(rng.uniform(1e-3, 1e-2, (-(-N // 128), Kd // 128)).astype(np.float32)).to(DEV)
+    bias = torch.from_numpy(rng.standard_normal(N).astype(np.float32)).to(DEV)
+    bm = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32)).to(DEV)
+    edge = [0, 1, 127, 128, 255, 256, 3839, 3840, M - 2, M - 1]
+    rows = np.unique(np.concatenate([edge, rng.choice(M, 100, replace=False)]))
+    for bb, what in ((None, "nobias"), (bias, "bias"), (bm, "bias matrix")):
+        got = f32(K.fp8_gemm(a, a_s, b, b_s, bb))[rows]
+        assert_close(got, gemm_oracle(a, a_s, b, b_s, bb, rows=rows), f"{M}x{N}x{Kd} {what}")
 
 
 @pytest.mark.parametrize("M", [1, 16, 128, 4096])
