@@ -235,20 +235,17 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
   // registers (fragments + scales), passes a second barrier, and only then
   // refills that same buffer with K block kt + NST, so NST blocks are in
   // flight while the MFMAs run (the LDS holds only NST stages).
+  // Every stage refill is issued, also past the last K block (it then
+  // re-copies block KT-1 into the stage just read, which is never read
+  // again), so that exactly NST-1 copy groups follow block kt's and the wait
+  // below is one constant count.
   load_scales(0);
 #pragma unroll
-  for (int s = 0; s < NST; ++s)
-    if (s < KT) issue(s, s);
+  for (int s = 0; s < NST; ++s) issue(min(s, KT - 1), s);
 
   for (int kt = 0; kt < KT; ++kt) {
     if (kt > 0 && kt % SCK == 0) load_scales(kt);  // old chunk last read before the previous B2
-    {
-      // K blocks issued after kt that may stay in flight
-      const int pending = min(NST - 1, KT - 1 - kt);
-      if (NST > 2 && pending >= 2) wait_vm<2 * LOADS>();
-      else if (pending >= 1) wait_vm<LOADS>();
-      else wait_vm<0>();
-    }
+    wait_vm<(NST - 1) * LOADS>();  // this wave's copies of block kt landed
     __syncthreads();  // B1: block kt (and the scale chunk) visible to every wave
     const uint8_t* st = smem + (kt % NST) * STAGE;
     const int kc = kt % SCK;
@@ -262,7 +259,11 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
     }
     wait_lgkm0();     // this wave's reads of the buffer have completed
     __syncthreads();  // B2: every wave is done with buffer kt % NST
-    if (kt + NST < KT) issue(kt + NST, kt % NST);
+    // refill buffer kt % NST with block kt + NST; its copies are spread over
+    // the MFMA sequence (one per two MFMAs) so that no wave waits behind a
+    // full load queue before its MFMAs.
+    const int kn = min(kt + NST, KT - 1);
+    const unsigned rbase = lds0 + (kt % NST) * STAGE;
     // MFMA k is issued, then the FMAs fold the product of MFMA k-2, which
     // has retired by then; scheduling fences keep the compiler from pulling
     // a fold up behind its own MFMA (which would idle the matrix core)
@@ -270,6 +271,11 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
 #pragma unroll
     for (int k = 0; k < 18; ++k) {
       if (k < 16) t[k] = mfma_fp8(fb[k & 3], fa[k >> 2]);
+      if ((k & 1) == 1 && (k >> 1) < LOADS) {
+        const int d = k >> 1;
+        if (d < A_PER_WAVE) dma16(srcA[d] + kn * BK, rbase + (wave + NW * d) * 1024);
+        else dma16(srcB[d - A_PER_WAVE] + kn * BK, rbase + A_BYTES + (wave + NW * (d - A_PER_WAVE)) * 1024);
+      }
       if (k >= 2) {
         const int p = k - 2;
 #pragma unroll
@@ -279,6 +285,7 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
     }
   }
 
+  wait_vm<0>();  // the trailing re-copies have landed before the stages are reused or the workgroup ends
   if (ws != nullptr) {
     // split-K partial: fp32, no bias; lane holds rows 16i + r16, columns
     // 16j + 4g .. +3 of its wave's 64x64 tile
