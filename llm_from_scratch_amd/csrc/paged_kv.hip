@@ -4,20 +4,19 @@
 // bf16, as allocated by engine/model_runner.py:184-190 of the reference; one
 // token's K (or V) row for all kv heads is Hkv*D*2 contiguous bytes.
 //
-// paged decode, phase 1 (one workgroup per (split, sequence)):
-//   The workgroup walks its chunk of the context in tiles of up to 128 tokens
-//   (a tile never crosses a KV block, so one block-table lookup per tile).
-//   Lane mapping inside a tile: lane j of a token row (j < Hkv*D/8) owns kv
-//   head j/(D/8) and dims (j%(D/8))*8 .. +7, so a token row is read with
-//   fully coalesced 16-byte loads; 256/(Hkv*D/8) tokens are in flight per
-//   pass.  Scores for the G query heads sharing a kv head are reduced over
-//   the D/8 lanes with an xor butterfly and staged in LDS; each wave then
-//   does the online-softmax update for a subset of heads (running max and
-//   sum in LDS, exp2 with log2(e) folded into q); V is streamed with the same
-//   lane mapping and accumulated in fp32 registers, rescaled per tile.
-//   The partial (unnormalised o, m, l) of the chunk goes to the workspace.
-// phase 2 (one workgroup per sequence): log-sum-exp merge of the chunks,
-//   normalise, bf16.  Padding rows (context_len 0) get zeros.
+// paged decode, phase 1 (paged_decode_split): one wave per (sequence, kv
+//   head, chunk of blocks_per_split KV blocks), four kv heads of one
+//   sequence and chunk per workgroup, grid (sequence, chunk, head group).
+//   The wave walks its chunk in tiles of up to 64 tokens that never cross a
+//   KV block (one block-table lookup per tile): S = K q^T on MFMA for the G
+//   query heads of its kv head, online softmax in the log2 domain, P through
+//   a wave-private LDS slice, P.V in fp32 registers.  Loads run two tiles
+//   ahead.  The partial (unnormalised o, m, l) of the chunk goes to the
+//   workspace, or, when the chunk is the whole context, the normalised bf16
+//   output is written directly.
+// phase 2 (paged_decode_merge, one workgroup per (head, sequence)):
+//   log-sum-exp merge of the chunks, normalise, bf16.  Padding rows
+//   (context_len 0) get zeros.
 #include "common.h"
 
 namespace lfs {
@@ -109,7 +108,11 @@ __global__ __launch_bounds__(256) void paged_decode_split(
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int kh = blockIdx.z * (blockDim.x >> 6) + wave;
   if (kh >= Hkv) return;
-  const int b = blockIdx.y, split = blockIdx.x;
+  // sequence index fastest: workgroups are dealt round-robin to the 8 XCDs,
+  // so consecutive ids must not be the splits of one sequence (split s would
+  // always land on XCD s mod 8, and short contexts leave the high splits
+  // empty, i.e. whole XCDs idle)
+  const int b = blockIdx.x, split = blockIdx.y;
   const int64_t Lc = min(ctx_lens[b], (int64_t)max_blocks * BS);
   const int64_t chunk = (int64_t)bps * BS;
   const int64_t t_begin = (int64_t)split * chunk;
@@ -460,8 +463,8 @@ extern "C" int lfs_paged_decode(const void* q, const void* k_cache, const void* 
   const float sl2 = scale * 1.4426950408889634f;
   if (max_splits > 0) {
     const int wpg = Hkv < 4 ? Hkv : 4;  // waves (kv heads) per workgroup
-    const dim3 grid((unsigned)max_splits, (unsigned)B, (unsigned)((Hkv + wpg - 1) / wpg));
-    LFS_REQUIRE(grid.z < 65536u, "paged_decode: too many kv heads");
+    const dim3 grid((unsigned)B, (unsigned)max_splits, (unsigned)((Hkv + wpg - 1) / wpg));
+    LFS_REQUIRE(grid.z < 65536u && grid.y < 65536u, "paged_decode: too many kv heads or splits");
     const dim3 block((unsigned)(64 * wpg));
     const int G = Hq / Hkv;
     const bool ok = D == 64
