@@ -34,7 +34,7 @@ METRIC = "FP8 block-GEMM TFLOP/s & paged-decode HBM GB/s (% of MI355X roofline)"
 # summarised in profiles/fp8_gemm_cfg2_sweep.md.  FETCH_SIZE is scaled by 2.0
 # and WRITE_SIZE by 1.0: a 256 MiB device copy in the same runs reads back
 # 128 MiB fetched and 256 MiB written.  Re-measure after kernel changes.
-GEMM_TRAFFIC_BYTES = 198.1e6
+GEMM_TRAFFIC_BYTES = 187.7e6
 
 
 def log(*a):
