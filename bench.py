@@ -110,6 +110,44 @@ def bench_act_quant(device, reps):
             "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "bytes": nbytes}
 
 
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def bench_prefill(device, reps):
+    """Varlen causal prefill attention at the cfg5 attention geometry (GQA
+    12/4, D = 64): 16 whole prompts of 2048 tokens (keys just stored,
+    contiguous), and 16 prompts of 2048 keys of which the first 1536 come
+    from the prefix cache (paged keys, block 256, 512 new queries each).
+    Algorithmic flop = 4 * D * Hq * (attended query-key pairs)."""
+    from llm_from_scratch_amd import kernels as K
+    Hq, Hkv, D, B, L, BS = 12, 4, 64, 16, 2048, 256
+    g = torch.Generator(device=device).manual_seed(9)
+    rnd = lambda *s: torch.randn(*s, generator=g, device=device).to(torch.bfloat16)
+    res = []
+    # whole prompts
+    cu = torch.arange(0, (B + 1) * L, L, dtype=torch.int32, device=device)
+    q, k, v = rnd(B * L, Hq, D), rnd(B * L, Hkv, D), rnd(B * L, Hkv, D)
+    t = timed_launches([lambda: K.flash_attn_varlen_func(q, k, v, cu, cu, L, L)], reps)[0]
+    pairs = B * L * (L + 1) // 2
+    fl = 4 * D * Hq * pairs
+    res.append({"case": f"{B} prompts x {L} tokens, contiguous keys", "us": t * 1e6, "TFLOP/s": fl / t / 1e12,
+                "frac": fl / t / 1e12 / BF16_PEAK_TFLOPS, "flop": fl})
+    del q, k, v
+    # cached prefix: 1536 cached + 512 new tokens per sequence, keys from the pool
+    lq = 512
+    nb = L // BS
+    kc, vc = rnd(B * nb, BS, Hkv, D), rnd(B * nb, BS, Hkv, D)
+    bt = torch.randperm(B * nb, generator=g, device=device).to(torch.int32).view(B, nb).contiguous()
+    cu_q = torch.arange(0, (B + 1) * lq, lq, dtype=torch.int32, device=device)
+    q = rnd(B * lq, Hq, D)
+    t = timed_launches([lambda: K.flash_attn_varlen_func(q, kc, vc, cu_q, cu, lq, L, block_table=bt)], reps)[0]
+    pairs = B * (lq * (L - lq) + lq * (lq + 1) // 2)
+    fl = 4 * D * Hq * pairs
+    res.append({"case": f"{B} prompts x {L} keys, {L - lq} from the prefix cache (paged, block {BS})",
+                "us": t * 1e6, "TFLOP/s": fl / t / 1e12, "frac": fl / t / 1e12 / BF16_PEAK_TFLOPS, "flop": fl})
+    return res
+
+
 def bench_decode(name, device, reps, flush_buf):
     from llm_from_scratch_amd import kernels as K
     from llm_from_scratch_amd import workloads as W
@@ -220,8 +258,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip decode / act_quant lines")
-    ap.add_argument("--extras", default="act_quant,cfg3,cfg4,cfg5",
-                    help="comma list of extra lines: act_quant, cfg3, cfg4 (paged decode), cfg5 (decode step)")
+    ap.add_argument("--extras", default="act_quant,cfg3,cfg4,prefill,cfg5",
+                    help="comma list of extra lines: act_quant, cfg3, cfg4 (paged decode), prefill "
+                         "(varlen prefill attention), cfg5 (decode step)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 4 plain device copies of 256 MiB (a known-traffic kernel for "
                          "scaling FETCH_SIZE / WRITE_SIZE counters)")
@@ -292,6 +331,9 @@ def main():
                 out["paged_decode"].append(bench_decode(name, dev, 20, flush_buf))
             del flush_buf
             torch.cuda.empty_cache()
+        if "prefill" in extras:
+            log("bench: prefill attention")
+            out["prefill_attention"] = bench_prefill(dev, 10)
         if "cfg5" in extras:
             log("bench: cfg5 decode step")
             out["decode_step"] = bench_decode_step(dev, 20)

@@ -36,6 +36,11 @@
  *                           decode call of the same absent layer; math of
  *                           model/attention/GQA.py:118-130, metadata contract
  *                           engine/model_runner.py:253-278 and :288-312
+ *   lfs_prefill_attention   varlen causal prefill attention, the
+ *                           flash_attn_varlen_func(..., causal=True) call the
+ *                           reference names at engine/model_runner.py:291-292
+ *                           (metadata :202-249; paged keys on a prefix-cache
+ *                           hit, :231-237); math of model/attention/GQA.py:118-130
  * Fused row kernels of the decode step around those calls (each replaces a
  * chain of torch ops of the reference model):
  *   lfs_add_rmsnorm         RMSNorm with fused residual add, model/utils.py:53-67
@@ -56,7 +61,7 @@
 extern "C" {
 #endif
 
-#define LFS_ABI_VERSION 2
+#define LFS_ABI_VERSION 3
 
 /* argument errors (negative); launch errors are positive hipError_t values */
 #define LFS_EINVAL (-1)
@@ -161,6 +166,26 @@ int lfs_paged_decode(const void* q, const void* k_cache, const void* v_cache,
                      int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                      int32_t block_size, int64_t num_blocks, int32_t max_blocks, float scale,
                      int32_t blocks_per_split, void* stream);
+
+/*
+ * Varlen causal prefill attention, GQA (G = Hq / Hkv):
+ *   sequence i: queries q[cu_q[i] .. cu_q[i+1]) at positions lk-lq .. lk-1 of
+ *   its context of lk = cu_k[i+1] - cu_k[i] keys; query position p:
+ *   o[:, h] = sum_{t <= p} softmax_t(scale * q[:, h] . K_i[t, h/G]) V_i[t, h/G]
+ *   K_i[t] = k[cu_k[i] + t]                          (block_tables == NULL;
+ *            k, v bf16 [cu_k[B], Hkv, D])
+ *   K_i[t] = k[block_tables[i][t / BS] * BS + t % BS] (paged; k, v the pool
+ *            bf16 [num_slots / BS, BS, Hkv, D], block_tables int32
+ *            [B, bt_stride]; entries outside [0, num_slots / BS) read slot 0)
+ * q, out: bf16 [cu_q[B], Hq, D] contiguous; cu_seqlens int32 [B + 1];
+ * max_seqlen_q >= every lq (sets the grid, so a fixed value keeps the call
+ * capturable).  D in {64, 128}; Hq % Hkv == 0, Hq / Hkv <= 8.
+ */
+int lfs_prefill_attention(const void* q, const void* k, const void* v, const int32_t* cu_seqlens_q,
+                          const int32_t* cu_seqlens_k, const int32_t* block_tables, int64_t bt_stride,
+                          int32_t block_size, int64_t num_slots, void* out, int64_t B,
+                          int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                          int32_t max_seqlen_q, float scale, void* stream);
 
 /*
  * add_rmsnorm, per row t of x: bf16 [T, d]:

@@ -1,0 +1,275 @@
+// Varlen causal prefill attention for gfx950 (the prefill half of the
+// engine step).
+//
+// Sequence i of the batch has lq = cu_q[i+1] - cu_q[i] new query tokens
+// (rows cu_q[i] .. of q) at positions lk - lq .. lk - 1 of its context of
+// lk = cu_k[i+1] - cu_k[i] keys; query token p attends to keys 0 .. p
+// (causal, aligned to the end of the context, as with a cached prefix).
+// Key t of sequence i is row cu_k[i] + t of k / v (contiguous mode) or slot
+// block_table[i][t / BS] * BS + t % BS of the KV pool (paged mode, a
+// prefix-cache hit: the cached blocks and the just-stored new tokens).
+//
+// One workgroup per (sequence, tile of 16 query tokens, kv head), one wave
+// per query head of the kv head's group (G waves).  Per tile of 32 keys:
+//   S^T = K Q^T   v_mfma_f32_16x16x32_bf16, K as the A operand loaded from
+//                 HBM in operand layout (lane l: key l % 16, dims
+//                 32c + 8(l / 16) .. +7), Q^T as the B operand (preloaded);
+//                 lane l ends with the scores of query (l % 16) for keys
+//                 4(l / 16) .. +3 of each 16-key half;
+//   softmax       online, log2 domain, max / sum over the four lanes of a
+//                 query with xor 16 / 32;
+//   O^T += V^T P^T  P^T is the B operand straight from the softmax registers:
+//                 MFMA k-index 8g + j (g = l / 16) stands for key 4g + j
+//                 (j < 4) or 16 + 4g + j - 4 -- the same permutation of the
+//                 32 keys on both operands leaves the sum unchanged; V^T is
+//                 the A operand, read from a transposed LDS copy of the V tile
+//                 ([dim][key]) that the G waves share, two 8-byte reads per
+//                 fragment.
+// The V tile is double-buffered in LDS with one barrier per key tile; K and
+// V of the next tile are loaded while the current one is computed.
+#include "common.h"
+
+namespace lfs {
+namespace {
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int KT = 32;          // keys per tile
+constexpr int QT = 16;          // query tokens per workgroup
+constexpr int VT_PITCH = 72;    // bytes per dim row of the transposed V tile (32 keys + pad)
+
+template <int D, int G>
+__global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k, const int32_t* __restrict__ bt,
+    int64_t bt_stride, int BS, int64_t num_slots, uint16_t* __restrict__ out, int Hkv, int qtiles,
+    float scale_log2) {
+  constexpr int NDC = D / 32;    // 32-dim chunks (MFMA k steps of S)
+  constexpr int NDB = D / 16;    // 16-dim blocks of O^T
+  constexpr int VCH = KT * D / 8;                    // 16-byte V chunks per tile
+  constexpr int VPT = (VCH + 64 * G - 1) / (64 * G); // chunks per thread
+  __shared__ __attribute__((aligned(16))) uint8_t vt[2][D * VT_PITCH];
+
+  const int i = blockIdx.x / qtiles, tq0 = (blockIdx.x % qtiles) * QT;
+  const int kh = blockIdx.y;
+  const int q0 = cu_q[i], lq = cu_q[i + 1] - q0;
+  if (tq0 >= lq) return;
+  const int k0 = cu_k[i], lk = cu_k[i + 1] - k0;
+  const int off = lk - lq;  // position of query token 0
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int h = kh * G + wave, Hq = Hkv * G;
+  const int c16 = lane & 15, g = lane >> 4;
+  const int64_t row = (int64_t)Hkv * D;  // elements per token row of k / v
+
+  // element offset of key t's row (head kh); t clamped into the context,
+  // invalid block-table entries read slot 0 (their keys are masked or the
+  // caller's tables are wrong -- never out of bounds)
+  auto key_off = [&](int t) -> int64_t {
+    t = min(t, lk - 1);
+    int64_t slot;
+    if (bt != nullptr) {
+      const int32_t blk = bt[(int64_t)i * bt_stride + min((int64_t)(t / BS), bt_stride - 1)];
+      slot = (int64_t)blk * BS + t % BS;
+      if (blk < 0 || slot >= num_slots) slot = 0;
+    } else {
+      slot = (int64_t)k0 + t;
+    }
+    return slot * row + (int64_t)kh * D;
+  };
+
+  // Q^T (B operand): lane l supplies query tq0 + l % 16, dims 32c + 8g .. +7
+  v8bf qb[NDC];
+  {
+    const int tq = tq0 + c16;
+#pragma unroll
+    for (int c = 0; c < NDC; ++c) {
+      uint4 w = make_uint4(0, 0, 0, 0);
+      if (tq < lq) w = *reinterpret_cast<const uint4*>(q + ((int64_t)(q0 + tq) * Hq + h) * D + c * 32 + g * 8);
+      qb[c] = __builtin_bit_cast(v8bf, w);
+    }
+  }
+  // this lane's query position; rows past lq are computed (finite) and not stored
+  const int qp = min(off + tq0 + c16, lk - 1);
+  // keys up to the last query of the tile
+  const int nkt = (min(lk, off + tq0 + QT) + KT - 1) / KT;
+
+  auto load_k = [&](uint4 (&ka)[2][NDC], int t0) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const int64_t o = key_off(t0 + 16 * kb + c16);
+#pragma unroll
+      for (int c = 0; c < NDC; ++c) ka[kb][c] = *reinterpret_cast<const uint4*>(k + o + c * 32 + g * 8);
+    }
+  };
+  // V chunk u of a tile: key u / (D / 8), dims (u % (D / 8)) * 8 .. +7
+  auto load_v = [&](uint4 (&vr)[VPT], int t0) {
+#pragma unroll
+    for (int e = 0; e < VPT; ++e) {
+      const int u = threadIdx.x + 64 * G * e;
+      vr[e] = make_uint4(0, 0, 0, 0);
+      if (u < VCH) vr[e] = *reinterpret_cast<const uint4*>(v + key_off(t0 + u / (D / 8)) + (u % (D / 8)) * 8);
+    }
+  };
+  auto store_vt = [&](const uint4 (&vr)[VPT], int buf) {
+#pragma unroll
+    for (int e = 0; e < VPT; ++e) {
+      const int u = threadIdx.x + 64 * G * e;
+      if (u < VCH) {
+        const int key = u / (D / 8), d0 = (u % (D / 8)) * 8;
+        const uint16_t* hv = reinterpret_cast<const uint16_t*>(&vr[e]);
+#pragma unroll
+        for (int x = 0; x < 8; ++x)
+          *reinterpret_cast<uint16_t*>(&vt[buf][(d0 + x) * VT_PITCH + key * 2]) = hv[x];
+      }
+    }
+  };
+
+  v4f o[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) o[db] = v4f{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  uint4 ka[2][NDC], vr[VPT];
+  load_k(ka, 0);
+  load_v(vr, 0);
+  for (int j = 0; j < nkt; ++j) {
+    const int t0 = j * KT;
+    const int buf = j & 1;
+    store_vt(vr, buf);
+    // V^T tile j visible to every wave.  The buffer written next (tile j+1)
+    // was last read in tile j-1, which every wave finished before this barrier.
+    __syncthreads();
+    uint4 kc[2][NDC];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int c = 0; c < NDC; ++c) kc[kb][c] = ka[kb][c];
+    if (j + 1 < nkt) {
+      load_k(ka, t0 + KT);
+      load_v(vr, t0 + KT);
+    }
+
+    // ---- S^T for the two 16-key halves
+    float s[2][4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      v4f sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < NDC; ++c)
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, kc[kb][c]), qb[c], sc, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int kp = t0 + 16 * kb + 4 * g + r;
+        s[kb][r] = kp <= qp ? sc[r] * scale_log2 : -INFINITY;
+        tmax = fmaxf(tmax, s[kb][r]);
+      }
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m_run, tmax);  // finite: key 0 is never masked
+    const float alpha = exp2f(m_run - m_new);
+    float psum = 0.f;
+    float p[2][4];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        p[kb][r] = exp2f(s[kb][r] - m_new);
+        psum += p[kb][r];
+      }
+    psum += __shfl_xor(psum, 16, 64);
+    psum += __shfl_xor(psum, 32, 64);
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+
+    // ---- O^T = O^T * alpha + V^T P^T
+    v8bf pb;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      pb[r] = (__bf16)p[0][r];
+      pb[4 + r] = (__bf16)p[1][r];
+    }
+    const uint8_t* vb = vt[buf];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const int dim = db * 16 + c16;
+      const uint2 lo = *reinterpret_cast<const uint2*>(vb + dim * VT_PITCH + (4 * g) * 2);
+      const uint2 hi = *reinterpret_cast<const uint2*>(vb + dim * VT_PITCH + (16 + 4 * g) * 2);
+      const uint4 w = make_uint4(lo.x, lo.y, hi.x, hi.y);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[db][r] *= alpha;
+      o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, w), pb, o[db], 0, 0, 0);
+    }
+  }
+
+  // ---- normalise and store: lane l holds query tq0 + l % 16, dims 16db + 4g .. +3
+  const int tq = tq0 + c16;
+  if (tq < lq) {
+    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+    uint16_t* dst = out + ((int64_t)(q0 + tq) * Hq + h) * D;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      uint2 w;
+      w.x = pack_bf16x2(o[db][0] * inv, o[db][1] * inv);
+      w.y = pack_bf16x2(o[db][2] * inv, o[db][3] * inv);
+      *reinterpret_cast<uint2*>(dst + db * 16 + 4 * g) = w;
+    }
+  }
+}
+
+template <int D>
+bool launch_prefill(int G, dim3 grid, hipStream_t st, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                    const int32_t* cu_q, const int32_t* cu_k, const int32_t* bt, int64_t bts, int BS,
+                    int64_t num_slots, uint16_t* out, int Hkv, int qtiles, float sl2) {
+#define LFS_PG(GG)                                                                                         \
+  case GG:                                                                                                 \
+    hipLaunchKernelGGL((prefill_attention_kernel<D, GG>), grid, dim3(64 * GG), 0, st, q, k, v, cu_q, cu_k, \
+                       bt, bts, BS, num_slots, out, Hkv, qtiles, sl2);                                     \
+    return true;
+  switch (G) {
+    LFS_PG(1) LFS_PG(2) LFS_PG(3) LFS_PG(4) LFS_PG(5) LFS_PG(6) LFS_PG(7) LFS_PG(8)
+    default: return false;
+  }
+#undef LFS_PG
+}
+
+}  // namespace
+}  // namespace lfs
+
+using namespace lfs;
+
+extern "C" int lfs_prefill_attention(const void* q, const void* k, const void* v, const int32_t* cu_seqlens_q,
+                                     const int32_t* cu_seqlens_k, const int32_t* block_tables,
+                                     int64_t bt_stride, int32_t block_size, int64_t num_slots, void* out,
+                                     int64_t B, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                     int32_t max_seqlen_q, float scale, void* stream) {
+  const int Hq = num_q_heads, Hkv = num_kv_heads, D = head_dim;
+  LFS_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && max_seqlen_q >= 0, "prefill_attention: bad shape");
+  LFS_REQUIRE(D == 64 || D == 128, "prefill_attention: head_dim must be 64 or 128 (got %d)", D);
+  LFS_REQUIRE(Hq % Hkv == 0 && Hq / Hkv <= 8,
+              "prefill_attention: num_q_heads (%d) must be a multiple of num_kv_heads (%d), ratio <= 8", Hq, Hkv);
+  if (B == 0 || max_seqlen_q == 0) return 0;
+  LFS_REQUIRE(q && k && v && cu_seqlens_q && cu_seqlens_k && out, "prefill_attention: null pointer");
+  LFS_REQUIRE(((((uintptr_t)q) | ((uintptr_t)k) | ((uintptr_t)v) | ((uintptr_t)out)) & 15u) == 0,
+              "prefill_attention: q, k, v and out must be 16-byte aligned");
+  if (block_tables != nullptr) {
+    LFS_REQUIRE(block_size > 0 && num_slots > 0 && bt_stride > 0, "prefill_attention: bad paged KV geometry");
+  }
+  const int64_t qtiles = ((int64_t)max_seqlen_q + QT - 1) / QT;
+  LFS_REQUIRE(B * qtiles < (1ll << 31) && Hkv < 65536, "prefill_attention: grid too large");
+  const dim3 grid((unsigned)(B * qtiles), (unsigned)Hkv);
+  const float sl2 = scale * 1.4426950408889634f;
+  hipStream_t st = (hipStream_t)stream;
+  const int G = Hq / Hkv;
+  const bool ok = D == 64
+      ? launch_prefill<64>(G, grid, st, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, cu_seqlens_q,
+                           cu_seqlens_k, block_tables, bt_stride, block_size, num_slots, (uint16_t*)out, Hkv,
+                           (int)qtiles, sl2)
+      : launch_prefill<128>(G, grid, st, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
+                            cu_seqlens_q, cu_seqlens_k, block_tables, bt_stride, block_size, num_slots,
+                            (uint16_t*)out, Hkv, (int)qtiles, sl2);
+  LFS_REQUIRE(ok, "prefill_attention: unsupported group size %d", G);
+  return check_launch("prefill_attention");
+}

@@ -11,8 +11,10 @@ model/architecture/mlp.py:48-67).  Every projection is an FP8Linear.
 
 The attention layer is the one engine/model_runner.py:8 imports but the
 reference does not ship: it writes the new K/V with store_kvcache at
-Context.slot_mapping and, in decode, attends over the paged pool with
-paged_attention_decode (Context.context_lens / block_tables).
+Context.slot_mapping; in decode it attends over the paged pool with
+paged_attention_decode (Context.context_lens / block_tables), in prefill
+with flash_attn_varlen_func (Context.cu_seqlens_q / _k; the pool through
+block_tables on a prefix-cache hit, else the just-stored keys).
 
 Interface (nano-vLLM style, as the runner expects):
     hidden = model(input_ids [T], positions [T])      # bf16 [T, d_model]
@@ -132,10 +134,16 @@ class PagedGQAAttention(nn.Module):
                                        positions, self.num_heads, self.num_kv_heads, self.q_norm.eps,
                                        self.k_cache, self.v_cache, ctx.slot_mapping)
         if ctx.is_prefill:
-            flat = (-1, self.num_kv_heads, self.head_dim)
-            k = self.k_cache.view(flat)[ctx.slot_mapping]
-            v = self.v_cache.view(flat)[ctx.slot_mapping]
-            o = self._prefill_attention(q, k, v, ctx)
+            if ctx.block_tables is not None:  # prefix-cache hit: keys from the pool
+                o = kernels.flash_attn_varlen_func(q, self.k_cache, self.v_cache, ctx.cu_seqlens_q,
+                                                   ctx.cu_seqlens_k, ctx.max_seqlen_q, ctx.max_seqlen_k,
+                                                   self.scale, block_table=ctx.block_tables)
+            else:  # whole prompts: the keys just stored, in slot order
+                flat = (-1, self.num_kv_heads, self.head_dim)
+                k = self.k_cache.view(flat)[ctx.slot_mapping]
+                v = self.v_cache.view(flat)[ctx.slot_mapping]
+                o = kernels.flash_attn_varlen_func(q, k, v, ctx.cu_seqlens_q, ctx.cu_seqlens_k,
+                                                   ctx.max_seqlen_q, ctx.max_seqlen_k, self.scale)
         else:
             o = kernels.paged_attention_decode(q, self.k_cache, self.v_cache, ctx.context_lens,
                                                ctx.block_tables, self.scale)
@@ -143,34 +151,6 @@ class PagedGQAAttention(nn.Module):
         out = self.output_proj(o)
         if trace is not None:
             trace.update(qkv=qkv, q=q, att_o=o, att_out=out)
-        return out
-
-    def _prefill_attention(self, q, k, v, ctx) -> torch.Tensor:
-        """Causal attention of each prompt over its full context (cached
-        prefix gathered from the pool).  fp32, one sequence at a time."""
-        G = self.num_heads // self.num_kv_heads
-        cu_q = ctx.cu_seqlens_q.tolist()
-        cu_k = ctx.cu_seqlens_k.tolist()
-        out = torch.empty_like(q)
-        BS = self.k_cache.size(1)
-        for i in range(len(cu_q) - 1):
-            qs, qe, lk = cu_q[i], cu_q[i + 1], cu_k[i + 1] - cu_k[i]
-            lq = qe - qs
-            if ctx.block_tables is not None and lk > lq:
-                t = torch.arange(lk, device=q.device)
-                blocks = ctx.block_tables[i].long()[t // BS]
-                K = self.k_cache[blocks, t % BS]
-                V = self.v_cache[blocks, t % BS]
-            else:
-                K, V = k[qs:qe], v[qs:qe]
-            Kh = K.float().repeat_interleave(G, dim=1).transpose(0, 1)  # [Hq, lk, D]
-            Vh = V.float().repeat_interleave(G, dim=1).transpose(0, 1)
-            Q = q[qs:qe].float().transpose(0, 1)                          # [Hq, lq, D]
-            s = torch.matmul(Q, Kh.transpose(1, 2).contiguous()) * self.scale
-            pos_q = torch.arange(lk - lq, lk, device=q.device)
-            mask = torch.arange(lk, device=q.device)[None, :] <= pos_q[:, None]
-            s = s.masked_fill(~mask, float("-inf"))
-            out[qs:qe] = torch.matmul(torch.softmax(s, -1), Vh).transpose(0, 1).to(out.dtype)
         return out
 
 

@@ -275,6 +275,54 @@ def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     return o
 
 
+def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                           cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor,
+                           max_seqlen_q: int, max_seqlen_k: int, softmax_scale: Optional[float] = None,
+                           causal: bool = True, block_table: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Varlen causal prefill attention, the call engine/model_runner.py:291-292
+    of the reference names for its prefill step (same argument meaning).
+
+    q: bf16 [total_q, Hq, D]; cu_seqlens_q / cu_seqlens_k: int32 [B + 1].
+    Without ``block_table``, k and v are bf16 [total_k, Hkv, D] (key t of
+    sequence i is row cu_seqlens_k[i] + t); with it (int32 [B, max_blocks],
+    a prefix-cache hit) they are the paged caches [num_blocks, block_size,
+    Hkv, D].  Queries of sequence i sit at the last lq positions of its lk
+    keys and attend to keys up to their own position.  softmax_scale
+    defaults to 1/sqrt(D).  Returns bf16 [total_q, Hq, D]."""
+    assert causal, "only causal prefill attention is provided"
+    assert q.dim() == 3 and q.is_contiguous(), "q must be contiguous [total_q, Hq, D]"
+    assert k.is_contiguous() and v.is_contiguous() and k.shape == v.shape
+    _on_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k)
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _dtype(t, torch.bfloat16, n)
+    _dtype(cu_seqlens_q, torch.int32, "cu_seqlens_q")
+    _dtype(cu_seqlens_k, torch.int32, "cu_seqlens_k")
+    assert cu_seqlens_q.is_contiguous() and cu_seqlens_k.is_contiguous()
+    assert cu_seqlens_q.numel() == cu_seqlens_k.numel() >= 1
+    B = cu_seqlens_q.numel() - 1
+    _, Hq, D = q.shape
+    if block_table is not None:
+        assert k.dim() == 4, "with block_table, k and v are the paged caches [NB, BS, Hkv, D]"
+        _on_gpu(block_table)
+        _dtype(block_table, torch.int32, "block_table")
+        assert block_table.dim() == 2 and block_table.stride(1) == 1 and block_table.size(0) == B
+        NB, BS, Hkv, Dk = k.shape
+        bt_ptr, bt_stride, num_slots = _ptr(block_table), block_table.stride(0), NB * BS
+    else:
+        assert k.dim() == 3, "k and v must be [total_k, Hkv, D]"
+        _, Hkv, Dk = k.shape
+        bt_ptr, bt_stride, BS, num_slots = None, 0, 0, k.size(0)
+    assert Dk == D, "head_dim mismatch between q and k"
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(D)
+    o = torch.empty_like(q)
+    rc = _lib.load().lfs_prefill_attention(_ptr(q), _ptr(k), _ptr(v), _ptr(cu_seqlens_q), _ptr(cu_seqlens_k),
+                                           bt_ptr, bt_stride, BS, num_slots, _ptr(o), B, Hq, Hkv, D,
+                                           int(max_seqlen_q), float(softmax_scale), _stream(q))
+    _lib.check(rc, "flash_attn_varlen_func")
+    return o
+
+
 # ------------------------------------------------- fused decode-step rows --
 def add_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
                 residual: Optional[torch.Tensor] = None, out: bool = True, quant: bool = False):

@@ -16,6 +16,12 @@ Pinning (tests/test_oracle_paged.py):
                     constant V gives V; invariant under a permutation of the
                     block pool with remapped tables; L=0 gives zeros.
   decode_slots   -- brute force slot(b,t) = bt[b][t//BS]*BS + t%BS.
+  prefill_attention -- a whole prompt (lq == lk) equals ``sdpa`` with the
+                    lower-triangular mask (the reference's causal
+                    scaled_dot_product_attention, utils.py:51-63 with
+                    GQA.py:126-130's causal mask); a cached prefix (lq < lk)
+                    equals the last lq rows of the whole prompt's result;
+                    paged keys equal the same keys stored contiguously.
 """
 from __future__ import annotations
 
@@ -102,4 +108,40 @@ def decode_slots(block_tables, context_lens, block_size):
         L = int(L)
         if L > 0:
             out[b] = int(block_tables[b][(L - 1) // block_size]) * block_size + (L - 1) % block_size
+    return out
+
+
+def prefill_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, scale, block_tables=None, dtype=np.float64):
+    """Varlen causal prefill attention (the flash_attn_varlen_func call named
+    at engine/model_runner.py:291-292, causal=True).
+
+    Sequence i: queries q[cu_q[i]:cu_q[i+1]] (lq tokens) at positions
+    lk-lq .. lk-1 of its context of lk = cu_k[i+1]-cu_k[i] keys; query p
+    attends to keys 0..p.  Keys: k[cu_k[i]:cu_k[i+1]] (contiguous, [Tk, Hkv,
+    D]) or, with block_tables, gathered from the pool k = [NB, BS, Hkv, D].
+    GQA head map h -> h // (Hq/Hkv).  Returns [Tq, Hq, D]."""
+    q = np.asarray(q, dtype)
+    Tq, Hq, D = q.shape
+    Hkv = k.shape[-2]
+    G = Hq // Hkv
+    out = np.zeros((Tq, Hq, D), dtype)
+    cu_q = np.asarray(cu_seqlens_q, np.int64)
+    cu_k = np.asarray(cu_seqlens_k, np.int64)
+    for i in range(len(cu_q) - 1):
+        qs, qe = int(cu_q[i]), int(cu_q[i + 1])
+        lq, lk = qe - qs, int(cu_k[i + 1] - cu_k[i])
+        if lq == 0:
+            continue
+        if block_tables is not None:
+            K = gather_kv(k, block_tables[i], lk)
+            V = gather_kv(v, block_tables[i], lk)
+        else:
+            K = k[int(cu_k[i]):int(cu_k[i + 1])]
+            V = v[int(cu_k[i]):int(cu_k[i + 1])]
+        Kh = np.repeat(np.asarray(K, dtype).transpose(1, 0, 2), G, axis=0)  # [Hq, lk, D]
+        Vh = np.repeat(np.asarray(V, dtype).transpose(1, 0, 2), G, axis=0)
+        pos_q = np.arange(lk - lq, lk)
+        mask = np.arange(lk)[None, :] <= pos_q[:, None]                      # [lq, lk]
+        out[qs:qe] = sdpa(q[qs:qe].transpose(1, 0, 2), Kh, Vh, mask=mask, scale=scale,
+                          dtype=dtype).transpose(1, 0, 2)
     return out

@@ -127,3 +127,80 @@ def test_decode_slots_brute_force():
         # enumerate every slot of the sequence in order; the newest is the last
         slots = [int(bt[b, j]) * BS + o for j in range(-(-L // BS)) for o in range(BS)][:L]
         assert got[b] == slots[-1]
+
+
+def _prefill_batch(rng, lens_q, lens_k, Hq, Hkv, D):
+    cu_q = np.concatenate([[0], np.cumsum(lens_q)]).astype(np.int32)
+    cu_k = np.concatenate([[0], np.cumsum(lens_k)]).astype(np.int32)
+    q = rng.standard_normal((int(cu_q[-1]), Hq, D)).astype(np.float32)
+    k = rng.standard_normal((int(cu_k[-1]), Hkv, D)).astype(np.float32)
+    v = rng.standard_normal((int(cu_k[-1]), Hkv, D)).astype(np.float32)
+    return q, k, v, cu_q, cu_k
+
+
+def test_prefill_attention_whole_prompt_is_causal_sdpa():
+    """lq == lk: per (sequence, head) the reference's causal SDPA (the
+    snapshot-pinned sdpa with a lower-triangular mask), GQA map h -> h // G."""
+    rng = np.random.default_rng(5)
+    Hq, Hkv, D = 8, 2, 16
+    lens = [1, 7, 20]
+    q, k, v, cu_q, cu_k = _prefill_batch(rng, lens, lens, Hq, Hkv, D)
+    out = P.prefill_attention(q, k, v, cu_q, cu_k, scale=0.3)
+    G = Hq // Hkv
+    for i, L in enumerate(lens):
+        s = slice(int(cu_q[i]), int(cu_q[i + 1]))
+        for h in range(Hq):
+            ref = P.sdpa(q[s, h], k[s, h // G], v[s, h // G], mask=np.tril(np.ones((L, L), bool)), scale=0.3)
+            np.testing.assert_allclose(out[s, h], ref, rtol=1e-12, atol=1e-12)
+
+
+def test_prefill_attention_brute_force_tiny():
+    """Scalar loops with math.exp: query p of a sequence attends to keys 0..p."""
+    import math
+    rng = np.random.default_rng(6)
+    Hq, Hkv, D = 4, 2, 3
+    lens = [3, 4]
+    q, k, v, cu_q, cu_k = _prefill_batch(rng, lens, lens, Hq, Hkv, D)
+    out = P.prefill_attention(q, k, v, cu_q, cu_k, scale=0.5)
+    for i in range(len(lens)):
+        base = int(cu_q[i])
+        for p in range(lens[i]):
+            for h in range(Hq):
+                kv = h // (Hq // Hkv)
+                sc = [0.5 * sum(float(q[base + p, h, d]) * float(k[base + t, kv, d]) for d in range(D)) for t in range(p + 1)]
+                mx = max(sc)
+                w = [math.exp(x - mx) for x in sc]
+                ref = [sum(w[t] * float(v[base + t, kv, d]) for t in range(p + 1)) / sum(w) for d in range(D)]
+                np.testing.assert_allclose(out[base + p, h], ref, rtol=1e-12, atol=1e-12)
+
+
+def test_prefill_attention_cached_prefix_and_paged_keys():
+    """A cached prefix (lq < lk) gives the last lq rows of the whole prompt's
+    result; keys gathered from a randomly permuted pool give the same as the
+    contiguous keys."""
+    rng = np.random.default_rng(7)
+    Hq, Hkv, D, BS, NB = 6, 3, 16, 16, 40
+    lens_k = [33, 16, 70]
+    lens_q = [5, 16, 1]
+    qf, k, v, cu_qf, cu_k = _prefill_batch(rng, lens_k, lens_k, Hq, Hkv, D)
+    full = P.prefill_attention(qf, k, v, cu_qf, cu_k, scale=0.25)
+    # the last lq query tokens of each prompt
+    rows = np.concatenate([np.arange(int(cu_qf[i + 1]) - lq, int(cu_qf[i + 1])) for i, lq in enumerate(lens_q)])
+    cu_q = np.concatenate([[0], np.cumsum(lens_q)]).astype(np.int32)
+    part = P.prefill_attention(qf[rows], k, v, cu_q, cu_k, scale=0.25)
+    np.testing.assert_allclose(part, full[rows], rtol=1e-12, atol=1e-12)
+    # same keys in a pool through block tables
+    maxb = max(-(-L // BS) for L in lens_k)
+    perm = rng.permutation(NB)
+    bt = np.full((len(lens_k), maxb), -1, np.int32)
+    kc = rng.standard_normal((NB, BS, Hkv, D)) * 100
+    vc = rng.standard_normal((NB, BS, Hkv, D)) * 100
+    pos = 0
+    for i, L in enumerate(lens_k):
+        nb = -(-L // BS)
+        bt[i, :nb] = perm[pos:pos + nb]
+        pos += nb
+        slots = np.array([bt[i, t // BS] * BS + t % BS for t in range(L)], np.int64)
+        P.store_kvcache(k[int(cu_k[i]):int(cu_k[i + 1])], v[int(cu_k[i]):int(cu_k[i + 1])], kc, vc, slots)
+    paged = P.prefill_attention(qf[rows], kc, vc, cu_q, cu_k, scale=0.25, block_tables=bt)
+    np.testing.assert_allclose(paged, full[rows], rtol=1e-12, atol=1e-12)
