@@ -41,6 +41,9 @@
  *                           reference names at engine/model_runner.py:291-292
  *                           (metadata :202-249; paged keys on a prefix-cache
  *                           hit, :231-237); math of model/attention/GQA.py:118-130
+ *   lfs_sample_gumbel       temperature + Gumbel-max sampling,
+ *                           utils/sampler.py:35-53 (Sampler.forward), with
+ *                           its Exp(1) noise from Philox4x32-10
  * Fused row kernels of the decode step around those calls (each replaces a
  * chain of torch ops of the reference model):
  *   lfs_add_rmsnorm         RMSNorm with fused residual add, model/utils.py:53-67
@@ -186,6 +189,18 @@ int lfs_prefill_attention(const void* q, const void* k, const void* v, const int
                           int32_t block_size, int64_t num_slots, void* out, int64_t B,
                           int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                           int32_t max_seqlen_q, float scale, void* stream);
+
+/*
+ * Temperature + Gumbel-max sampling, per row b of logits (bf16 [B, ld]):
+ *   out[b] = argmax_i softmax(logits[b, :vocab] / T[b])_i / max(e[b,i], 1e-10)
+ * (ties: lowest index); e[b,i] = -log((w + 1) * 2^-32), w = word i % 4 of
+ * Philox4x32-10 with counter (i/4 + offset_lo, offset_hi + carry, b,
+ * 0x53414D50) and key (seed_lo, seed_hi).  temperatures fp32 [B] (> 0);
+ * out int64 [B]; noise_out (fp32 [B, vocab]) receives e when not NULL.
+ * A caller advances offset by ceil(vocab / 4) per call for fresh noise.
+ */
+int lfs_sample_gumbel(const void* logits, int64_t ld, const float* temperatures, int64_t B, int32_t vocab,
+                      uint64_t seed, uint64_t offset, int64_t* out, float* noise_out, void* stream);
 
 /*
  * add_rmsnorm, per row t of x: bf16 [T, d]:

@@ -1,0 +1,151 @@
+// Fused temperature + Gumbel-max sampler for gfx950 (the decode step's
+// last op, utils/sampler.py:35-53 of the reference):
+//
+//   token[b] = argmax_i softmax(logits[b] / T[b])_i / max(e[b,i], 1e-10)
+//
+// e[b,i] ~ Exp(1) from a counter-based generator, Philox4x32-10 (Salmon,
+// Moraes, Dror, Shaw, SC'11): counter (i/4 + offset_lo, offset_hi (+carry),
+// b, 0x53414D50), key (seed_lo, seed_hi), word i % 4 as w, then
+// e = -log((w + 1) * 2^-32) in double precision.  One workgroup per row:
+// an online max / sum pass over the row, then a pass that forms p / e and
+// keeps the best (ties: lowest index); four consecutive elements per lane
+// per step (one 8-byte load, one Philox call).
+#include "common.h"
+
+namespace lfs {
+namespace {
+
+constexpr int SNT = 256;  // threads per row
+
+__device__ __forceinline__ void philox4x32_10(uint32_t (&c)[4], uint32_t k0, uint32_t k1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    if (r) {
+      k0 += 0x9E3779B9u;
+      k1 += 0xBB67AE85u;
+    }
+    const uint64_t p0 = (uint64_t)c[0] * 0xD2511F53u;
+    const uint64_t p1 = (uint64_t)c[2] * 0xCD9E8D57u;
+    const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c[1] ^ k0;
+    const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c[3] ^ k1;
+    c[1] = (uint32_t)p1;
+    c[3] = (uint32_t)p0;
+    c[0] = n0;
+    c[2] = n2;
+  }
+}
+
+__device__ __forceinline__ void load4(const uint16_t* row, int64_t i, int V, float (&x)[4], bool vec) {
+  if (vec && i + 3 < V) {
+    const uint2 w = *reinterpret_cast<const uint2*>(row + i);
+    x[0] = bf16lo(w.x); x[1] = bf16hi(w.x); x[2] = bf16lo(w.y); x[3] = bf16hi(w.y);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = i + e < V ? bf16_to_f32(row[i + e]) : -INFINITY;
+  }
+}
+
+__global__ __launch_bounds__(SNT) void sample_gumbel_kernel(const uint16_t* __restrict__ logits, int64_t ld,
+                                                            const float* __restrict__ temps, int V, uint64_t seed,
+                                                            uint64_t offset, int64_t* __restrict__ out,
+                                                            float* __restrict__ noise_out) {
+  __shared__ float red_m[SNT / 64], red_s[SNT / 64];
+  __shared__ float red_v[SNT / 64];
+  __shared__ int red_i[SNT / 64];
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint16_t* row = logits + (int64_t)b * ld;
+  const float T = temps[b];
+  const bool vec = ((ld & 3) == 0) && ((((uintptr_t)logits) & 7u) == 0);
+  const int n4 = (V + 3) / 4;
+
+  // ---- pass 1: online max and sum of exp(x - max), x = logit / T
+  float m = -INFINITY, s = 0.f;
+  for (int g = tid; g < n4; g += SNT) {
+    float x[4];
+    load4(row, 4ll * g, V, x, vec);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (4 * g + e >= V) continue;
+      const float xv = x[e] / T;
+      if (xv > m) {
+        s = s * expf(m - xv) + 1.f;
+        m = xv;
+      } else {
+        s += expf(xv - m);
+      }
+    }
+  }
+  auto combine = [](float& m1, float& s1, float m2, float s2) {
+    const float mm = fmaxf(m1, m2);
+    if (mm == -INFINITY) return;
+    s1 = s1 * expf(m1 - mm) + s2 * expf(m2 - mm);
+    m1 = mm;
+  };
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float m2 = __shfl_xor(m, o, 64), s2 = __shfl_xor(s, o, 64);
+    combine(m, s, m2, s2);
+  }
+  if (lane == 0) { red_m[wave] = m; red_s[wave] = s; }
+  __syncthreads();
+  m = red_m[0];
+  s = red_s[0];
+#pragma unroll
+  for (int w = 1; w < SNT / 64; ++w) combine(m, s, red_m[w], red_s[w]);
+
+  // ---- pass 2: p / e, argmax (ties: lowest index)
+  const uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+  float best = -INFINITY;
+  int besti = 0x7FFFFFFF;
+  for (int g = tid; g < n4; g += SNT) {
+    float x[4];
+    load4(row, 4ll * g, V, x, vec);
+    const uint64_t lo = (uint64_t)(uint32_t)offset + (uint64_t)g;
+    uint32_t c[4] = {(uint32_t)lo, (uint32_t)(offset >> 32) + (uint32_t)(lo >> 32), (uint32_t)b, 0x53414D50u};
+    philox4x32_10(c, k0, k1);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 4 * g + e;
+      if (i >= V) continue;
+      const float ev = (float)(-log(((double)c[e] + 1.0) * 0x1p-32));
+      if (noise_out != nullptr) noise_out[(int64_t)b * V + i] = ev;
+      const float p = expf(x[e] / T - m) / s;
+      const float score = p / fmaxf(ev, 1e-10f);
+      if (score > best || (score == best && i < besti)) {
+        best = score;
+        besti = i;
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float v2 = __shfl_xor(best, o, 64);
+    const int i2 = __shfl_xor(besti, o, 64);
+    if (v2 > best || (v2 == best && i2 < besti)) { best = v2; besti = i2; }
+  }
+  if (lane == 0) { red_v[wave] = best; red_i[wave] = besti; }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < SNT / 64; ++w)
+      if (red_v[w] > best || (red_v[w] == best && red_i[w] < besti)) { best = red_v[w]; besti = red_i[w]; }
+    out[b] = besti == 0x7FFFFFFF ? 0 : besti;
+  }
+}
+
+}  // namespace
+}  // namespace lfs
+
+using namespace lfs;
+
+extern "C" int lfs_sample_gumbel(const void* logits, int64_t ld, const float* temperatures, int64_t B,
+                                 int32_t vocab, uint64_t seed, uint64_t offset, int64_t* out, float* noise_out,
+                                 void* stream) {
+  LFS_REQUIRE(B >= 0 && vocab > 0 && ld >= vocab, "sample_gumbel: bad shape B=%lld V=%d ld=%lld", (long long)B,
+              vocab, (long long)ld);
+  if (B == 0) return 0;
+  LFS_REQUIRE(logits && temperatures && out, "sample_gumbel: null pointer");
+  LFS_REQUIRE(B < (1ll << 31), "sample_gumbel: too many rows");
+  hipLaunchKernelGGL(sample_gumbel_kernel, dim3((unsigned)B), dim3(SNT), 0, (hipStream_t)stream,
+                     (const uint16_t*)logits, ld, temperatures, vocab, seed, offset, out, noise_out);
+  return check_launch("sample_gumbel");
+}

@@ -27,6 +27,7 @@ from typing import Optional
 
 import torch
 
+from .. import kernels
 from ..context import get_context, reset_context, set_context
 from .sequence import Sequence
 
@@ -67,14 +68,28 @@ def decode_metadata(seqs: list[Sequence], block_size: int) -> dict:
 
 class Sampler:
     """Temperature + Gumbel-max sampling (utils/sampler.py:35-53): argmax of
-    softmax(logits / T) / Exp(1) noise."""
+    softmax(logits / T) / Exp(1) noise, in one kernel (kernels.sample_gumbel).
+
+    The noise comes from a counter-based generator keyed by a seed and a
+    per-call offset: the seed is the given generator's initial seed, or one
+    drawn from torch's default generator on first use (so torch.manual_seed
+    makes runs repeatable); the offset advances every call."""
+
+    def __init__(self):
+        self._seed: Optional[int] = None
+        self._offset = 0
 
     def __call__(self, logits: torch.Tensor, temperatures: torch.Tensor,
                  generator: Optional[torch.Generator] = None) -> torch.Tensor:
-        logits = logits.float().div_(temperatures.unsqueeze(1))
-        probs = torch.softmax(logits, dim=-1)
-        noise = torch.empty_like(probs).exponential_(1, generator=generator).clamp_min_(1e-10)
-        return probs.div_(noise).argmax(dim=-1)
+        if generator is not None:
+            seed = generator.initial_seed()
+        else:
+            if self._seed is None:
+                self._seed = int(torch.randint(0, 2 ** 62, (1,)).item())
+            seed = self._seed
+        offset = self._offset
+        self._offset += (logits.size(-1) + 3) // 4
+        return kernels.sample_gumbel(logits.to(torch.bfloat16), temperatures.to(torch.float32), seed, offset)
 
 
 class ModelRunner:

@@ -12,6 +12,13 @@ Same names, arguments and return values as the reference's operators:
   paged_attention_decode(q, k_cache, v_cache, context_lens, block_tables,
                          scale=None) -> o
       GQA decode over block tables, math of model/attention/GQA.py:118-130
+  flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
+                         max_seqlen_k, softmax_scale=None, causal=True,
+                         block_table=None) -> o
+      varlen causal prefill attention, the call engine/model_runner.py:291-292
+      names
+  sample_gumbel(logits, temperatures, seed, offset) -> tokens
+      temperature + Gumbel-max sampling, utils/sampler.py:35-53
 
 Every call goes through the C ABI of liblfs_kernels.so on torch's current
 stream; outputs are allocated here, as the reference wrappers do
@@ -321,6 +328,34 @@ def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                                            int(max_seqlen_q), float(softmax_scale), _stream(q))
     _lib.check(rc, "flash_attn_varlen_func")
     return o
+
+
+def sample_gumbel(logits: torch.Tensor, temperatures: torch.Tensor, seed: int, offset: int,
+                  return_noise: bool = False):
+    """Temperature + Gumbel-max sampling in one launch (utils/sampler.py:35-53:
+    argmax(softmax(logits / T) / Exp(1) noise), noise clamped at 1e-10).
+
+    logits: bf16 [B, V] (unit column stride); temperatures: fp32 [B].  The
+    noise of element (b, i) is fixed by (seed, offset, b, i) through
+    Philox4x32-10; advance ``offset`` by ceil(V / 4) per call for fresh
+    noise.  Returns int64 [B] (and the fp32 [B, V] noise when
+    ``return_noise``)."""
+    assert logits.dim() == 2 and logits.stride(1) == 1, "logits must be [B, V] with unit column stride"
+    _on_gpu(logits, temperatures)
+    _dtype(logits, torch.bfloat16, "logits")
+    _dtype(temperatures, torch.float32, "temperatures")
+    B, V = logits.shape
+    if logits.stride(0) < V:  # broadcast rows (an expanded view): give each row its own copy
+        logits = logits.contiguous()
+    temperatures = temperatures.contiguous()
+    assert temperatures.shape == (B,)
+    out = torch.empty(B, dtype=torch.int64, device=logits.device)
+    noise = torch.empty(B, V, dtype=torch.float32, device=logits.device) if return_noise else None
+    rc = _lib.load().lfs_sample_gumbel(_ptr(logits), logits.stride(0), _ptr(temperatures), B, V,
+                                       int(seed) & ((1 << 64) - 1), int(offset) & ((1 << 64) - 1), _ptr(out),
+                                       _ptr(noise) if noise is not None else None, _stream(logits))
+    _lib.check(rc, "sample_gumbel")
+    return (out, noise) if return_noise else out
 
 
 # ------------------------------------------------- fused decode-step rows --
