@@ -148,6 +148,24 @@ def bench_prefill(device, reps):
     return res
 
 
+def bench_indexer(device, reps):
+    """DSA indexer score, fp8_index (model/attention/utils.py:175-250), at the
+    lightning-indexer shape of 64 heads x 128 dims: one sequence of 4096
+    queries against 4096 cached keys.  Algorithmic flop = 2*B*M*N*H*D (the
+    q.k products; ReLU, weights and sums add 3*B*M*N*H)."""
+    from llm_from_scratch_amd import kernels as K
+    B, M, N, H, D = 1, 4096, 4096, 64, 128
+    g = torch.Generator(device=device).manual_seed(10)
+    q = (torch.randn(B, M, H, D, generator=g, device=device) * 16).to(torch.float8_e4m3fn)
+    k = (torch.randn(B, N, D, generator=g, device=device) * 16).to(torch.float8_e4m3fn)
+    qs = torch.rand(B, M, H, generator=g, device=device)
+    ks = torch.rand(B, N, generator=g, device=device)
+    t = timed_launches([lambda: K.fp8_index(q, qs, k, ks)], reps)[0]
+    fl = 2 * B * M * N * H * D
+    return {"shape": {"B": B, "M": M, "N": N, "H": H, "D": D}, "us": t * 1e6, "TFLOP/s": fl / t / 1e12,
+            "frac": fl / t / 1e12 / FP8_PEAK_TFLOPS, "flop": fl}
+
+
 def bench_decode(name, device, reps, flush_buf):
     from llm_from_scratch_amd import kernels as K
     from llm_from_scratch_amd import workloads as W
@@ -258,9 +276,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip decode / act_quant lines")
-    ap.add_argument("--extras", default="act_quant,cfg3,cfg4,prefill,cfg5",
+    ap.add_argument("--extras", default="act_quant,cfg3,cfg4,prefill,indexer,cfg5",
                     help="comma list of extra lines: act_quant, cfg3, cfg4 (paged decode), prefill "
-                         "(varlen prefill attention), cfg5 (decode step)")
+                         "(varlen prefill attention), indexer (DSA fp8_index), cfg5 (decode step)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 4 plain device copies of 256 MiB (a known-traffic kernel for "
                          "scaling FETCH_SIZE / WRITE_SIZE counters)")
@@ -331,6 +349,9 @@ def main():
                 out["paged_decode"].append(bench_decode(name, dev, 20, flush_buf))
             del flush_buf
             torch.cuda.empty_cache()
+        if "indexer" in extras:
+            log("bench: fp8_index")
+            out["fp8_index"] = bench_indexer(dev, 10)
         if "prefill" in extras:
             log("bench: prefill attention")
             out["prefill_attention"] = bench_prefill(dev, 10)

@@ -41,6 +41,9 @@
  *                           reference names at engine/model_runner.py:291-292
  *                           (metadata :202-249; paged keys on a prefix-cache
  *                           hit, :231-237); math of model/attention/GQA.py:118-130
+ *   lfs_fp8_index           fp8_index(q, q_s, k, k_s), the DSA indexer score,
+ *                           model/attention/utils.py:175-250 (caller
+ *                           model/attention/DSA.py:105)
  *   lfs_sample_gumbel       temperature + Gumbel-max sampling,
  *                           utils/sampler.py:35-53 (Sampler.forward), with
  *                           its Exp(1) noise from Philox4x32-10
@@ -189,6 +192,17 @@ int lfs_prefill_attention(const void* q, const void* k, const void* v, const int
                           int32_t block_size, int64_t num_slots, void* out, int64_t B,
                           int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                           int32_t max_seqlen_q, float scale, void* stream);
+
+/*
+ * FP8 indexer score (DSA lightning indexer):
+ *   o[b,m,n] = k_s[b][n] * sum_h relu(q[b,m,h,:] . k[b,n,:]) * q_s[b,m,h]
+ * q: e4m3fn [B, M, H, D] contiguous; q_s fp32 [B, M, H]; k: e4m3fn rows of
+ * D bytes, batch b at k + b * k_stride_b (bytes, multiple of 16, >= N*D);
+ * k_s fp32 [B, ks_stride_b]; o fp32 [B, M, N].  D in {32, 64, 128}; H <= 128.
+ */
+int lfs_fp8_index(const void* q, const float* q_s, const void* k, const float* k_s, float* o, int64_t B,
+                  int32_t M, int32_t N, int32_t H, int32_t D, int64_t k_stride_b, int64_t ks_stride_b,
+                  void* stream);
 
 /*
  * Temperature + Gumbel-max sampling, per row b of logits (bf16 [B, ld]):

@@ -39,6 +39,8 @@ SIGNATURES = {
     "lfs_moe_route": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_i32,
                                      _c_i32, _c_p]),
     "lfs_swiglu_quant": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_p]),
+    "lfs_fp8_index": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i64,
+                                     _c_i64, _c_p]),
     "lfs_sample_gumbel": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_i32, ctypes.c_uint64, ctypes.c_uint64,
                                          _c_p, _c_p, _c_p]),
     "lfs_prefill_attention": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i64, _c_p,

@@ -19,6 +19,8 @@ Same names, arguments and return values as the reference's operators:
       names
   sample_gumbel(logits, temperatures, seed, offset) -> tokens
       temperature + Gumbel-max sampling, utils/sampler.py:35-53
+  fp8_index(q, q_s, k, k_s) -> index_score
+      the DSA indexer score, model/attention/utils.py:175-250
 
 Every call goes through the C ABI of liblfs_kernels.so on torch's current
 stream; outputs are allocated here, as the reference wrappers do
@@ -327,6 +329,37 @@ def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                                            bt_ptr, bt_stride, BS, num_slots, _ptr(o), B, Hq, Hkv, D,
                                            int(max_seqlen_q), float(softmax_scale), _stream(q))
     _lib.check(rc, "flash_attn_varlen_func")
+    return o
+
+
+def fp8_index(q: torch.Tensor, q_s: torch.Tensor, k: torch.Tensor, k_s: torch.Tensor) -> torch.Tensor:
+    """Index score of the DSA lightning indexer (model/attention/utils.py:
+    230-250): fp8 q @ fp8 k -> fp32 logits, relu(logits) * q_s, sum over
+    heads, * k_s.
+
+    q: e4m3fn [b, m, h, d] contiguous; q_s: fp32 [b, m, h] (or [b, m, h, 1]);
+    k: e4m3fn [b, n, d] (rows contiguous; a slice of a longer FP8 K cache
+    along n is accepted without a copy); k_s: fp32 [b, n].  d in {32, 64,
+    128}, h <= 128.  Returns fp32 [b, m, n]."""
+    assert q.dim() == 4 and q.is_contiguous(), "q must be contiguous [b, m, h, d]"
+    if q_s.dim() == 4:
+        assert q_s.size(-1) == 1, "q_s must be [b, m, h] (one weight per head)"
+        q_s = q_s.squeeze(-1)
+    q_s = q_s.contiguous()
+    assert k.dim() == 3 and k.stride(2) == 1 and k.stride(1) == k.size(2), "k rows must be contiguous [b, n, d]"
+    assert k_s.dim() == 2 and k_s.stride(1) == 1, "k_s must be [b, n]"
+    _on_gpu(q, q_s, k, k_s)
+    _dtype(q, FP8, "q")
+    _dtype(k, FP8, "k")
+    _dtype(q_s, torch.float32, "q_s")
+    _dtype(k_s, torch.float32, "k_s")
+    b, m, h, d = q.shape
+    n = k.size(1)
+    assert k.shape == (b, n, d) and q_s.shape == (b, m, h) and k_s.shape == (b, n)
+    o = torch.empty(b, m, n, dtype=torch.float32, device=q.device)
+    rc = _lib.load().lfs_fp8_index(_ptr(q), _ptr(q_s), _ptr(k), _ptr(k_s), _ptr(o), b, m, n, h, d,
+                                   k.stride(0), k_s.stride(0), _stream(q))
+    _lib.check(rc, "fp8_index")
     return o
 
 

@@ -24,6 +24,8 @@ Pinning (what checks each function, see tests/test_oracle_fp8.py):
   weight_dequant-- bit-exact vs torch (fp32 product, RNE to bf16).
   fp8_gemm      -- float64 dequant(A) @ dequant(B)^T (textbook), exact on
                    small-integer codes with unit scales.
+  fp8_index     -- scalar brute force on tiny inputs; all-negative dot
+                   products give 0 (ReLU); linear in q_s and in k_s.
 """
 from __future__ import annotations
 
@@ -222,3 +224,15 @@ def fp8_gemm(a, a_s, b, b_s, bias=None, block_size: int = 128, accum=np.float64)
         bias = np.asarray(bias, dtype=accum)
         acc = acc + (bias[None, :] if bias.ndim == 1 else bias)
     return bf16_round(acc.astype(np.float32))
+
+
+def fp8_index(q, q_s, k, k_s, accum=np.float64) -> np.ndarray:
+    """o[b, m, n] = k_s[b, n] * sum_h relu(q[b, m, h] . k[b, n]) * q_s[b, m, h]
+    (the indexer score of model/attention/utils.py:175-227: fp8 q.k per head,
+    ReLU, head weights, head sum, key scale).  q: codes [B, M, H, D], q_s
+    [B, M, H]; k: codes [B, N, D], k_s [B, N].  Returns float [B, M, N]."""
+    qd = e4m3_decode(np.asarray(q)).astype(accum)
+    kd = e4m3_decode(np.asarray(k)).astype(accum)
+    logits = np.einsum("bmhd,bnd->bmhn", qd, kd)
+    w = np.maximum(logits, 0) * np.asarray(q_s, accum)[..., None]
+    return w.sum(axis=2) * np.asarray(k_s, accum)[:, None, :]

@@ -211,3 +211,30 @@ def test_fp8_gemm_exact_small_integers():
     want = F.bf16_round(exact.astype(np.float32))
     assert np.array_equal(F.fp8_gemm(a, ones_a, b, ones_b), want)
     assert np.array_equal(F.fp8_gemm(a, ones_a, b, ones_b, accum=np.float32), want)
+
+
+def test_fp8_index_brute_force_and_invariants():
+    """The indexer score (utils.py:175-227) by scalar loops on a tiny case;
+    ReLU zeroes all-negative dot products; the score is linear in q_s and k_s."""
+    rng = np.random.default_rng(12)
+    B, M, N, H, D = 2, 3, 5, 4, 8
+    q = F.e4m3_encode(rng.standard_normal((B, M, H, D)))
+    k = F.e4m3_encode(rng.standard_normal((B, N, D)))
+    qs = rng.uniform(0.1, 2.0, (B, M, H))
+    ks = rng.uniform(0.1, 2.0, (B, N))
+    o = F.fp8_index(q, qs, k, ks)
+    qd, kd = F.e4m3_decode(q).astype(float), F.e4m3_decode(k).astype(float)
+    for b in range(B):
+        for m in range(M):
+            for n in range(N):
+                tot = 0.0
+                for h in range(H):
+                    dot = sum(qd[b, m, h, d] * kd[b, n, d] for d in range(D))
+                    tot += max(dot, 0.0) * qs[b, m, h]
+                assert abs(o[b, m, n] - tot * ks[b, n]) <= 1e-12 * max(1.0, abs(tot))
+    # all q.k < 0: q = -|x|, k = +|y| elementwise
+    qn = F.e4m3_encode(-np.abs(rng.standard_normal((1, 2, 3, 8))) - 0.5)
+    kp = F.e4m3_encode(np.abs(rng.standard_normal((1, 4, 8))) + 0.5)
+    assert np.all(F.fp8_index(qn, np.ones((1, 2, 3)), kp, np.ones((1, 4))) == 0)
+    np.testing.assert_allclose(F.fp8_index(q, 3 * qs, k, ks), 3 * o, rtol=1e-12)
+    np.testing.assert_allclose(F.fp8_index(q, qs, k, 0.5 * ks), 0.5 * o, rtol=1e-12)
