@@ -6,16 +6,17 @@
 // e[b,i] ~ Exp(1) from a counter-based generator, Philox4x32-10 (Salmon,
 // Moraes, Dror, Shaw, SC'11): counter (i/4 + offset_lo, offset_hi (+carry),
 // b, 0x53414D50), key (seed_lo, seed_hi), word i % 4 as w, then
-// e = -log((w + 1) * 2^-32) in double precision.  One workgroup per row:
-// an online max / sum pass over the row, then a pass that forms p / e and
-// keeps the best (ties: lowest index); four consecutive elements per lane
-// per step (one 8-byte load, one Philox call).
+// e = -log((w + 1) * 2^-32) to float rounding.  One workgroup per row and
+// one pass: the pick maximises x_i / T - log(max(e_i, 1e-10)), which orders
+// the elements as softmax(x / T)_i / max(e_i, 1e-10) does (the softmax's
+// normaliser is common to the row); ties go to the lowest index.  Four
+// consecutive elements per lane per step (one 8-byte load, one Philox call).
 #include "common.h"
 
 namespace lfs {
 namespace {
 
-constexpr int SNT = 256;  // threads per row
+constexpr int SNT = 1024;  // threads per row
 
 __device__ __forceinline__ void philox4x32_10(uint32_t (&c)[4], uint32_t k0, uint32_t k1) {
 #pragma unroll
@@ -35,6 +36,15 @@ __device__ __forceinline__ void philox4x32_10(uint32_t (&c)[4], uint32_t k0, uin
   }
 }
 
+// e = -log(u), u = (w + 1) * 2^-32 in (0, 1], to float rounding: for
+// u >= 1/2 through log1p of the (exact) complement v = (2^32 - 1 - w) * 2^-32,
+// so that u close to 1 keeps its small e; otherwise the log of u itself
+// (float(w + 1) is within 2^-24 relative, the power-of-two scale exact).
+__device__ __forceinline__ float exp1_from_word(uint32_t w) {
+  if (w >= 0x80000000u) return -log1pf(-(float)(0xFFFFFFFFu - w) * 0x1p-32f);
+  return -logf(((float)w + 1.0f) * 0x1p-32f);
+}
+
 __device__ __forceinline__ void load4(const uint16_t* row, int64_t i, int V, float (&x)[4], bool vec) {
   if (vec && i + 3 < V) {
     const uint2 w = *reinterpret_cast<const uint2*>(row + i);
@@ -45,11 +55,10 @@ __device__ __forceinline__ void load4(const uint16_t* row, int64_t i, int V, flo
   }
 }
 
-__global__ __launch_bounds__(SNT) void sample_gumbel_kernel(const uint16_t* __restrict__ logits, int64_t ld,
+__global__ __launch_bounds__(1024) void sample_gumbel_kernel(const uint16_t* __restrict__ logits, int64_t ld,
                                                             const float* __restrict__ temps, int V, uint64_t seed,
                                                             uint64_t offset, int64_t* __restrict__ out,
                                                             float* __restrict__ noise_out) {
-  __shared__ float red_m[SNT / 64], red_s[SNT / 64];
   __shared__ float red_v[SNT / 64];
   __shared__ int red_i[SNT / 64];
   const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -58,43 +67,11 @@ __global__ __launch_bounds__(SNT) void sample_gumbel_kernel(const uint16_t* __re
   const bool vec = ((ld & 3) == 0) && ((((uintptr_t)logits) & 7u) == 0);
   const int n4 = (V + 3) / 4;
 
-  // ---- pass 1: online max and sum of exp(x - max), x = logit / T
-  float m = -INFINITY, s = 0.f;
-  for (int g = tid; g < n4; g += SNT) {
-    float x[4];
-    load4(row, 4ll * g, V, x, vec);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if (4 * g + e >= V) continue;
-      const float xv = x[e] / T;
-      if (xv > m) {
-        s = s * expf(m - xv) + 1.f;
-        m = xv;
-      } else {
-        s += expf(xv - m);
-      }
-    }
-  }
-  auto combine = [](float& m1, float& s1, float m2, float s2) {
-    const float mm = fmaxf(m1, m2);
-    if (mm == -INFINITY) return;
-    s1 = s1 * expf(m1 - mm) + s2 * expf(m2 - mm);
-    m1 = mm;
-  };
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float m2 = __shfl_xor(m, o, 64), s2 = __shfl_xor(s, o, 64);
-    combine(m, s, m2, s2);
-  }
-  if (lane == 0) { red_m[wave] = m; red_s[wave] = s; }
-  __syncthreads();
-  m = red_m[0];
-  s = red_s[0];
-#pragma unroll
-  for (int w = 1; w < SNT / 64; ++w) combine(m, s, red_m[w], red_s[w]);
-
-  // ---- pass 2: p / e, argmax (ties: lowest index)
+  // ---- one pass: softmax(x / T)_i / e_i = exp(x_i / T - log e_i) / Z, so
+  // its argmax is the argmax of x_i / T - log(max(e_i, 1e-10)) (ties: lowest
+  // index); no max / sum over the row is needed for the pick
   const uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+  const float invT = 1.0f / T;
   float best = -INFINITY;
   int besti = 0x7FFFFFFF;
   for (int g = tid; g < n4; g += SNT) {
@@ -107,10 +84,11 @@ __global__ __launch_bounds__(SNT) void sample_gumbel_kernel(const uint16_t* __re
     for (int e = 0; e < 4; ++e) {
       const int i = 4 * g + e;
       if (i >= V) continue;
-      const float ev = (float)(-log(((double)c[e] + 1.0) * 0x1p-32));
+      const float ev = exp1_from_word(c[e]);
       if (noise_out != nullptr) noise_out[(int64_t)b * V + i] = ev;
-      const float p = expf(x[e] / T - m) / s;
-      const float score = p / fmaxf(ev, 1e-10f);
+      // ranking only: x * (1/T) and the hardware log2 are within a few ulp
+      // of x / T and log, which can only reorder near-ties
+      const float score = x[e] * invT - __log2f(fmaxf(ev, 1e-10f)) * 0.6931471805599453f;
       if (score > best || (score == best && i < besti)) {
         best = score;
         besti = i;
