@@ -57,6 +57,21 @@
  *   lfs_moe_route           MoE gate, model/architecture/moe.py:45-90
  *   lfs_swiglu_quant        silu(w1 x) * w3 x, model/architecture/mlp.py:60-67,
  *                           quantised for the experts' down projection
+ * MoE expert dispatch (MoE.moe_infer, model/architecture/moe.py:288-341,
+ * without its argsort / bincount / .tolist() host sync and scatter_add_):
+ *   lfs_moe_align_tiles     capacity (128-row tiles) lfs_moe_align needs
+ *   lfs_moe_align           (token, pick) entries grouped by expert into
+ *                           128-row tiles (moe.py:298-307)
+ *   lfs_fp8_grouped_gemm    one FP8 block-scaled GEMM per expert segment (the
+ *                           per-expert MLP calls, moe.py:318-330)
+ *   lfs_moe_combine         weighted sum of a token's expert rows (the
+ *                           scatter_add_ of moe.py:332-339 and the shared
+ *                           expert add of moe.py:272-273)
+ * Weighted segment reduction (the Triton kernels of
+ * model/architecture/moe_kernels.py):
+ *   lfs_segment_reduce_weighted   segment_reduce_weighted, :70-125
+ *   lfs_scatter_add_weighted      fused_scatter_add_weighted, :128-171
+ *   lfs_scatter_add_weighted_workspace_bytes
  */
 #ifndef LFS_KERNELS_H
 #define LFS_KERNELS_H
@@ -67,7 +82,7 @@
 extern "C" {
 #endif
 
-#define LFS_ABI_VERSION 3
+#define LFS_ABI_VERSION 4
 
 /* argument errors (negative); launch errors are positive hipError_t values */
 #define LFS_EINVAL (-1)
@@ -258,11 +273,17 @@ int lfs_qk_norm_rope_store(const void* qkv, int64_t ld, const float* q_weight, c
  *   dense_weights[t] (fp32 [T, E + S]) = those weights, then S ones for the
  *   shared experts; bias_out[t] (fp32 [T, d]) = sum_e dense_weights[t][e] *
  *   down_bias[e] (fp32 [E + S, d]).
+ *   Optionally (both or neither) the picks in the gate's index form:
+ *   topk_idx (int64 [T, top_k], in pick order) and topk_weight (fp32
+ *   [T, top_k], their weights) -- the (topk_idx, topk_weight) the reference
+ *   gate returns (moe.py:90).  dense_weights may be NULL when topk_idx is
+ *   given; bias_out may be NULL (then down_bias may be too).
  * E + S <= 64; d % 8 == 0.
  */
 int lfs_moe_route(const void* h, const void* gate_weight, const float* expert_bias,
                   const float* down_bias, float* dense_weights, float* bias_out, int64_t T,
-                  int32_t d, int32_t num_experts, int32_t num_shared, int32_t top_k, void* stream);
+                  int32_t d, int32_t num_experts, int32_t num_shared, int32_t top_k,
+                  int64_t* topk_idx, float* topk_weight, void* stream);
 
 /*
  * swiglu_quant, for h13: bf16 [T, E, 2, F] (per expert the w1 then the w3
@@ -274,6 +295,93 @@ int lfs_moe_route(const void* h, const void* gate_weight, const float* expert_bi
  */
 int lfs_swiglu_quant(const void* h13, const float* route_weights, void* q, float* q_scale, int64_t T,
                      int32_t num_experts, int32_t d_ff, void* stream);
+
+/* ------------------------------------------------------------ MoE dispatch */
+
+/*
+ * Number of 128-row tiles lfs_moe_align may fill for T tokens with top_k
+ * picks and S shared experts over E routed ones:
+ * ceil((T * (top_k + S) + (E + S) * 127) / 128).
+ */
+int64_t lfs_moe_align_tiles(int64_t T, int32_t top_k, int32_t num_experts, int32_t num_shared);
+
+/*
+ * moe_align.  Entry i = t * (top_k + S) + j: for j < top_k the routed expert
+ * topk_idx[t][j] (int64 [T, top_k]; values outside [0, E) are dropped) with
+ * weight topk_weight[t][j] (fp32), for j >= top_k the shared expert
+ * E + j - top_k with weight 1.  Rows are grouped by expert, experts in index
+ * order, each expert's entries in entry order, each expert's segment padded
+ * to a multiple of 128 rows:
+ *   row_token[r] (int32 [num_tiles*128])  token of row r, -1 for padding
+ *   row_weight[r] (fp32 [num_tiles*128])  weight of row r, 0 for padding
+ *   tile_expert[i] (int32 [num_tiles])    expert of rows 128i .. 128i+127,
+ *                                         -1 for tiles past the last segment
+ *   entry_row[i] (int32 [T*(top_k+S)])    row of entry i (-1 if dropped)
+ * num_tiles >= lfs_moe_align_tiles(...); E + S <= 64.  One workgroup; the
+ * launch shape depends only on num_tiles (graph-capturable).
+ */
+int lfs_moe_align(const int64_t* topk_idx, const float* topk_weight, int64_t T, int32_t top_k,
+                  int32_t num_experts, int32_t num_shared, int32_t* row_token, float* row_weight,
+                  int32_t* tile_expert, int64_t num_tiles, int32_t* entry_row, void* stream);
+
+/*
+ * fp8_grouped_gemm: for every tile i < num_tiles with e = tile_expert[i] >= 0
+ * and every row m of it (m = 128i .. 128i+127):
+ *   C[m, n] = sum_kb a_s[r, kb] * Bs_e[n/128, kb] * (A[r, kb] . B_e[n, kb]) (+ bias_e[n])
+ * with r = row_index[m] (row_index NULL: r = m; r < 0 reads row 0 -- a
+ * padding row, whose result is written but means nothing), A e4m3fn
+ * [a_rows, K], a_s fp32 [a_rows, K/128], B_e = b + e*b_expert_stride (row n
+ * at + n*ldb bytes), Bs_e = b_s + e*bs_expert_stride (row n/128 at
+ * + (n/128)*ldbs floats), bias_e = bias + e*bias_expert_stride (fp32, NULL
+ * for none).  Exactly one output: c bf16 [num_tiles*128, N] (with the
+ * bias), or c_f32 fp32 [num_tiles*128, N] (no bias).  Rows of tiles with
+ * e < 0 are not written.  K % 128 == 0; ldb, b_expert_stride % 16 == 0.
+ */
+int lfs_fp8_grouped_gemm(const void* a, const float* a_s, int64_t a_rows, const int32_t* row_index,
+                         const int32_t* tile_expert, int64_t num_tiles, const void* b, const float* b_s,
+                         int64_t b_expert_stride, int64_t ldb, int64_t bs_expert_stride, int64_t ldbs,
+                         const float* bias, int64_t bias_expert_stride, void* c, float* c_f32, int64_t N,
+                         int64_t K, void* stream);
+
+/*
+ * moe_combine, per token t (entries i = t*(top_k+S) + j as in moe_align):
+ *   y[t] = bf16( sum_j out[entry_row[i]] + sum_j w_j * down_bias[e_j] )
+ * summed in fp32 in j order, entries with entry_row < 0 skipped; out fp32
+ * [rows, ld] (the down projection's rows, routing weights already applied),
+ * down_bias fp32 [E + S, d] or NULL; y bf16 [T, d].  d % 8 == 0.
+ */
+int lfs_moe_combine(const float* out, int64_t ld, const int32_t* entry_row, const int64_t* topk_idx,
+                    const float* topk_weight, int64_t T, int32_t top_k, int32_t num_experts,
+                    int32_t num_shared, const float* down_bias, int32_t d, void* y, void* stream);
+
+/*
+ * segment_reduce_weighted: y[t] = sum_{p : idx[p] == t} w[p] * x[p] for
+ * t < num_tokens, p in increasing order, fp32 accumulation, stored in x's
+ * dtype.  x: bf16 (x_is_f32 = 0) or fp32 [n, ldx]; w: bf16 or fp32 [n];
+ * sorted_token_idx: int64 [n], non-decreasing (each token's segment is
+ * found by binary search, like torch.searchsorted).  y contiguous
+ * [num_tokens, d].  Every entry of a segment is summed (the reference's
+ * kernel stops after next_pow2(max(top_k, 2)) of them).  2-byte alignment
+ * suffices.
+ */
+int lfs_segment_reduce_weighted(const void* x, int32_t x_is_f32, int64_t ldx, const void* weights,
+                                int32_t w_is_f32, const int64_t* sorted_token_idx, int64_t n,
+                                int64_t num_tokens, int32_t d, void* y, void* stream);
+
+/* workspace bytes of lfs_scatter_add_weighted: 4 * (3 * num_tokens + 1 + n) */
+int64_t lfs_scatter_add_weighted_workspace_bytes(int64_t n, int64_t num_tokens);
+
+/*
+ * scatter_add_weighted: the same sum for any order of token_idx (int64 [n];
+ * entries outside [0, num_tokens) are skipped): the entries are counted,
+ * scanned and placed per token in a caller-owned int32 workspace, then
+ * each token's segment is summed in increasing entry order (segments of
+ * more than 256 entries in placement order).  Six launches, no
+ * synchronisation, no memset (the counters are cleared by a kernel).
+ */
+int lfs_scatter_add_weighted(const void* x, int32_t x_is_f32, int64_t ldx, const void* weights,
+                             int32_t w_is_f32, const int64_t* token_idx, int64_t n, int64_t num_tokens,
+                             int32_t d, void* y, void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

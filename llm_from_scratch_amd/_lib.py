@@ -11,7 +11,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "liblfs_kernels.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _c_i64, _c_i32, _c_p, _c_f = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p, ctypes.c_float
 
@@ -37,7 +37,7 @@ SIGNATURES = {
     "lfs_qk_norm_rope_store": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
                                               _c_i64, _c_i32, _c_i32, _c_i32, _c_i64, _c_i64, _c_f, _c_p]),
     "lfs_moe_route": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_i32,
-                                     _c_i32, _c_p]),
+                                     _c_i32, _c_p, _c_p, _c_p]),
     "lfs_swiglu_quant": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_p]),
     "lfs_fp8_index": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i64,
                                      _c_i64, _c_p]),
@@ -45,6 +45,18 @@ SIGNATURES = {
                                          _c_p, _c_p, _c_p]),
     "lfs_prefill_attention": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i64, _c_p,
                                              _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_f, _c_p]),
+    "lfs_moe_align_tiles": (ctypes.c_int64, [_c_i64, _c_i32, _c_i32, _c_i32]),
+    "lfs_moe_align": (ctypes.c_int, [_c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_i64, _c_p,
+                                     _c_p]),
+    "lfs_fp8_grouped_gemm": (ctypes.c_int, [_c_p, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64,
+                                            _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_p]),
+    "lfs_moe_combine": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_p,
+                                       _c_i32, _c_p, _c_p]),
+    "lfs_segment_reduce_weighted": (ctypes.c_int, [_c_p, _c_i32, _c_i64, _c_p, _c_i32, _c_p, _c_i64, _c_i64,
+                                                   _c_i32, _c_p, _c_p]),
+    "lfs_scatter_add_weighted_workspace_bytes": (ctypes.c_int64, [_c_i64, _c_i64]),
+    "lfs_scatter_add_weighted": (ctypes.c_int, [_c_p, _c_i32, _c_i64, _c_p, _c_i32, _c_p, _c_i64, _c_i64, _c_i32,
+                                                _c_p, _c_p, _c_i64, _c_p]),
 }
 
 _LIB = None

@@ -19,7 +19,7 @@ PKG_DIR = Path(__file__).resolve().parent
 REPO = PKG_DIR.parent
 CSRC = PKG_DIR / "csrc"
 LIB_PATH = PKG_DIR / "liblfs_kernels.so"
-SOURCES = ["capi.hip", "quant.hip", "fp8_gemm.hip", "paged_kv.hip", "fused.hip", "prefill.hip", "sampler.hip", "indexer.hip"]
+SOURCES = ["capi.hip", "quant.hip", "fp8_gemm.hip", "paged_kv.hip", "fused.hip", "prefill.hip", "sampler.hip", "indexer.hip", "moe.hip"]
 
 HIPCC_FLAGS = [
     "-O3",

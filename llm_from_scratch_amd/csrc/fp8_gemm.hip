@@ -129,11 +129,26 @@ __device__ __forceinline__ int swz(int r, int c) {
 // Scale products a_s * b_s are staged per chunk of SCK K blocks in a
 // k-major table ([SCK][BM+1] floats) instead of one strided 4-byte gather
 // per K block.
-template <int BM, int NST, int SCK>
+//
+// GROUPED: one GEMM per expert over row segments (the MoE expert GEMMs).  C
+// rows are grouped in 128-row tiles, tile tm belonging to expert
+// tile_expert[tm] (< 0: the tile is unused and exits).  Row m of C takes A
+// row row_index[m] (a gather of the tokens routed to the expert; < 0 reads
+// row 0, whose result is padding) or, with row_index null, A row m.  The
+// expert's weights are B + e * b_es (rows ldb bytes apart), its scales
+// Bs + e * bs_es (rows ldbs floats apart), its bias bias + e * bias_es.
+struct Grouped {
+  const int32_t* tile_expert;
+  const int32_t* row_index;
+  int64_t b_es, bs_es, bias_es;
+  int a_rows;
+};
+
+template <int BM, int NST, int SCK, bool GROUPED = false>
 __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ B,
     const float* __restrict__ Bs, const float* __restrict__ bias, int64_t bias_ld, uint16_t* __restrict__ C, int M,
-    int N, int K, int tiles_m, int tiles_n, float* __restrict__ ws, int kps) {
+    int N, int K, int tiles_m, int tiles_n, float* __restrict__ ws, int kps, int64_t ldb, int ldbs, Grouped grp) {
   constexpr int NW = BM / 32;  // waves
   constexpr int NT = 64 * NW;  // threads
   constexpr int SCP = BM + 1;  // padded row of the k-major scale table
@@ -156,6 +171,25 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
   const int tm = first_m + (pid % gsize);
   const int tn = (pid % (GROUP_M * tiles_n)) / gsize;
   const int m0 = tm * BM, n0 = tn * BN;
+  __shared__ int s_arow[GROUPED ? BM : 1];  // A row of each tile row (gathered)
+  if constexpr (GROUPED) {
+    const int e = grp.tile_expert[tm];
+    if (e < 0) return;  // whole workgroup, before any barrier
+    B += e * grp.b_es;
+    Bs += e * grp.bs_es;
+    if (bias != nullptr) bias += e * grp.bias_es;
+    for (int r = threadIdx.x; r < BM; r += BM * 2) {
+      const int m = min(m0 + r, M - 1);
+      const int ar = grp.row_index != nullptr ? grp.row_index[m] : m;
+      s_arow[r] = min(max(ar, 0), grp.a_rows - 1);
+    }
+    __syncthreads();
+  }
+  // A row of tile row r (rows past M are clamped; their results are never stored)
+  auto arow = [&](int r) -> int {
+    if constexpr (GROUPED) return s_arow[r];
+    else return min(m0 + r, M - 1);
+  };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -177,16 +211,16 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
   for (int u = 0; u < A_PER_WAVE; ++u) {
     const int r = 8 * (wave + NW * u) + (lane >> 3);
     const int c = (lane & 7) ^ (((r >> 1) & 7) ^ ((r & 1) << 2));
-    srcA[u] = A + (size_t)min(m0 + r, M - 1) * K + (size_t)kb0 * BK + c * 16;
+    srcA[u] = A + (size_t)arow(r) * K + (size_t)kb0 * BK + c * 16;
   }
 #pragma unroll
   for (int u = 0; u < B_PER_WAVE; ++u) {
     const int r = 8 * (wave + NW * u) + (lane >> 3);
     const int c = (lane & 7) ^ (((r >> 1) & 7) ^ ((r & 1) << 2));
-    srcB[u] = B + (size_t)min(n0 + r, N - 1) * K + (size_t)kb0 * BK + c * 16;
+    srcB[u] = B + (size_t)min(n0 + r, N - 1) * ldb + (size_t)kb0 * BK + c * 16;
   }
   const unsigned lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
-  const float* bs_row = Bs + (size_t)(n0 / 128) * KTA + kb0;
+  const float* bs_row = Bs + (size_t)(n0 / 128) * ldbs + kb0;
   const float* as_base = As + kb0;
 
   auto issue = [&](int kt, int buf) {
@@ -206,7 +240,7 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
       const int idx = tid + NT * v;
       const int row = idx / SCK, k = idx % SCK;
       ssc[k * SCP + row] =
-          k < nk ? as_base[(size_t)min(m0 + row, M - 1) * KTA + kt0 + k] * bs_row[kt0 + k] : 0.f;
+          k < nk ? as_base[(size_t)arow(row) * KTA + kt0 + k] * bs_row[kt0 + k] : 0.f;
     }
   };
 
@@ -666,7 +700,8 @@ int fp8_gemm_impl(const void* a, const float* a_s, const void* b, const float* b
   // 8-wave workgroup per CU measured 10-15% slower on every benchmark shape.)
   hipLaunchKernelGGL((fp8_gemm_tile<128, 2, 16>), dim3((unsigned)(tiles_m128 * tiles_n), (unsigned)(used > 1 ? used : 1)),
                      dim3(256), 0, st, (const uint8_t*)a, a_s, (const uint8_t*)b, b_s, bias, bias_ld,
-                     (uint16_t*)c, (int)M, (int)N, (int)K, (int)tiles_m128, (int)tiles_n, ws, kps);
+                     (uint16_t*)c, (int)M, (int)N, (int)K, (int)tiles_m128, (int)tiles_n, ws, kps, (int64_t)K,
+                     (int)KT, Grouped{});
   int rc = check_launch("fp8_gemm");
   if (rc != 0 || ws == nullptr) return rc;
   const int64_t quads = M * ((N + 3) / 4);
@@ -688,4 +723,35 @@ extern "C" int lfs_fp8_gemm_splitk(const void* a, const float* a_s, const void* 
                                    void* stream) {
   return fp8_gemm_impl(a, a_s, b, b_s, bias, bias_ld, c, M, N, K, splits, workspace, workspace_bytes,
                        stream);
+}
+
+extern "C" int lfs_fp8_grouped_gemm(const void* a, const float* a_s, int64_t a_rows, const int32_t* row_index,
+                                    const int32_t* tile_expert, int64_t num_tiles, const void* b, const float* b_s,
+                                    int64_t b_expert_stride, int64_t ldb, int64_t bs_expert_stride, int64_t ldbs,
+                                    const float* bias, int64_t bias_expert_stride, void* c, float* c_f32, int64_t N,
+                                    int64_t K, void* stream) {
+  LFS_REQUIRE(a_rows >= 0 && num_tiles >= 0 && N >= 0 && K >= 0, "fp8_grouped_gemm: negative shape");
+  LFS_REQUIRE(K % 128 == 0 && K > 0, "fp8_grouped_gemm: K=%lld must be a positive multiple of 128", (long long)K);
+  LFS_REQUIRE(ldb >= K && ldb % 16 == 0 && b_expert_stride >= 0 && b_expert_stride % 16 == 0,
+              "fp8_grouped_gemm: weight rows must be 16-byte aligned, ldb >= K");
+  LFS_REQUIRE(ldbs >= K / 128 && bs_expert_stride >= 0 && bias_expert_stride >= 0,
+              "fp8_grouped_gemm: bad scale / bias strides");
+  LFS_REQUIRE((c == nullptr) != (c_f32 == nullptr), "fp8_grouped_gemm: exactly one of c (bf16) and c_f32");
+  LFS_REQUIRE(c_f32 == nullptr || bias == nullptr, "fp8_grouped_gemm: the fp32 output takes no bias");
+  const int64_t M = num_tiles * 128;
+  LFS_REQUIRE(M < (1ll << 31) && N < (1ll << 31) && K < (1ll << 31) && a_rows < (1ll << 31) && ldb < (1ll << 31),
+              "fp8_grouped_gemm: shape too large");
+  if (num_tiles == 0 || N == 0) return 0;
+  LFS_REQUIRE(a_rows > 0 && a && a_s && b && b_s && tile_expert, "fp8_grouped_gemm: null pointer");
+  LFS_REQUIRE(row_index != nullptr || a_rows >= M, "fp8_grouped_gemm: without row_index A needs num_tiles*128 rows");
+  LFS_REQUIRE((((uintptr_t)a | (uintptr_t)b) & 15u) == 0, "fp8_grouped_gemm: a and b must be 16-byte aligned");
+  LFS_REQUIRE((((uintptr_t)c | (uintptr_t)c_f32) & 15u) == 0, "fp8_grouped_gemm: output must be 16-byte aligned");
+  const int64_t tiles_n = (N + BN - 1) / BN;
+  LFS_REQUIRE(num_tiles * tiles_n < (1ll << 31), "fp8_grouped_gemm: too many tiles");
+  const Grouped grp{tile_expert, row_index, b_expert_stride, bs_expert_stride, bias_expert_stride, (int)a_rows};
+  hipLaunchKernelGGL((fp8_gemm_tile<128, 2, 16, true>), dim3((unsigned)(num_tiles * tiles_n)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint8_t*)a, a_s, (const uint8_t*)b, b_s, bias, (int64_t)0,
+                     (uint16_t*)c, (int)M, (int)N, (int)K, (int)num_tiles, (int)tiles_n, c_f32, (int)(K / 128),
+                     ldb, (int)ldbs, grp);
+  return check_launch("fp8_grouped_gemm");
 }

@@ -231,9 +231,10 @@ constexpr int kMaxExperts = 64;
 __global__ __launch_bounds__(256) void moe_route_kernel(
     const uint16_t* __restrict__ h, const uint16_t* __restrict__ gw, const float* __restrict__ ebias,
     const float* __restrict__ b2, float* __restrict__ dense, float* __restrict__ bias_out, int d,
-    int E, int S, int top_k) {
+    int E, int S, int top_k, int64_t* __restrict__ topk_idx, float* __restrict__ topk_w) {
   __shared__ float logits[kMaxExperts];
   __shared__ float wsel[kMaxExperts];
+  __shared__ int sel[kMaxExperts];
   const int64_t t = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int cpr = d / 8;
@@ -269,18 +270,25 @@ __global__ __launch_bounds__(256) void moe_route_kernel(
         if (ob > best || (ob == best && oi < bi)) { best = ob; bi = oi; }
       }
       if (lane == bi) chosen = true;
+      if (lane == 0) sel[k] = bi;
       wsum = add_rn(wsum, __shfl(score, bi < 64 ? bi : 0, 64) * (bi < 64 ? 1.f : 0.f));
     }
     float wgt = chosen ? score : 0.f;
     if (top_k > 1) wgt = chosen ? wgt / add_rn(wsum, 1e-10f) : 0.f;
     if (lane < E + S) {
       const float v = lane < E ? wgt : 1.0f;
-      dense[t * (E + S) + lane] = v;
+      if (dense != nullptr) dense[t * (E + S) + lane] = v;
       wsel[lane] = v;
     }
   }
   __syncthreads();
+  // the picks in index form (the reference gate's topk_idx / topk_weight)
+  if (topk_idx != nullptr && (int)threadIdx.x < top_k) {
+    topk_idx[t * top_k + threadIdx.x] = sel[threadIdx.x];
+    topk_w[t * top_k + threadIdx.x] = wsel[sel[threadIdx.x]];
+  }
   // routed bias: sum_e w[e] * b2[e, n], experts in index order
+  if (bias_out == nullptr) return;
   for (int n = threadIdx.x; n < d; n += 256) {
     float acc = 0.f;
     for (int e = 0; e < E + S; ++e) acc = add_rn(acc, mul_rn(wsel[e], b2[(int64_t)e * d + n]));
@@ -395,18 +403,20 @@ extern "C" int lfs_qk_norm_rope_store(const void* qkv, int64_t ld, const float* 
 extern "C" int lfs_moe_route(const void* h, const void* gate_weight, const float* expert_bias,
                              const float* down_bias, float* dense_weights, float* bias_out, int64_t T,
                              int32_t d, int32_t num_experts, int32_t num_shared, int32_t top_k,
-                             void* stream) {
+                             int64_t* topk_idx, float* topk_weight, void* stream) {
   LFS_REQUIRE(T >= 0 && d > 0 && d % 8 == 0, "moe_route: d=%d must be a positive multiple of 8", d);
   LFS_REQUIRE(num_experts > 0 && num_shared >= 0 && num_experts + num_shared <= kMaxExperts,
               "moe_route: at most %d experts", kMaxExperts);
   LFS_REQUIRE(top_k >= 1 && top_k <= num_experts, "moe_route: bad top_k");
   if (T == 0) return 0;
-  LFS_REQUIRE(h && gate_weight && expert_bias && down_bias && dense_weights && bias_out,
-              "moe_route: null pointer");
+  LFS_REQUIRE(h && gate_weight && expert_bias, "moe_route: null pointer");
+  LFS_REQUIRE(bias_out == nullptr || down_bias != nullptr, "moe_route: bias_out needs down_bias");
+  LFS_REQUIRE(dense_weights != nullptr || topk_idx != nullptr, "moe_route: no output");
   LFS_REQUIRE(((uintptr_t)h | (uintptr_t)gate_weight) % 16 == 0, "moe_route: h and gate_weight must be 16-byte aligned");
+  LFS_REQUIRE((topk_idx == nullptr) == (topk_weight == nullptr), "moe_route: topk_idx and topk_weight go together");
   hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)T), dim3(256), 0, (hipStream_t)stream,
                      (const uint16_t*)h, (const uint16_t*)gate_weight, expert_bias, down_bias,
-                     dense_weights, bias_out, d, num_experts, num_shared, top_k);
+                     dense_weights, bias_out, d, num_experts, num_shared, top_k, topk_idx, topk_weight);
   return check_launch("moe_route");
 }
 

@@ -172,7 +172,21 @@ class MoE(nn.Module):
         accumulator sums sum_e w_e * (w2_e h_e) directly, plus the bias
         matrix.
     The reference rounds each expert's output to bf16 and scatter-adds in
-    bf16 (moe.py:288-341); here the weighted sum is rounded once."""
+    bf16 (moe.py:288-341); here the weighted sum is rounded once.
+
+    Grouped dispatch (prefill-sized batches, ``dispatch`` "grouped", or
+    "auto" with more than GROUPED_MIN_TOKENS tokens): only the picked
+    experts run.  moe_route also returns the picks in index form,
+    moe_align groups the (token, pick) entries by expert into 128-row
+    tiles on the GPU (no host sync), one grouped FP8 GEMM runs w13 over
+    each expert's gathered rows (the same stacked weights, viewed
+    [E, 2F, d]), swiglu_quant folds each row's routing weight into its
+    scales, a second grouped GEMM runs w2 (the K-stacked matrix viewed
+    [E, d, F]) into fp32 rows, and moe_combine sums each token's rows and
+    its weighted down biases, rounding once.  Both dispatches compute the
+    same sum up to fp32 summation order."""
+
+    GROUPED_MIN_TOKENS = 256
 
     def __init__(self, cfg: DecodeModelConfig, device=None):
         super().__init__()
@@ -188,6 +202,21 @@ class MoE(nn.Module):
         self.w13 = FP8Linear(cfg.d_model, E * 2 * cfg.d_ff, device=device)
         self.w2 = FP8Linear(E * cfg.d_ff, cfg.d_model, bias=False, device=device)
         self.register_buffer("w2_bias", torch.zeros(E, cfg.d_model, device=device))
+        self.dispatch = "auto"  # "dense" | "grouped" | "auto"
+
+    def _expert_views(self):
+        """Per-expert views of the stacked weights for the grouped GEMMs:
+        w13 [E, 2F, d] (+ scales [E, 2F/128, d/128], bias [E, 2F]) and w2
+        [E, d, F] (columns e*F .. of the K-stacked matrix; scales
+        [E, ceil(d/128), F/128])."""
+        E, F = self.n_experts + self.n_shared, self.d_ff
+        d = self.w2.out_features
+        w13 = self.w13.weight.view(E, 2 * F, d)
+        w13s = self.w13.weight_scale.view(E, 2 * F // 128, d // 128)
+        b13 = self.w13.bias.view(E, 2 * F)
+        w2 = self.w2.weight.view(d, E, F).permute(1, 0, 2)
+        w2s = self.w2.weight_scale.view(-1, E, F // 128).permute(1, 0, 2)
+        return w13, w13s, b13, w2, w2s
 
     @torch.no_grad()
     def load_experts(self, experts: list[tuple]) -> None:
@@ -204,6 +233,8 @@ class MoE(nn.Module):
         """h: the ffn_norm output (bf16, for the gate); hq, hs: the same
         quantised (for the experts)."""
         T, F = h.size(0), self.d_ff
+        if self.dispatch == "grouped" or (self.dispatch == "auto" and T > self.GROUPED_MIN_TOKENS):
+            return self.forward_grouped(h, hq, hs, trace)
         w, bias = kernels.moe_route(h, self.gate_weight, self.expert_bias, self.w2_bias, self.top_k,
                                     self.n_shared)
         h13 = self.w13.gemm(hq, hs)
@@ -211,6 +242,24 @@ class MoE(nn.Module):
         y = kernels.fp8_gemm(gq, gs, self.w2.weight, self.w2.weight_scale, bias)
         if trace is not None:
             trace.update(route_w=w, route_bias=bias, h13=h13, ffn_out=y)
+        return y
+
+    def forward_grouped(self, h: torch.Tensor, hq: torch.Tensor, hs: torch.Tensor,
+                        trace: Optional[dict] = None) -> torch.Tensor:
+        """MoE.moe_infer (model/architecture/moe.py:288-341) plus the shared
+        expert, with only the picked experts computed."""
+        E, S, F = self.n_experts, self.n_shared, self.d_ff
+        _, _, idx, wt = kernels.moe_route(h, self.gate_weight, self.expert_bias, None, self.top_k, S,
+                                          dense=False, return_topk=True)
+        rows = kernels.moe_align(idx, wt, E, S)
+        w13, w13s, b13, w2, w2s = self._expert_views()
+        h13 = kernels.fp8_grouped_gemm(hq, hs, rows.row_token, rows.tile_expert, w13, w13s, b13)
+        P = rows.num_rows
+        gq, gs = kernels.swiglu_quant(h13.view(P, 1, 2, F), rows.row_weight.view(P, 1))
+        out = kernels.fp8_grouped_gemm(gq, gs, None, rows.tile_expert, w2, w2s, out_dtype=torch.float32)
+        y = kernels.moe_combine(out, rows.entry_row, idx, wt, E, S, self.w2_bias)
+        if trace is not None:
+            trace.update(topk_idx=idx, topk_weight=wt, moe_rows=rows, h13_rows=h13, ffn_out=y)
         return y
 
 

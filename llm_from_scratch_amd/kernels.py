@@ -468,29 +468,41 @@ def qk_norm_rope_store(qkv: torch.Tensor, q_weight: torch.Tensor, k_weight: torc
 
 
 def moe_route(h: torch.Tensor, gate_weight: torch.Tensor, expert_bias: torch.Tensor,
-              down_bias: torch.Tensor, top_k: int, num_shared: int):
-    """MoE gate (model/architecture/moe.py:45-90) as dense weights.
+              down_bias: Optional[torch.Tensor], top_k: int, num_shared: int, dense: bool = True,
+              return_topk: bool = False):
+    """MoE gate (model/architecture/moe.py:45-90).
 
     h: bf16 [T, d]; gate_weight bf16 [E, d]; expert_bias fp32 [E];
-    down_bias fp32 [E + S, d].  Returns (weights fp32 [T, E + S] -- the
-    renormalised top-k sigmoid scores, 0 for unpicked experts, 1 for the S
-    shared experts -- and bias fp32 [T, d] = weights @ down_bias).
+    down_bias fp32 [E + S, d] or None.  Returns (weights fp32 [T, E + S] --
+    the renormalised top-k sigmoid scores, 0 for unpicked experts, 1 for the
+    S shared experts -- and bias fp32 [T, d] = weights @ down_bias, None
+    without down_bias); with ``dense=False`` both are None.  With
+    ``return_topk`` also (topk_idx int64 [T, top_k], topk_weight fp32
+    [T, top_k]), the gate's index form in pick order.
     """
     assert h.dim() == 2 and h.is_contiguous() and gate_weight.is_contiguous()
+    assert dense or return_topk, "moe_route: nothing to return"
     T, d = h.shape
     E = gate_weight.size(0)
-    _on_gpu(h, gate_weight, expert_bias, down_bias)
+    _on_gpu(h, gate_weight, expert_bias)
     _dtype(h, torch.bfloat16, "h")
     _dtype(gate_weight, torch.bfloat16, "gate_weight")
     _dtype(expert_bias, torch.float32, "expert_bias")
-    _dtype(down_bias, torch.float32, "down_bias")
     assert gate_weight.shape == (E, d) and expert_bias.shape == (E,)
-    assert down_bias.shape == (E + num_shared, d) and down_bias.is_contiguous()
-    w = torch.empty(T, E + num_shared, dtype=torch.float32, device=h.device)
-    bias = torch.empty(T, d, dtype=torch.float32, device=h.device)
+    if down_bias is not None:
+        _on_gpu(h, down_bias)
+        _dtype(down_bias, torch.float32, "down_bias")
+        assert down_bias.shape == (E + num_shared, d) and down_bias.is_contiguous()
+    w = torch.empty(T, E + num_shared, dtype=torch.float32, device=h.device) if dense else None
+    bias = torch.empty(T, d, dtype=torch.float32, device=h.device) if dense and down_bias is not None else None
+    idx = torch.empty(T, top_k, dtype=torch.int64, device=h.device) if return_topk else None
+    wt = torch.empty(T, top_k, dtype=torch.float32, device=h.device) if return_topk else None
     rc = _lib.load().lfs_moe_route(_ptr(h), _ptr(gate_weight), _ptr(expert_bias), _ptr(down_bias),
-                                   _ptr(w), _ptr(bias), T, d, E, num_shared, top_k, _stream(h))
+                                   _ptr(w), _ptr(bias), T, d, E, num_shared, top_k, _ptr(idx), _ptr(wt),
+                                   _stream(h))
     _lib.check(rc, "moe_route")
+    if return_topk:
+        return w, bias, idx, wt
     return w, bias
 
 
@@ -515,3 +527,184 @@ def swiglu_quant(h13: torch.Tensor, route_weights: torch.Tensor):
                                       _stream(h13))
     _lib.check(rc, "swiglu_quant")
     return q, qs
+
+
+# ------------------------------------------------------------ MoE dispatch --
+class MoeRows:
+    """Result of moe_align: rows grouped by expert in 128-row tiles.
+
+    row_token int32 [P] (token of each row, -1 padding), row_weight fp32 [P]
+    (0 padding), tile_expert int32 [P / 128] (-1 past the last segment),
+    entry_row int32 [T, top_k + S] (row of each (token, pick), -1 if
+    dropped); P = num_tiles * 128."""
+
+    def __init__(self, row_token, row_weight, tile_expert, entry_row):
+        self.row_token, self.row_weight = row_token, row_weight
+        self.tile_expert, self.entry_row = tile_expert, entry_row
+
+    @property
+    def num_rows(self) -> int:
+        return self.row_token.numel()
+
+
+def moe_align_tiles(T: int, top_k: int, num_experts: int, num_shared: int) -> int:
+    """128-row tiles moe_align may fill (its output size; fixed per T)."""
+    return int(_lib.load().lfs_moe_align_tiles(T, top_k, num_experts, num_shared))
+
+
+def moe_align(topk_idx: torch.Tensor, topk_weight: torch.Tensor, num_experts: int,
+              num_shared: int = 0) -> MoeRows:
+    """Group a batch's (token, pick) entries by expert -- the argsort +
+    bincount + offsets of MoE.moe_infer (model/architecture/moe.py:298-307)
+    on the GPU, with no host sync and an output size fixed by T.
+
+    topk_idx int64 [T, k], topk_weight fp32 [T, k] (the gate's outputs);
+    the S shared experts (indices E .. E+S-1, weight 1) are appended to
+    every token.  Each expert's rows keep the entries' flat order."""
+    assert topk_idx.dim() == 2 and topk_idx.is_contiguous() and topk_weight.is_contiguous()
+    _on_gpu(topk_idx, topk_weight)
+    _dtype(topk_idx, torch.int64, "topk_idx")
+    _dtype(topk_weight, torch.float32, "topk_weight")
+    T, k = topk_idx.shape
+    assert topk_weight.shape == (T, k)
+    tiles = moe_align_tiles(T, k, num_experts, num_shared)
+    dev = topk_idx.device
+    row_token = torch.empty(tiles * 128, dtype=torch.int32, device=dev)
+    row_weight = torch.empty(tiles * 128, dtype=torch.float32, device=dev)
+    tile_expert = torch.empty(tiles, dtype=torch.int32, device=dev)
+    entry_row = torch.empty(T, k + num_shared, dtype=torch.int32, device=dev)
+    rc = _lib.load().lfs_moe_align(_ptr(topk_idx), _ptr(topk_weight), T, k, num_experts, num_shared,
+                                   _ptr(row_token), _ptr(row_weight), _ptr(tile_expert), tiles, _ptr(entry_row),
+                                   _stream(topk_idx))
+    _lib.check(rc, "moe_align")
+    return MoeRows(row_token, row_weight, tile_expert, entry_row)
+
+
+def fp8_grouped_gemm(a: torch.Tensor, a_s: torch.Tensor, row_index: Optional[torch.Tensor],
+                     tile_expert: torch.Tensor, b: torch.Tensor, b_s: torch.Tensor,
+                     bias: Optional[torch.Tensor] = None, out_dtype: torch.dtype = torch.bfloat16
+                     ) -> torch.Tensor:
+    """Per-expert block-scaled FP8 GEMMs over 128-row tiles (the expert MLP
+    calls of MoE.moe_infer, model/architecture/moe.py:318-330, batched).
+
+    a e4m3fn [A, K], a_s fp32 [A, K/128]; tile_expert int32 [tiles]; row m
+    of the output (tile m // 128) is a[row_index[m]] (row_index int32
+    [tiles*128], -1 = padding) or a[m] (row_index None) times expert
+    e = tile_expert[m // 128]'s weights b[e] (e4m3fn [E, N, K], any strides
+    with unit K stride, e.g. a permuted view of a matrix stacked along K),
+    scales b_s[e] (fp32 [E, ceil(N/128), K/128], unit last stride), plus
+    bias[e] (fp32 [E, N]) for a bf16 output.  Returns [tiles*128, N] in
+    out_dtype (bfloat16, or float32 without bias); rows of tiles with
+    e < 0 are left unwritten."""
+    _on_gpu(a, a_s, tile_expert, b, b_s)
+    _dtype(a, FP8, "a")
+    _dtype(b, FP8, "b")
+    _dtype(a_s, torch.float32, "a_s")
+    _dtype(b_s, torch.float32, "b_s")
+    _dtype(tile_expert, torch.int32, "tile_expert")
+    assert a.dim() == 2 and a.is_contiguous() and a_s.is_contiguous(), "a, a_s must be contiguous [A, K]"
+    A, K = a.shape
+    assert K % 128 == 0 and a_s.shape == (A, K // 128)
+    assert b.dim() == 3 and b.size(2) == K and b.stride(2) == 1, "b must be [E, N, K] with unit K stride"
+    E, N, _ = b.shape
+    assert b_s.dim() == 3 and b_s.shape == (E, math.ceil(N / 128), K // 128) and b_s.stride(2) == 1
+    assert tile_expert.dim() == 1 and tile_expert.is_contiguous()
+    tiles = tile_expert.numel()
+    if row_index is not None:
+        _on_gpu(a, row_index)
+        _dtype(row_index, torch.int32, "row_index")
+        assert row_index.is_contiguous() and row_index.numel() == tiles * 128
+    else:
+        assert A >= tiles * 128, "without row_index, a needs tiles*128 rows"
+    assert out_dtype in (torch.bfloat16, torch.float32)
+    bias_es = 0
+    if bias is not None:
+        assert out_dtype == torch.bfloat16, "the fp32 output takes no bias"
+        _on_gpu(a, bias)
+        _dtype(bias, torch.float32, "bias")
+        assert bias.shape == (E, N) and bias.stride(1) == 1
+        bias_es = bias.stride(0)
+    c = torch.empty(tiles * 128, N, dtype=out_dtype, device=a.device)
+    is_f32 = out_dtype == torch.float32
+    rc = _lib.load().lfs_fp8_grouped_gemm(
+        _ptr(a), _ptr(a_s), A, _ptr(row_index), _ptr(tile_expert), tiles, _ptr(b), _ptr(b_s), b.stride(0),
+        b.stride(1), b_s.stride(0), b_s.stride(1), _ptr(bias), bias_es, None if is_f32 else _ptr(c),
+        _ptr(c) if is_f32 else None, N, K, _stream(a))
+    _lib.check(rc, "fp8_grouped_gemm")
+    return c
+
+
+def moe_combine(out: torch.Tensor, entry_row: torch.Tensor, topk_idx: torch.Tensor, topk_weight: torch.Tensor,
+                num_experts: int, num_shared: int = 0, down_bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y[t] = bf16(sum_j out[entry_row[t, j]] + sum_j w_tj * down_bias[e_tj])
+    over the token's picks then its shared experts, fp32 in that order: the
+    scatter_add_ of MoE.moe_infer (model/architecture/moe.py:332-339) plus
+    the shared-expert add (:272-273).  out: fp32 [rows, d] (routing weights
+    already applied); down_bias fp32 [E + S, d] or None."""
+    _on_gpu(out, entry_row, topk_idx, topk_weight)
+    _dtype(out, torch.float32, "out")
+    _dtype(entry_row, torch.int32, "entry_row")
+    assert out.dim() == 2 and out.stride(1) == 1 and entry_row.is_contiguous()
+    T, k = topk_idx.shape
+    assert entry_row.shape == (T, k + num_shared)
+    d = out.size(1)
+    if down_bias is not None:
+        _on_gpu(out, down_bias)
+        _dtype(down_bias, torch.float32, "down_bias")
+        assert down_bias.shape == (num_experts + num_shared, d) and down_bias.is_contiguous()
+    y = torch.empty(T, d, dtype=torch.bfloat16, device=out.device)
+    rc = _lib.load().lfs_moe_combine(_ptr(out), out.stride(0), _ptr(entry_row), _ptr(topk_idx), _ptr(topk_weight),
+                                     T, k, num_experts, num_shared, _ptr(down_bias), d, _ptr(y), _stream(out))
+    _lib.check(rc, "moe_combine")
+    return y
+
+
+def _seg_args(expert_output: torch.Tensor, weights: torch.Tensor, idx: torch.Tensor):
+    assert expert_output.dim() == 2 and expert_output.stride(1) == 1, "expert_output must be [n, d] rows"
+    assert expert_output.dtype in (torch.bfloat16, torch.float32), "expert_output must be bf16 or fp32"
+    assert weights.dtype in (torch.bfloat16, torch.float32), "weights must be bf16 or fp32"
+    _on_gpu(expert_output, weights, idx)
+    _dtype(idx, torch.int64, "token indices")
+    weights = weights.reshape(-1).contiguous()
+    idx = idx.reshape(-1).contiguous()
+    n = expert_output.size(0)
+    assert weights.numel() == n and idx.numel() == n
+    return weights, idx, n
+
+
+def segment_reduce_weighted(expert_output: torch.Tensor, sorted_weights: torch.Tensor,
+                            sorted_token_idx: torch.Tensor, num_tokens: int, top_k: int) -> torch.Tensor:
+    """model/architecture/moe_kernels.py:70-125: y[t] = sum of
+    expert_output[p] * sorted_weights[p] over the segment of p with
+    sorted_token_idx[p] == t (sorted_token_idx non-decreasing), fp32
+    accumulation, returned in expert_output's dtype [num_tokens, d].
+    ``top_k`` is accepted for the signature; every entry of a segment is
+    summed."""
+    w, idx, n = _seg_args(expert_output, sorted_weights, sorted_token_idx)
+    d = expert_output.size(1)
+    y = torch.empty(num_tokens, d, dtype=expert_output.dtype, device=expert_output.device)
+    rc = _lib.load().lfs_segment_reduce_weighted(
+        _ptr(expert_output), int(expert_output.dtype == torch.float32), expert_output.stride(0), _ptr(w),
+        int(w.dtype == torch.float32), _ptr(idx), n, num_tokens, d, _ptr(y), _stream(expert_output))
+    _lib.check(rc, "segment_reduce_weighted")
+    return y
+
+
+def fused_scatter_add_weighted(expert_output: torch.Tensor, sorted_token_idx: torch.Tensor,
+                               sorted_weights: torch.Tensor, num_tokens: int, top_k: int = 2) -> torch.Tensor:
+    """model/architecture/moe_kernels.py:128-171: y[t] = sum over entries i
+    with sorted_token_idx[i] == t (any order) of expert_output[i] *
+    sorted_weights[i], fp32 accumulation in increasing i, returned in
+    expert_output's dtype [num_tokens, d].  ``top_k`` is accepted for the
+    signature."""
+    w, idx, n = _seg_args(expert_output, sorted_weights, sorted_token_idx)
+    d = expert_output.size(1)
+    L = _lib.load()
+    ws = torch.empty(max(1, int(L.lfs_scatter_add_weighted_workspace_bytes(n, num_tokens)) // 4),
+                     dtype=torch.int32, device=expert_output.device)
+    y = torch.empty(num_tokens, d, dtype=expert_output.dtype, device=expert_output.device)
+    rc = L.lfs_scatter_add_weighted(_ptr(expert_output), int(expert_output.dtype == torch.float32),
+                                    expert_output.stride(0), _ptr(w), int(w.dtype == torch.float32), _ptr(idx), n,
+                                    num_tokens, d, _ptr(y), _ptr(ws), ws.numel() * 4, _stream(expert_output))
+    _lib.check(rc, "fused_scatter_add_weighted")
+    return y

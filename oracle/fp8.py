@@ -194,7 +194,8 @@ def weight_dequant(codes, s, block_size: int = 128) -> np.ndarray:
 # ---------------------------------------------------------------------------
 # block-scaled FP8 GEMM: C[m, n] = sum_kb a_s[m,kb] b_s[n//128,kb] A_kb . B_kb
 # ---------------------------------------------------------------------------
-def fp8_gemm(a, a_s, b, b_s, bias=None, block_size: int = 128, accum=np.float64) -> np.ndarray:
+def fp8_gemm(a, a_s, b, b_s, bias=None, block_size: int = 128, accum=np.float64,
+             round_bf16: bool = True) -> np.ndarray:
     """a: uint8 [M,K] codes, a_s float32 [M, K/bs]; b: uint8 [N,K] codes,
     b_s float32 [ceil(N/bs), K/bs].  Returns bf16 values (as float32) of
     ``sum_kb (a_s*b_s) * (A_kb @ B_kb^T) (+ bias)``.
@@ -203,6 +204,7 @@ def fp8_gemm(a, a_s, b, b_s, bias=None, block_size: int = 128, accum=np.float64)
     parity oracle).  accum=np.float32: one fp32 matmul per K block with the
     scale product applied to the partial in an fp32 accumulator -- the same
     structure as the GPU kernel, used as the timed CPU baseline.
+    round_bf16=False returns the unrounded sum (in ``accum``).
     """
     a = np.asarray(a, np.uint8)
     b = np.asarray(b, np.uint8)
@@ -223,6 +225,8 @@ def fp8_gemm(a, a_s, b, b_s, bias=None, block_size: int = 128, accum=np.float64)
     if bias is not None:
         bias = np.asarray(bias, dtype=accum)
         acc = acc + (bias[None, :] if bias.ndim == 1 else bias)
+    if not round_bf16:
+        return acc
     return bf16_round(acc.astype(np.float32))
 
 

@@ -64,10 +64,32 @@ def test_argument_errors_are_reported_without_launch(lib):
     rc = lib.lfs_qk_norm_rope_store(None, 1280, None, None, None, None, None, None, None, None, 4, 12, 4, 72,
                                     0, 4096, 1e-6, None)
     assert rc == -1 and b"head_dim" in lib.lfs_last_error()
-    rc = lib.lfs_moe_route(None, None, None, None, None, None, 4, 768, 8, 1, 9, None)
+    rc = lib.lfs_moe_route(None, None, None, None, None, None, 4, 768, 8, 1, 9, None, None, None)
     assert rc == -1 and b"top_k" in lib.lfs_last_error()
+    rc = lib.lfs_moe_route(16, 16, 16, None, 16, 16, 4, 768, 8, 1, 2, None, None, None)
+    assert rc == -1 and b"down_bias" in lib.lfs_last_error()
     rc = lib.lfs_swiglu_quant(None, None, None, None, 4, 9, 500, None)
     assert rc == -1 and b"d_ff" in lib.lfs_last_error()
+    # MoE dispatch: capacity too small, too many experts, fp32 output with a bias, bad K
+    rc = lib.lfs_moe_align(16, 16, 100, 2, 8, 1, 16, 16, 16, 3, 16, None)
+    assert rc == -1 and b"tiles needed" in lib.lfs_last_error()
+    rc = lib.lfs_moe_align(16, 16, 100, 2, 64, 1, 16, 16, 16, 1000, 16, None)
+    assert rc == -1 and b"at most 64 experts" in lib.lfs_last_error()
+    rc = lib.lfs_fp8_grouped_gemm(16, 16, 8, None, 16, 1, 16, 16, 0, 256, 0, 2, 16, 0, None, 16, 128, 256, None)
+    assert rc == -1 and b"no bias" in lib.lfs_last_error()
+    rc = lib.lfs_fp8_grouped_gemm(16, 16, 8, None, 16, 1, 16, 16, 0, 256, 0, 2, None, 0, 16, None, 128, 200, None)
+    assert rc == -1 and b"multiple of 128" in lib.lfs_last_error()
+    rc = lib.lfs_moe_combine(16, 100, 16, 16, 16, 4, 2, 8, 1, None, 100, 16, None)
+    assert rc == -1 and b"multiple of 8" in lib.lfs_last_error()
+    rc = lib.lfs_scatter_add_weighted(16, 0, 8, 16, 1, 16, 10, 5, 8, 16, None, 0, None)
+    assert rc == -1 and b"workspace" in lib.lfs_last_error()
+
+
+def test_moe_capacity_helpers(lib):
+    # 100 tokens x (2 picks + 1 shared) over 9 experts: (300 + 9*127 + 127) // 128
+    assert lib.lfs_moe_align_tiles(100, 2, 8, 1) == (300 + 9 * 127 + 127) // 128
+    assert lib.lfs_moe_align_tiles(0, 2, 8, 1) == 0
+    assert lib.lfs_scatter_add_weighted_workspace_bytes(10, 5) == 4 * (3 * 5 + 1 + 10)
 
 
 def test_gemm_workspace_bytes(lib):
