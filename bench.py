@@ -175,6 +175,39 @@ def bench_indexer(device, reps):
             "frac": fl / t / 1e12 / FP8_PEAK_TFLOPS, "flop": fl}
 
 
+def bench_moe(device, reps):
+    """The MoE layer of cfg5 (d 768, d_ff 512, 8 routed experts top-2 + 1
+    shared, random nn.Linear-init weights) over a prefill batch of 16384
+    tokens, dispatched grouped (moe_route -> moe_align -> grouped w13 GEMM
+    -> swiglu_quant -> grouped w2 GEMM -> moe_combine) and dense (every
+    expert over every token).  Algorithmic flop = 2 * T * (top_k + S) *
+    3 * d * d_ff (the picked experts' three projections)."""
+    from llm_from_scratch_amd import kernels as K
+    from llm_from_scratch_amd.decode_model import DecodeModel, DecodeModelConfig
+    cfg = DecodeModelConfig(vocab_size=256, num_layers=1, max_model_length=64)
+    model = DecodeModel(cfg, device=device, seed=11)
+    f = model.layers[0].ffn
+    T = 16384
+    g = torch.Generator(device=device).manual_seed(12)
+    h = torch.randn(T, cfg.d_model, generator=g, device=device).to(torch.bfloat16)
+    hq, hs = K.act_quant(h)
+    kk = cfg.num_experts_per_tok + cfg.n_shared_experts
+    fl = 2.0 * T * kk * 3 * cfg.d_model * cfg.d_ff
+    out = {"tokens": T, "experts": [cfg.n_routed_experts, cfg.num_experts_per_tok, cfg.n_shared_experts],
+           "d_model": cfg.d_model, "d_ff": cfg.d_ff, "flop": fl}
+    with torch.no_grad():
+        for mode in ("grouped", "dense"):
+            f.dispatch = mode
+            fn = lambda: f(h, hq, hs)  # noqa: E731
+            fn()
+            torch.cuda.synchronize()
+            t = timed_launches([fn], reps)[0]
+            out[mode] = {"us": t * 1e6, "TFLOP/s": fl / t / 1e12, "frac": fl / t / 1e12 / FP8_PEAK_TFLOPS}
+    del model, f
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_decode(name, device, reps, flush_buf):
     from llm_from_scratch_amd import kernels as K
     from llm_from_scratch_amd import workloads as W
@@ -285,9 +318,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip decode / act_quant lines")
-    ap.add_argument("--extras", default="act_quant,cfg3,cfg4,prefill,indexer,cfg5",
+    ap.add_argument("--extras", default="act_quant,cfg3,cfg4,prefill,indexer,moe,cfg5",
                     help="comma list of extra lines: act_quant, cfg3, cfg4 (paged decode), prefill "
-                         "(varlen prefill attention), indexer (DSA fp8_index), cfg5 (decode step)")
+                         "(varlen prefill attention), indexer (DSA fp8_index), moe (MoE layer, grouped "
+                         "vs dense dispatch), cfg5 (decode step)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 4 plain device copies of 256 MiB (a known-traffic kernel for "
                          "scaling FETCH_SIZE / WRITE_SIZE counters)")
@@ -361,6 +395,9 @@ def main():
         if "indexer" in extras:
             log("bench: fp8_index")
             out["fp8_index"] = bench_indexer(dev, 10)
+        if "moe" in extras:
+            log("bench: MoE layer (grouped / dense dispatch)")
+            out["moe_layer"] = bench_moe(dev, 10)
         if "prefill" in extras:
             log("bench: prefill attention")
             out["prefill_attention"] = bench_prefill(dev, 10)

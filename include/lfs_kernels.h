@@ -60,6 +60,7 @@
  * MoE expert dispatch (MoE.moe_infer, model/architecture/moe.py:288-341,
  * without its argsort / bincount / .tolist() host sync and scatter_add_):
  *   lfs_moe_align_tiles     capacity (128-row tiles) lfs_moe_align needs
+ *   lfs_moe_align_workspace_bytes
  *   lfs_moe_align           (token, pick) entries grouped by expert into
  *                           128-row tiles (moe.py:298-307)
  *   lfs_fp8_grouped_gemm    one FP8 block-scaled GEMM per expert segment (the
@@ -82,7 +83,7 @@
 extern "C" {
 #endif
 
-#define LFS_ABI_VERSION 4
+#define LFS_ABI_VERSION 5
 
 /* argument errors (negative); launch errors are positive hipError_t values */
 #define LFS_EINVAL (-1)
@@ -317,12 +318,19 @@ int64_t lfs_moe_align_tiles(int64_t T, int32_t top_k, int32_t num_experts, int32
  *   tile_expert[i] (int32 [num_tiles])    expert of rows 128i .. 128i+127,
  *                                         -1 for tiles past the last segment
  *   entry_row[i] (int32 [T*(top_k+S)])    row of entry i (-1 if dropped)
- * num_tiles >= lfs_moe_align_tiles(...); E + S <= 64.  One workgroup; the
- * launch shape depends only on num_tiles (graph-capturable).
+ * num_tiles >= lfs_moe_align_tiles(...); E + S <= 64.  Three launches
+ * (per-chunk ranks, one-workgroup offsets, per-chunk placement) whose shapes
+ * depend only on T and num_tiles (graph-capturable); the caller-owned int32
+ * workspace holds the per-chunk counts.
  */
 int lfs_moe_align(const int64_t* topk_idx, const float* topk_weight, int64_t T, int32_t top_k,
                   int32_t num_experts, int32_t num_shared, int32_t* row_token, float* row_weight,
-                  int32_t* tile_expert, int64_t num_tiles, int32_t* entry_row, void* stream);
+                  int32_t* tile_expert, int64_t num_tiles, int32_t* entry_row, void* workspace,
+                  int64_t workspace_bytes, void* stream);
+
+/* workspace bytes of lfs_moe_align: 4 * (chunks * (E + S) + 2 * (E + S) + 1),
+ * chunks = ceil(T * (top_k + S) / 1024) */
+int64_t lfs_moe_align_workspace_bytes(int64_t T, int32_t top_k, int32_t num_experts, int32_t num_shared);
 
 /*
  * fp8_grouped_gemm: for every tile i < num_tiles with e = tile_expert[i] >= 0

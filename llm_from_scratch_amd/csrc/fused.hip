@@ -223,12 +223,156 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(
 }
 
 // --------------------------------------------------------------- moe_route --
-// One workgroup of 4 waves per token.  Wave w computes the gate logits of
-// experts w, w+4, ... (lane l sums chunks l, l+64, ... then a butterfly);
-// wave 0 picks the top k; all 256 threads form the routed bias.
+// Large batches: four tokens per workgroup.  Phase 1, one wave per token: lane l sums the
+// products of 16-byte chunks l, l+64, ... of the token row with the same
+// chunks of up to 8 experts' gate rows at a time, then a butterfly per
+// expert leaves expert e's logit in lane e; the top k is a repeated wave
+// argmax.  Phase 2, the whole workgroup: the routed bias of the four tokens,
+// one column per thread and pass (each b2 value loaded once for the four).
 constexpr int kMaxExperts = 64;
+constexpr int kRouteTokens = 4;  // tokens (waves) per workgroup
+constexpr int kRouteSmallT = 1024;  // up to this many tokens: one workgroup per token
 
-__global__ __launch_bounds__(256) void moe_route_kernel(
+__global__ __launch_bounds__(64 * kRouteTokens) void moe_route_kernel(
+    const uint16_t* __restrict__ h, const uint16_t* __restrict__ gw, const float* __restrict__ ebias,
+    const float* __restrict__ b2, float* __restrict__ dense, float* __restrict__ bias_out, int64_t T, int d,
+    int E, int S, int top_k, int64_t* __restrict__ topk_idx, float* __restrict__ topk_w) {
+  __shared__ float wsel[kRouteTokens][kMaxExperts];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t t0 = (int64_t)blockIdx.x * kRouteTokens;
+  const int64_t t = t0 + wave;
+  if (t < T) {
+    const int cpr = d / 8;
+    const uint16_t* hrow = h + t * d;
+    float logit = 0.f;  // lane e: expert e's logit
+    for (int e0 = 0; e0 < E; e0 += 8) {
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int c = lane; c < cpr; c += 64) {
+        float hv[8];
+        unpack8(*reinterpret_cast<const uint4*>(hrow + c * 8), hv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (e0 + j >= E) break;
+          float gv[8];
+          unpack8(*reinterpret_cast<const uint4*>(gw + (int64_t)(e0 + j) * d + c * 8), gv);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[j] = add_rn(acc[j], mul_rn(hv[i], gv[i]));
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (e0 + j >= E) break;
+        const float tot = group_sum<64>(acc[j]);
+        if (lane == e0 + j) logit = tot;
+      }
+    }
+    const bool valid = lane < E;
+    // sigmoid score and biased logit of expert `lane`
+    const float score = valid ? 1.0f / (1.0f + expf(-logit)) : 0.f;
+    const float key = valid ? add_rn(logit, ebias[lane]) : -INFINITY;
+    // top-k by repeated wave argmax (ties: lowest expert index)
+    bool chosen = false;
+    int myk = -1;  // pick order of this lane's expert
+    float wsum = 0.f;
+    for (int k = 0; k < top_k; ++k) {
+      float best = chosen ? -INFINITY : key;
+      int bi = valid && !chosen ? lane : kMaxExperts;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const float ob = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (ob > best || (ob == best && oi < bi)) { best = ob; bi = oi; }
+      }
+      if (lane == bi) { chosen = true; myk = k; }
+      wsum = add_rn(wsum, __shfl(score, bi < 64 ? bi : 0, 64) * (bi < 64 ? 1.f : 0.f));
+    }
+    float wgt = chosen ? score : 0.f;
+    if (top_k > 1) wgt = chosen ? wgt / add_rn(wsum, 1e-10f) : 0.f;
+    const float v = lane < E ? wgt : (lane < E + S ? 1.0f : 0.f);  // lane e: weight of expert e
+    wsel[wave][lane] = v;
+    if (dense != nullptr && lane < E + S) dense[t * (E + S) + lane] = v;
+    // the picks in index form (the reference gate's topk_idx / topk_weight)
+    if (topk_idx != nullptr && chosen) {
+      topk_idx[t * top_k + myk] = lane;
+      topk_w[t * top_k + myk] = wgt;
+    }
+  } else {
+    wsel[wave][lane] = 0.f;
+  }
+  if (bias_out == nullptr) return;  // uniform: no barrier below is skipped by part of the workgroup
+  __syncthreads();
+  // routed bias: sum_e w[e] * b2[e, n], experts in index order
+  const int EE = E + S;
+  if (EE <= 16) {
+    // every b2 load of a pass issued before the first use: one memory latency
+    for (int n0 = 0; n0 < d; n0 += 64 * kRouteTokens * 4) {
+      float bv[16][4];
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int n = n0 + threadIdx.x + 64 * kRouteTokens * c;
+          bv[e][c] = (e < EE && n < d) ? b2[(int64_t)e * d + n] : 0.f;
+        }
+#pragma unroll
+      for (int w = 0; w < kRouteTokens; ++w) {
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          if (e < EE) {
+            const float we = wsel[w][e];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[c] = add_rn(acc[c], mul_rn(we, bv[e][c]));
+          }
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int n = n0 + threadIdx.x + 64 * kRouteTokens * c;
+          if (n < d && t0 + w < T) bias_out[(t0 + w) * d + n] = acc[c];
+        }
+      }
+    }
+    return;
+  }
+  for (int n0 = 0; n0 < d; n0 += 64 * kRouteTokens * 4) {
+    float acc[kRouteTokens][4] = {};
+    for (int e0 = 0; e0 < EE; e0 += 2) {
+      float bv[2][4];
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int n = n0 + threadIdx.x + 64 * kRouteTokens * c;
+          bv[x][c] = (e0 + x < EE && n < d) ? b2[(int64_t)(e0 + x) * d + n] : 0.f;
+        }
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        if (e0 + x < EE) {
+#pragma unroll
+          for (int w = 0; w < kRouteTokens; ++w) {
+            const float we = wsel[w][e0 + x];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[w][c] = add_rn(acc[w][c], mul_rn(we, bv[x][c]));
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int w = 0; w < kRouteTokens; ++w) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int n = n0 + threadIdx.x + 64 * kRouteTokens * c;
+        if (n < d && t0 + w < T) bias_out[(t0 + w) * d + n] = acc[w][c];
+      }
+    }
+  }
+}
+
+// Small batches (decode): one workgroup of 4 waves per token, so that the
+// tokens spread over as many CUs as possible.  Wave w computes the gate
+// logits of experts w, w+4, ... (lane l sums chunks l, l+64, ... then a
+// butterfly); wave 0 picks the top k; all 256 threads form the routed bias.
+__global__ __launch_bounds__(256) void moe_route_token_kernel(
     const uint16_t* __restrict__ h, const uint16_t* __restrict__ gw, const float* __restrict__ ebias,
     const float* __restrict__ b2, float* __restrict__ dense, float* __restrict__ bias_out, int d,
     int E, int S, int top_k, int64_t* __restrict__ topk_idx, float* __restrict__ topk_w) {
@@ -414,9 +558,16 @@ extern "C" int lfs_moe_route(const void* h, const void* gate_weight, const float
   LFS_REQUIRE(dense_weights != nullptr || topk_idx != nullptr, "moe_route: no output");
   LFS_REQUIRE(((uintptr_t)h | (uintptr_t)gate_weight) % 16 == 0, "moe_route: h and gate_weight must be 16-byte aligned");
   LFS_REQUIRE((topk_idx == nullptr) == (topk_weight == nullptr), "moe_route: topk_idx and topk_weight go together");
-  hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)T), dim3(256), 0, (hipStream_t)stream,
-                     (const uint16_t*)h, (const uint16_t*)gate_weight, expert_bias, down_bias,
-                     dense_weights, bias_out, d, num_experts, num_shared, top_k, topk_idx, topk_weight);
+  LFS_REQUIRE(T < (1ll << 31), "moe_route: too many tokens");
+  if (T <= kRouteSmallT)
+    hipLaunchKernelGGL(moe_route_token_kernel, dim3((unsigned)T), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t*)h, (const uint16_t*)gate_weight, expert_bias, down_bias, dense_weights,
+                       bias_out, d, num_experts, num_shared, top_k, topk_idx, topk_weight);
+  else
+    hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)((T + kRouteTokens - 1) / kRouteTokens)),
+                       dim3(64 * kRouteTokens), 0, (hipStream_t)stream, (const uint16_t*)h,
+                       (const uint16_t*)gate_weight, expert_bias, down_bias, dense_weights, bias_out, T, d,
+                       num_experts, num_shared, top_k, topk_idx, topk_weight);
   return check_launch("moe_route");
 }
 

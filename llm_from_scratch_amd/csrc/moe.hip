@@ -3,9 +3,9 @@
 //
 //   moe_align        (token, pick) entries -> rows grouped by expert, each
 //                    expert's segment padded to 128-row tiles, plus the
-//                    tile -> expert map and each entry's row; one workgroup,
-//                    stable (entries of an expert keep their flat order), no
-//                    host synchronisation (model/architecture/moe.py:288-341
+//                    tile -> expert map and each entry's row; three
+//                    launches over 1024-entry chunks, stable (entries of an
+//                    expert keep their flat order), no host synchronisation (model/architecture/moe.py:288-341
 //                    does argsort + bincount + .tolist()).
 //   moe_combine      y[t] = bf16( sum_j out[row(t, j)] + sum_j w_tj * b2[e_tj] )
 //                    over the token's picks and shared experts, fp32, in pick
@@ -47,29 +47,73 @@ __device__ __forceinline__ void entry(const int64_t* idx, const float* w, int64_
   }
 }
 
-__global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
+// moe_align in three launches over chunks of 1024 entries (workspace:
+// hist[chunks][E'] counts then bases, cnt[E'], off[E' + 1]):
+//   rank     per chunk: each entry's rank among the chunk's entries of its
+//            expert (wave ballots + a prefix over the waves) -> entry_row
+//            (temporarily), the chunk's count per expert -> hist
+//   offsets  one workgroup: per expert an exclusive scan of hist over the
+//            chunks, the padded segment offsets, tile_expert, padding rows
+//   place    per chunk: row = off[e] + hist[chunk][e] + rank -> row_token,
+//            row_weight, entry_row
+// The order is stable: entry i precedes entry i' > i of the same expert.
+__global__ __launch_bounds__(kAlignThreads) void moe_align_rank_kernel(
     const int64_t* __restrict__ topk_idx, const float* __restrict__ topk_w, int T, int top_k, int E, int S,
-    int32_t* __restrict__ row_token, float* __restrict__ row_weight, int32_t* __restrict__ tile_expert,
-    int num_tiles, int32_t* __restrict__ entry_row) {
+    int32_t* __restrict__ entry_row, int32_t* __restrict__ hist) {
   constexpr int NW = kAlignThreads / 64;
-  __shared__ int cnt[kAlignMaxExperts];
-  __shared__ int off[kAlignMaxExperts + 1];
-  __shared__ int run[kAlignMaxExperts];
   __shared__ int wcnt[NW][kAlignMaxExperts];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kk = top_k + S, EE = E + S;
   const int64_t n = (int64_t)T * kk;
-  if (tid < kAlignMaxExperts) { cnt[tid] = 0; run[tid] = 0; }
+  for (int x = tid; x < NW * kAlignMaxExperts; x += kAlignThreads) (&wcnt[0][0])[x] = 0;
   __syncthreads();
-  // ---- counts per expert
-  for (int64_t i = tid; i < n; i += kAlignThreads) {
-    int t, e;
-    float wt;
-    entry(topk_idx, topk_w, i, kk, top_k, E, t, e, wt);
-    if (e >= 0) atomicAdd(&cnt[e], 1);
+  const int64_t i = (int64_t)blockIdx.x * kAlignThreads + tid;
+  int t = 0, e = -1;
+  float wt = 0.f;
+  if (i < n) entry(topk_idx, topk_w, i, kk, top_k, E, t, e, wt);
+  // rank inside the wave: one ballot per distinct expert present
+  int rank = 0;
+  uint64_t todo = __ballot(e >= 0);
+  while (todo != 0) {
+    const int leader = __builtin_ctzll(todo);
+    const int el = __shfl(e, leader, 64);
+    const uint64_t same = __ballot(e == el);
+    if (e == el) rank = __builtin_popcountll(same & ((1ull << lane) - 1ull));
+    if (lane == leader) wcnt[wave][el] = __builtin_popcountll(same);
+    todo &= ~same;
   }
   __syncthreads();
-  // ---- padded segment offsets, tile -> expert map
+  if (tid < EE) {  // exclusive prefix over the waves; the chunk's total
+    int acc = 0;
+    for (int w = 0; w < NW; ++w) {
+      const int c = wcnt[w][tid];
+      wcnt[w][tid] = acc;
+      acc += c;
+    }
+    hist[(int64_t)blockIdx.x * EE + tid] = acc;
+  }
+  __syncthreads();
+  if (i < n) entry_row[i] = e >= 0 ? wcnt[wave][e] + rank : -1;
+}
+
+__global__ __launch_bounds__(kAlignThreads) void moe_align_offsets_kernel(
+    int chunks, int E, int S, int32_t* __restrict__ hist, int32_t* __restrict__ cnt_out,
+    int32_t* __restrict__ off_out, int32_t* __restrict__ row_token, float* __restrict__ row_weight,
+    int32_t* __restrict__ tile_expert, int num_tiles) {
+  __shared__ int cnt[kAlignMaxExperts];
+  __shared__ int off[kAlignMaxExperts + 1];
+  const int tid = threadIdx.x, EE = E + S;
+  if (tid < EE) {
+    int run = 0;
+    for (int c = 0; c < chunks; ++c) {
+      const int v = hist[(int64_t)c * EE + tid];
+      hist[(int64_t)c * EE + tid] = run;
+      run += v;
+    }
+    cnt[tid] = run;
+    cnt_out[tid] = run;
+  }
+  __syncthreads();
   if (tid == 0) {
     int o = 0;
     for (int e = 0; e < EE; ++e) {
@@ -79,72 +123,48 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
     off[EE] = o;
   }
   __syncthreads();
-  // expert whose padded segment holds row r (-1 past the last segment)
-  auto seg_of = [&](int r) -> int {
-    if (r >= off[EE]) return -1;
-    int lo = 0, hi = EE;  // off[lo] <= r < off[hi]
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (off[mid] <= r) lo = mid;
-      else hi = mid;
-    }
-    return lo;
-  };
-  for (int tile = tid; tile < num_tiles; tile += kAlignThreads) tile_expert[tile] = seg_of(tile * kTile);
-  // ---- stable placement, 1024 entries per round: the rank of an entry
-  // among the entries of its expert = entries of that expert in earlier
-  // rounds + in earlier waves of this round + in lower lanes of its wave
-  const int64_t rounds = (n + kAlignThreads - 1) / kAlignThreads;
-  for (int64_t rd = 0; rd < rounds; ++rd) {
-    for (int x = tid; x < NW * kAlignMaxExperts; x += kAlignThreads) (&wcnt[0][0])[x] = 0;
-    __syncthreads();
-    const int64_t i = rd * kAlignThreads + tid;
-    int t = 0, e = -1;
-    float wt = 0.f;
-    if (i < n) entry(topk_idx, topk_w, i, kk, top_k, E, t, e, wt);
-    // rank inside the wave: one ballot per distinct expert present
-    int rank = 0;
-    uint64_t todo = __ballot(e >= 0);
-    while (todo != 0) {
-      const int leader = __builtin_ctzll(todo);
-      const int el = __shfl(e, leader, 64);
-      const uint64_t same = __ballot(e == el);
-      if (e == el) rank = __builtin_popcountll(same & ((1ull << lane) - 1ull));
-      if (lane == leader) wcnt[wave][el] = __builtin_popcountll(same);
-      todo &= ~same;
-    }
-    __syncthreads();
-    // per expert: exclusive prefix over the waves, then advance the run
-    if (tid < EE) {
-      int acc = run[tid];
-      for (int w = 0; w < NW; ++w) {
-        const int c = wcnt[w][tid];
-        wcnt[w][tid] = acc;
-        acc += c;
+  if (tid <= EE) off_out[tid] = off[tid];
+  for (int tile = tid; tile < num_tiles; tile += kAlignThreads) {
+    const int r = tile * kTile;
+    int ex = -1;
+    if (r < off[EE]) {  // off[lo] <= r < off[hi]
+      int lo = 0, hi = EE;
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (off[mid] <= r) lo = mid;
+        else hi = mid;
       }
-      run[tid] = acc;
+      ex = lo;
     }
-    __syncthreads();
-    if (i < n) {
-      int row = -1;
-      if (e >= 0) {
-        row = off[e] + wcnt[wave][e] + rank;
-        row_token[row] = t;
-        row_weight[row] = wt;
-      }
-      entry_row[i] = row;
-    }
-    __syncthreads();
+    tile_expert[tile] = ex;
   }
-  // ---- padding rows (segment tails and the rows past the last segment)
-  const int rows = num_tiles * kTile;
-  for (int r = tid; r < rows; r += kAlignThreads) {
-    const int ex = seg_of(r);
-    if (ex < 0 || r - off[ex] >= cnt[ex]) {
+  // padding: each segment's tail, then the rows past the last segment
+  for (int e = 0; e <= EE; ++e) {
+    const int b = e < EE ? off[e] + cnt[e] : off[EE];
+    const int end = e < EE ? off[e + 1] : num_tiles * kTile;
+    for (int r = b + tid; r < end; r += kAlignThreads) {
       row_token[r] = -1;
       row_weight[r] = 0.f;
     }
   }
+}
+
+__global__ __launch_bounds__(kAlignThreads) void moe_align_place_kernel(
+    const int64_t* __restrict__ topk_idx, const float* __restrict__ topk_w, int T, int top_k, int E, int S,
+    const int32_t* __restrict__ hist, const int32_t* __restrict__ off, int32_t* __restrict__ row_token,
+    float* __restrict__ row_weight, int32_t* __restrict__ entry_row) {
+  const int kk = top_k + S, EE = E + S;
+  const int64_t n = (int64_t)T * kk;
+  const int64_t i = (int64_t)blockIdx.x * kAlignThreads + threadIdx.x;
+  if (i >= n) return;
+  int t, e;
+  float wt;
+  entry(topk_idx, topk_w, i, kk, top_k, E, t, e, wt);
+  if (e < 0) return;  // entry_row already -1
+  const int row = off[e] + hist[(int64_t)blockIdx.x * EE + e] + entry_row[i];
+  row_token[row] = t;
+  row_weight[row] = wt;
+  entry_row[i] = row;
 }
 
 // One workgroup per token, 8 consecutive columns per thread and pass.
@@ -322,9 +342,18 @@ extern "C" int64_t lfs_moe_align_tiles(int64_t T, int32_t top_k, int32_t num_exp
   return (n + (int64_t)(num_experts + num_shared) * (kTile - 1) + kTile - 1) / kTile;
 }
 
+extern "C" int64_t lfs_moe_align_workspace_bytes(int64_t T, int32_t top_k, int32_t num_experts,
+                                                 int32_t num_shared) {
+  if (T < 0 || top_k <= 0 || num_experts <= 0 || num_shared < 0) return 0;
+  const int64_t EE = num_experts + num_shared;
+  const int64_t chunks = (T * (top_k + num_shared) + kAlignThreads - 1) / kAlignThreads;
+  return 4 * (chunks * EE + 2 * EE + 1);
+}
+
 extern "C" int lfs_moe_align(const int64_t* topk_idx, const float* topk_weight, int64_t T, int32_t top_k,
                              int32_t num_experts, int32_t num_shared, int32_t* row_token, float* row_weight,
-                             int32_t* tile_expert, int64_t num_tiles, int32_t* entry_row, void* stream) {
+                             int32_t* tile_expert, int64_t num_tiles, int32_t* entry_row, void* workspace,
+                             int64_t workspace_bytes, void* stream) {
   LFS_REQUIRE(T >= 0 && top_k >= 1 && num_experts >= 1 && num_shared >= 0, "moe_align: bad shape");
   LFS_REQUIRE(num_experts + num_shared <= kAlignMaxExperts && top_k <= num_experts,
               "moe_align: at most %d experts, top_k <= num_experts", kAlignMaxExperts);
@@ -334,11 +363,27 @@ extern "C" int lfs_moe_align(const int64_t* topk_idx, const float* topk_weight, 
   LFS_REQUIRE(num_tiles * kTile < (1ll << 31) && T * (top_k + num_shared) < (1ll << 31),
               "moe_align: too many rows");
   if (num_tiles == 0) return 0;
-  LFS_REQUIRE(row_token && row_weight && tile_expert && (T == 0 || (topk_idx && topk_weight && entry_row)),
-              "moe_align: null pointer");
-  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, (hipStream_t)stream, topk_idx,
-                     topk_weight, (int)T, top_k, num_experts, num_shared, row_token, row_weight, tile_expert,
-                     (int)num_tiles, entry_row);
+  LFS_REQUIRE(row_token && row_weight && tile_expert, "moe_align: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  const int EE = num_experts + num_shared;
+  // (T == 0: no chunks; every tile unused, every row padding)
+  const int64_t wneed = lfs_moe_align_workspace_bytes(T, top_k, num_experts, num_shared);
+  LFS_REQUIRE(workspace != nullptr && workspace_bytes >= wneed,
+              "moe_align: needs a workspace of %lld bytes", (long long)wneed);
+  LFS_REQUIRE(T == 0 || (topk_idx && topk_weight && entry_row), "moe_align: null pointer");
+  const int chunks = (int)((T * (top_k + num_shared) + kAlignThreads - 1) / kAlignThreads);
+  int32_t* hist = (int32_t*)workspace;
+  int32_t* cnt = hist + (int64_t)chunks * EE;
+  int32_t* off = cnt + EE;
+  if (chunks > 0)
+    hipLaunchKernelGGL(moe_align_rank_kernel, dim3((unsigned)chunks), dim3(kAlignThreads), 0, st, topk_idx,
+                       topk_weight, (int)T, top_k, num_experts, num_shared, entry_row, hist);
+  hipLaunchKernelGGL(moe_align_offsets_kernel, dim3(1), dim3(kAlignThreads), 0, st, chunks, num_experts,
+                     num_shared, hist, cnt, off, row_token, row_weight, tile_expert, (int)num_tiles);
+  if (chunks > 0)
+    hipLaunchKernelGGL(moe_align_place_kernel, dim3((unsigned)chunks), dim3(kAlignThreads), 0, st, topk_idx,
+                       topk_weight, (int)T, top_k, num_experts, num_shared, (const int32_t*)hist,
+                       (const int32_t*)off, row_token, row_weight, entry_row);
   return check_launch("moe_align");
 }
 

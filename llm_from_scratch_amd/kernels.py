@@ -573,9 +573,12 @@ def moe_align(topk_idx: torch.Tensor, topk_weight: torch.Tensor, num_experts: in
     row_weight = torch.empty(tiles * 128, dtype=torch.float32, device=dev)
     tile_expert = torch.empty(tiles, dtype=torch.int32, device=dev)
     entry_row = torch.empty(T, k + num_shared, dtype=torch.int32, device=dev)
-    rc = _lib.load().lfs_moe_align(_ptr(topk_idx), _ptr(topk_weight), T, k, num_experts, num_shared,
-                                   _ptr(row_token), _ptr(row_weight), _ptr(tile_expert), tiles, _ptr(entry_row),
-                                   _stream(topk_idx))
+    L = _lib.load()
+    ws = torch.empty(int(L.lfs_moe_align_workspace_bytes(T, k, num_experts, num_shared)) // 4, dtype=torch.int32,
+                     device=dev)
+    rc = L.lfs_moe_align(_ptr(topk_idx), _ptr(topk_weight), T, k, num_experts, num_shared, _ptr(row_token),
+                         _ptr(row_weight), _ptr(tile_expert), tiles, _ptr(entry_row), _ptr(ws), ws.numel() * 4,
+                         _stream(topk_idx))
     _lib.check(rc, "moe_align")
     return MoeRows(row_token, row_weight, tile_expert, entry_row)
 

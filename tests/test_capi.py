@@ -71,10 +71,12 @@ def test_argument_errors_are_reported_without_launch(lib):
     rc = lib.lfs_swiglu_quant(None, None, None, None, 4, 9, 500, None)
     assert rc == -1 and b"d_ff" in lib.lfs_last_error()
     # MoE dispatch: capacity too small, too many experts, fp32 output with a bias, bad K
-    rc = lib.lfs_moe_align(16, 16, 100, 2, 8, 1, 16, 16, 16, 3, 16, None)
+    rc = lib.lfs_moe_align(16, 16, 100, 2, 8, 1, 16, 16, 16, 3, 16, 16, 1 << 20, None)
     assert rc == -1 and b"tiles needed" in lib.lfs_last_error()
-    rc = lib.lfs_moe_align(16, 16, 100, 2, 64, 1, 16, 16, 16, 1000, 16, None)
+    rc = lib.lfs_moe_align(16, 16, 100, 2, 64, 1, 16, 16, 16, 1000, 16, 16, 1 << 20, None)
     assert rc == -1 and b"at most 64 experts" in lib.lfs_last_error()
+    rc = lib.lfs_moe_align(16, 16, 100, 2, 8, 1, 16, 16, 16, 20, 16, 16, 8, None)
+    assert rc == -1 and b"workspace" in lib.lfs_last_error()
     rc = lib.lfs_fp8_grouped_gemm(16, 16, 8, None, 16, 1, 16, 16, 0, 256, 0, 2, 16, 0, None, 16, 128, 256, None)
     assert rc == -1 and b"no bias" in lib.lfs_last_error()
     rc = lib.lfs_fp8_grouped_gemm(16, 16, 8, None, 16, 1, 16, 16, 0, 256, 0, 2, None, 0, 16, None, 128, 200, None)
@@ -89,6 +91,8 @@ def test_moe_capacity_helpers(lib):
     # 100 tokens x (2 picks + 1 shared) over 9 experts: (300 + 9*127 + 127) // 128
     assert lib.lfs_moe_align_tiles(100, 2, 8, 1) == (300 + 9 * 127 + 127) // 128
     assert lib.lfs_moe_align_tiles(0, 2, 8, 1) == 0
+    # 3000 entries -> 3 chunks of 1024, 9 experts
+    assert lib.lfs_moe_align_workspace_bytes(1000, 2, 8, 1) == 4 * (3 * 9 + 2 * 9 + 1)
     assert lib.lfs_scatter_add_weighted_workspace_bytes(10, 5) == 4 * (3 * 5 + 1 + 10)
 
 
