@@ -83,7 +83,7 @@
 extern "C" {
 #endif
 
-#define LFS_ABI_VERSION 5
+#define LFS_ABI_VERSION 6
 
 /* argument errors (negative); launch errors are positive hipError_t values */
 #define LFS_EINVAL (-1)
@@ -354,13 +354,15 @@ int lfs_fp8_grouped_gemm(const void* a, const float* a_s, int64_t a_rows, const 
 /*
  * moe_combine, per token t (entries i = t*(top_k+S) + j as in moe_align):
  *   y[t] = bf16( sum_j out[entry_row[i]] + sum_j w_j * down_bias[e_j] )
- * summed in fp32 in j order, entries with entry_row < 0 skipped; out fp32
- * [rows, ld] (the down projection's rows, routing weights already applied),
- * down_bias fp32 [E + S, d] or NULL; y bf16 [T, d].  d % 8 == 0.
+ * summed in fp32 in j order, entries with entry_row < 0 skipped; out
+ * [rows, ld] bf16 (out_is_f32 = 0) or fp32 (the down projection's rows,
+ * routing weights already applied), down_bias fp32 [E + S, d] or NULL;
+ * y bf16 [T, d].  d % 8 == 0, ld % 8 == 0.
  */
-int lfs_moe_combine(const float* out, int64_t ld, const int32_t* entry_row, const int64_t* topk_idx,
-                    const float* topk_weight, int64_t T, int32_t top_k, int32_t num_experts,
-                    int32_t num_shared, const float* down_bias, int32_t d, void* y, void* stream);
+int lfs_moe_combine(const void* out, int32_t out_is_f32, int64_t ld, const int32_t* entry_row,
+                    const int64_t* topk_idx, const float* topk_weight, int64_t T, int32_t top_k,
+                    int32_t num_experts, int32_t num_shared, const float* down_bias, int32_t d, void* y,
+                    void* stream);
 
 /*
  * segment_reduce_weighted: y[t] = sum_{p : idx[p] == t} w[p] * x[p] for

@@ -11,7 +11,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "liblfs_kernels.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _c_i64, _c_i32, _c_p, _c_f = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p, ctypes.c_float
 
@@ -51,8 +51,8 @@ SIGNATURES = {
     "lfs_moe_align_workspace_bytes": (ctypes.c_int64, [_c_i64, _c_i32, _c_i32, _c_i32]),
     "lfs_fp8_grouped_gemm": (ctypes.c_int, [_c_p, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64,
                                             _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_p]),
-    "lfs_moe_combine": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_p,
-                                       _c_i32, _c_p, _c_p]),
+    "lfs_moe_combine": (ctypes.c_int, [_c_p, _c_i32, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_i32,
+                                       _c_p, _c_i32, _c_p, _c_p]),
     "lfs_segment_reduce_weighted": (ctypes.c_int, [_c_p, _c_i32, _c_i64, _c_p, _c_i32, _c_p, _c_i64, _c_i64,
                                                    _c_i32, _c_p, _c_p]),
     "lfs_scatter_add_weighted_workspace_bytes": (ctypes.c_int64, [_c_i64, _c_i64]),

@@ -10,7 +10,7 @@
 //   moe_combine      y[t] = bf16( sum_j out[row(t, j)] + sum_j w_tj * b2[e_tj] )
 //                    over the token's picks and shared experts, fp32, in pick
 //                    order (the weights are already inside out: they scale
-//                    the down GEMM's activation scales).
+//                    the down GEMM's activation scales); out bf16 or fp32.
 //   segment_reduce_weighted / scatter_add_weighted
 //                    y[t] = sum_{i : idx[i] = t} w_i * x_i in fp32, rounded to
 //                    x's dtype: the Triton kernels of
@@ -168,7 +168,8 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_place_kernel(
 }
 
 // One workgroup per token, 8 consecutive columns per thread and pass.
-__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ out, int64_t ld,
+template <typename OutT>
+__global__ __launch_bounds__(256) void moe_combine_kernel(const OutT* __restrict__ out, int64_t ld,
                                                           const int32_t* __restrict__ entry_row,
                                                           const int64_t* __restrict__ topk_idx,
                                                           const float* __restrict__ topk_w, int top_k, int E,
@@ -191,10 +192,16 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int j = 0; j < kk; ++j) {
       if (rows[j] < 0) continue;
-      const float4* p = reinterpret_cast<const float4*>(out + (int64_t)rows[j] * ld + c);
-      const float4 a = p[0], b = p[1];
-      acc[0] += a.x; acc[1] += a.y; acc[2] += a.z; acc[3] += a.w;
-      acc[4] += b.x; acc[5] += b.y; acc[6] += b.z; acc[7] += b.w;
+      float v[8];
+      if constexpr (sizeof(OutT) == 4) {
+        const float4* p = reinterpret_cast<const float4*>(out + (int64_t)rows[j] * ld + c);
+        const float4 a = p[0], b = p[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+      } else {
+        unpack8(*reinterpret_cast<const uint4*>(out + (int64_t)rows[j] * ld + c), v);
+      }
+#pragma unroll
+      for (int x = 0; x < 8; ++x) acc[x] += v[x];
     }
     if (b2 != nullptr) {
       for (int j = 0; j < kk; ++j) {
@@ -387,19 +394,26 @@ extern "C" int lfs_moe_align(const int64_t* topk_idx, const float* topk_weight, 
   return check_launch("moe_align");
 }
 
-extern "C" int lfs_moe_combine(const float* out, int64_t ld, const int32_t* entry_row, const int64_t* topk_idx,
-                               const float* topk_weight, int64_t T, int32_t top_k, int32_t num_experts,
-                               int32_t num_shared, const float* down_bias, int32_t d, void* y, void* stream) {
+extern "C" int lfs_moe_combine(const void* out, int32_t out_is_f32, int64_t ld, const int32_t* entry_row,
+                               const int64_t* topk_idx, const float* topk_weight, int64_t T, int32_t top_k,
+                               int32_t num_experts, int32_t num_shared, const float* down_bias, int32_t d, void* y,
+                               void* stream) {
   LFS_REQUIRE(T >= 0 && top_k >= 1 && num_experts >= 1 && num_shared >= 0 &&
                   top_k + num_shared <= kAlignMaxExperts,
               "moe_combine: bad shape");
-  LFS_REQUIRE(d > 0 && d % 8 == 0 && ld >= d && ld % 4 == 0, "moe_combine: d=%d must be a multiple of 8", d);
+  LFS_REQUIRE(d > 0 && d % 8 == 0 && ld >= d && ld % 8 == 0, "moe_combine: d=%d must be a multiple of 8", d);
   if (T == 0) return 0;
   LFS_REQUIRE(out && entry_row && topk_idx && topk_weight && y, "moe_combine: null pointer");
   LFS_REQUIRE((((uintptr_t)out) | ((uintptr_t)y)) % 16 == 0, "moe_combine: buffers must be 16-byte aligned");
   LFS_REQUIRE(T < (1ll << 31), "moe_combine: too many tokens");
-  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T), dim3(256), 0, (hipStream_t)stream, out, ld, entry_row,
-                     topk_idx, topk_weight, top_k, num_experts, num_shared, down_bias, d, (uint16_t*)y);
+  if (out_is_f32)
+    hipLaunchKernelGGL(moe_combine_kernel<float>, dim3((unsigned)T), dim3(256), 0, (hipStream_t)stream,
+                       (const float*)out, ld, entry_row, topk_idx, topk_weight, top_k, num_experts, num_shared,
+                       down_bias, d, (uint16_t*)y);
+  else
+    hipLaunchKernelGGL(moe_combine_kernel<uint16_t>, dim3((unsigned)T), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t*)out, ld, entry_row, topk_idx, topk_weight, top_k, num_experts, num_shared,
+                       down_bias, d, (uint16_t*)y);
   return check_launch("moe_combine");
 }
 

@@ -182,9 +182,10 @@ class MoE(nn.Module):
     each expert's gathered rows (the same stacked weights, viewed
     [E, 2F, d]), swiglu_quant folds each row's routing weight into its
     scales, a second grouped GEMM runs w2 (the K-stacked matrix viewed
-    [E, d, F]) into fp32 rows, and moe_combine sums each token's rows and
-    its weighted down biases, rounding once.  Both dispatches compute the
-    same sum up to fp32 summation order."""
+    [E, d, F]) into bf16 rows (each expert's weighted output rounded once,
+    as the reference rounds each expert's output), and moe_combine sums
+    each token's rows and its weighted down biases in fp32, rounding once
+    more.  The two dispatches agree to a bf16 rounding per expert."""
 
     GROUPED_MIN_TOKENS = 256
 
@@ -256,7 +257,8 @@ class MoE(nn.Module):
         h13 = kernels.fp8_grouped_gemm(hq, hs, rows.row_token, rows.tile_expert, w13, w13s, b13)
         P = rows.num_rows
         gq, gs = kernels.swiglu_quant(h13.view(P, 1, 2, F), rows.row_weight.view(P, 1))
-        out = kernels.fp8_grouped_gemm(gq, gs, None, rows.tile_expert, w2, w2s, out_dtype=torch.float32)
+        # bf16 expert rows (the reference also rounds each expert's output), fp32 sum
+        out = kernels.fp8_grouped_gemm(gq, gs, None, rows.tile_expert, w2, w2s)
         y = kernels.moe_combine(out, rows.entry_row, idx, wt, E, S, self.w2_bias)
         if trace is not None:
             trace.update(topk_idx=idx, topk_weight=wt, moe_rows=rows, h13_rows=h13, ffn_out=y)

@@ -642,10 +642,10 @@ def moe_combine(out: torch.Tensor, entry_row: torch.Tensor, topk_idx: torch.Tens
     """y[t] = bf16(sum_j out[entry_row[t, j]] + sum_j w_tj * down_bias[e_tj])
     over the token's picks then its shared experts, fp32 in that order: the
     scatter_add_ of MoE.moe_infer (model/architecture/moe.py:332-339) plus
-    the shared-expert add (:272-273).  out: fp32 [rows, d] (routing weights
-    already applied); down_bias fp32 [E + S, d] or None."""
+    the shared-expert add (:272-273).  out: bf16 or fp32 [rows, d] (routing
+    weights already applied); down_bias fp32 [E + S, d] or None."""
     _on_gpu(out, entry_row, topk_idx, topk_weight)
-    _dtype(out, torch.float32, "out")
+    assert out.dtype in (torch.bfloat16, torch.float32), "out must be bf16 or fp32"
     _dtype(entry_row, torch.int32, "entry_row")
     assert out.dim() == 2 and out.stride(1) == 1 and entry_row.is_contiguous()
     T, k = topk_idx.shape
@@ -656,8 +656,9 @@ def moe_combine(out: torch.Tensor, entry_row: torch.Tensor, topk_idx: torch.Tens
         _dtype(down_bias, torch.float32, "down_bias")
         assert down_bias.shape == (num_experts + num_shared, d) and down_bias.is_contiguous()
     y = torch.empty(T, d, dtype=torch.bfloat16, device=out.device)
-    rc = _lib.load().lfs_moe_combine(_ptr(out), out.stride(0), _ptr(entry_row), _ptr(topk_idx), _ptr(topk_weight),
-                                     T, k, num_experts, num_shared, _ptr(down_bias), d, _ptr(y), _stream(out))
+    rc = _lib.load().lfs_moe_combine(_ptr(out), int(out.dtype == torch.float32), out.stride(0), _ptr(entry_row),
+                                     _ptr(topk_idx), _ptr(topk_weight), T, k, num_experts, num_shared,
+                                     _ptr(down_bias), d, _ptr(y), _stream(out))
     _lib.check(rc, "moe_combine")
     return y
 

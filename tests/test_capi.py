@@ -81,7 +81,7 @@ def test_argument_errors_are_reported_without_launch(lib):
     assert rc == -1 and b"no bias" in lib.lfs_last_error()
     rc = lib.lfs_fp8_grouped_gemm(16, 16, 8, None, 16, 1, 16, 16, 0, 256, 0, 2, None, 0, 16, None, 128, 200, None)
     assert rc == -1 and b"multiple of 128" in lib.lfs_last_error()
-    rc = lib.lfs_moe_combine(16, 100, 16, 16, 16, 4, 2, 8, 1, None, 100, 16, None)
+    rc = lib.lfs_moe_combine(16, 1, 104, 16, 16, 16, 4, 2, 8, 1, None, 100, 16, None)
     assert rc == -1 and b"multiple of 8" in lib.lfs_last_error()
     rc = lib.lfs_scatter_add_weighted(16, 0, 8, 16, 1, 16, 10, 5, 8, 16, None, 0, None)
     assert rc == -1 and b"workspace" in lib.lfs_last_error()

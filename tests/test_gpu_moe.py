@@ -113,16 +113,17 @@ def test_grouped_gemm_k_stacked_view():
         assert np.all(np.abs(got - ref) <= 1e-4 * (np.abs(ref).max(1, keepdims=True) + 1e-30)), f"tile {i}"
 
 
-def test_moe_combine():
+@pytest.mark.parametrize("rows_dtype", [torch.float32, torch.bfloat16])
+def test_moe_combine(rows_dtype):
     rng = np.random.default_rng(7)
     T, E, k, S, d = 300, 8, 2, 1, 768
     idx, w = picks(rng, T, E, k, bad=3)
     rows = K.moe_align(dev(idx), dev(w), E, S)
     _, _, _, er = MO.moe_align(idx, w, E, S)
-    out = rng.standard_normal((rows.num_rows, d)).astype(np.float32)
+    out = dev(rng.standard_normal((rows.num_rows, d)).astype(np.float32)).to(rows_dtype)
     b2 = rng.standard_normal((E + S, d)).astype(np.float32)
-    y = K.moe_combine(dev(out), rows.entry_row, dev(idx), dev(w), E, S, dev(b2)).float().cpu().numpy()
-    ref = MO.moe_combine(out, er, idx, w, E, S, b2)
+    y = K.moe_combine(out, rows.entry_row, dev(idx), dev(w), E, S, dev(b2)).float().cpu().numpy()
+    ref = MO.moe_combine(out.double().cpu().numpy(), er, idx, w, E, S, b2)
     # one bf16 rounding of an fp32 sum vs of a float64 sum
     assert np.all(np.abs(y - ref) <= 2.0 ** -7 * np.abs(ref) + 1e-6)
 
