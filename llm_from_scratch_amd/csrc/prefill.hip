@@ -39,16 +39,17 @@ constexpr int KT = 32;          // keys per tile
 constexpr int QT = 16;          // query tokens per workgroup
 constexpr int VT_PITCH = 72;    // bytes per dim row of the transposed V tile (32 keys + pad)
 
-template <int D, int G>
+template <int D, int G, bool PAGED>
 __global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k, const int32_t* __restrict__ bt,
     int64_t bt_stride, int BS, int64_t num_slots, uint16_t* __restrict__ out, int Hkv, int qtiles,
     float scale_log2) {
-  constexpr int NDC = D / 32;    // 32-dim chunks (MFMA k steps of S)
-  constexpr int NDB = D / 16;    // 16-dim blocks of O^T
-  constexpr int VCH = KT * D / 8;                    // 16-byte V chunks per tile
-  constexpr int VPT = (VCH + 64 * G - 1) / (64 * G); // chunks per thread
+  constexpr int NDC = D / 32;                        // 32-dim chunks (MFMA k steps of S)
+  constexpr int NDB = D / 16;                        // 16-dim blocks of O^T
+  constexpr int CPK = D / 8;                         // 16-byte chunks of a key row
+  constexpr int VUN = KT / 2 * CPK;                  // (key pair, chunk) units of a V tile
+  constexpr int VPT = (VUN + 64 * G - 1) / (64 * G); // units per thread
   __shared__ __attribute__((aligned(16))) uint8_t vt[2][D * VT_PITCH];
 
   const int i = blockIdx.x / qtiles, tq0 = (blockIdx.x % qtiles) * QT;
@@ -61,21 +62,29 @@ __global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
   const int h = kh * G + wave, Hq = Hkv * G;
   const int c16 = lane & 15, g = lane >> 4;
   const int64_t row = (int64_t)Hkv * D;  // elements per token row of k / v
+  const int64_t hoff = (int64_t)kh * D;
 
-  // element offset of key t's row (head kh); t clamped into the context,
-  // invalid block-table entries read slot 0 (their keys are masked or the
-  // caller's tables are wrong -- never out of bounds)
-  auto key_off = [&](int t) -> int64_t {
-    t = min(t, lk - 1);
-    int64_t slot;
-    if (bt != nullptr) {
-      const int32_t blk = bt[(int64_t)i * bt_stride + min((int64_t)(t / BS), bt_stride - 1)];
-      slot = (int64_t)blk * BS + t % BS;
-      if (blk < 0 || slot >= num_slots) slot = 0;
+  // Key addresses per 16-key half of a tile.  Keys past the context read
+  // the row of key lk - 1 (their scores are masked, but their V rows still
+  // enter the P.V product with weight 0, so they must hold finite data:
+  // pool slots past a sequence's keys may hold anything).  Paged: BS % 16
+  // == 0, so a half (16-aligned) lies in one block and key x of it is the
+  // half's slot base + x; an invalid table entry reads slot 0.
+  // Contiguous: key t is row k0 + min(t, lk - 1) of k / v.
+  auto half_slot = [&](int tstart) -> int64_t {  // paged only
+    const int tc = min(tstart, lk - 1);
+    const int32_t blk = bt[(int64_t)i * bt_stride + min((int64_t)(tc / BS), bt_stride - 1)];
+    if (blk < 0 || (int64_t)blk * BS >= num_slots) return 0;
+    return (int64_t)blk * BS + tc % BS;
+  };
+  auto key_elem = [&](const int64_t (&hs)[2], int t0, int kx) -> int64_t {  // key t0 + kx, kx < 32
+    const int hf = kx >> 4;
+    if constexpr (PAGED) {
+      // half base = slot of key min(t0 + 16 hf, lk - 1)
+      return (hs[hf] + max(0, min(kx & 15, lk - 1 - (t0 + 16 * hf)))) * row + hoff;
     } else {
-      slot = (int64_t)k0 + t;
+      return ((int64_t)k0 + min(t0 + kx, lk - 1)) * row + hoff;
     }
-    return slot * row + (int64_t)kh * D;
   };
 
   // Q^T (B operand): lane l supplies query tq0 + l % 16, dims 32c + 8g .. +7
@@ -94,33 +103,63 @@ __global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
   // keys up to the last query of the tile
   const int nkt = (min(lk, off + tq0 + QT) + KT - 1) / KT;
 
-  auto load_k = [&](uint4 (&ka)[2][NDC], int t0) {
+  auto halves = [&](int64_t (&hs)[2], int t0) {
+    if constexpr (PAGED) {
+      hs[0] = half_slot(t0);
+      hs[1] = half_slot(t0 + 16);
+    } else {
+      hs[0] = hs[1] = 0;
+    }
+  };
+  auto load_k = [&](uint4 (&ka)[2][NDC], const int64_t (&hs)[2], int t0) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      const int64_t o = key_off(t0 + 16 * kb + c16);
+      const int64_t o = key_elem(hs, t0, 16 * kb + c16);
 #pragma unroll
       for (int c = 0; c < NDC; ++c) ka[kb][c] = *reinterpret_cast<const uint4*>(k + o + c * 32 + g * 8);
     }
   };
-  // V chunk u of a tile: key u / (D / 8), dims (u % (D / 8)) * 8 .. +7
-  auto load_v = [&](uint4 (&vr)[VPT], int t0) {
+  // V unit u of a tile: key pair kp (keys 2kp, 2kp + 1), 16-byte chunk cc of
+  // both rows; eight consecutive units cover the chunks of one pair (whole
+  // rows per eight lanes), the pair index is swizzled by the chunk's high
+  // half so that a wave's 32-bit LDS writes below hit distinct banks
+  auto vunit = [&](int u, int& kp, int& cc) {
+    cc = (u & 7) + 8 * ((u >> 3) / (KT / 2) % (CPK / 8));
+    const int kpl = (u >> 3) % (KT / 2);
+    kp = (kpl + 8 * ((u & 7) >> 2)) % (KT / 2);
+  };
+  auto load_v = [&](uint4 (&vr)[VPT][2], const int64_t (&hs)[2], int t0) {
 #pragma unroll
     for (int e = 0; e < VPT; ++e) {
       const int u = threadIdx.x + 64 * G * e;
-      vr[e] = make_uint4(0, 0, 0, 0);
-      if (u < VCH) vr[e] = *reinterpret_cast<const uint4*>(v + key_off(t0 + u / (D / 8)) + (u % (D / 8)) * 8);
+      vr[e][0] = vr[e][1] = make_uint4(0, 0, 0, 0);
+      if (u < VUN) {
+        int kp, cc;
+        vunit(u, kp, cc);
+        vr[e][0] = *reinterpret_cast<const uint4*>(v + key_elem(hs, t0, 2 * kp) + cc * 8);
+        vr[e][1] = *reinterpret_cast<const uint4*>(v + key_elem(hs, t0, 2 * kp + 1) + cc * 8);
+      }
     }
   };
-  auto store_vt = [&](const uint4 (&vr)[VPT], int buf) {
+  // transposed store: dim d of keys (2kp, 2kp + 1) as one 32-bit word at
+  // vt[d][2kp]
+  auto store_vt = [&](const uint4 (&vr)[VPT][2], int buf) {
 #pragma unroll
     for (int e = 0; e < VPT; ++e) {
       const int u = threadIdx.x + 64 * G * e;
-      if (u < VCH) {
-        const int key = u / (D / 8), d0 = (u % (D / 8)) * 8;
-        const uint16_t* hv = reinterpret_cast<const uint16_t*>(&vr[e]);
+      if (u < VUN) {
+        int kp, cc;
+        vunit(u, kp, cc);
+        const uint32_t* a = reinterpret_cast<const uint32_t*>(&vr[e][0]);
+        const uint32_t* b = reinterpret_cast<const uint32_t*>(&vr[e][1]);
 #pragma unroll
-        for (int x = 0; x < 8; ++x)
-          *reinterpret_cast<uint16_t*>(&vt[buf][(d0 + x) * VT_PITCH + key * 2]) = hv[x];
+        for (int x = 0; x < 4; ++x) {
+          // dims 8cc + 2x (low halves) and 8cc + 2x + 1 (high halves)
+          const uint32_t lo = (a[x] & 0xFFFFu) | (b[x] << 16);
+          const uint32_t hi = (a[x] >> 16) | (b[x] & 0xFFFF0000u);
+          *reinterpret_cast<uint32_t*>(&vt[buf][(8 * cc + 2 * x) * VT_PITCH + kp * 4]) = lo;
+          *reinterpret_cast<uint32_t*>(&vt[buf][(8 * cc + 2 * x + 1) * VT_PITCH + kp * 4]) = hi;
+        }
       }
     }
   };
@@ -130,9 +169,11 @@ __global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
   for (int db = 0; db < NDB; ++db) o[db] = v4f{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
 
-  uint4 ka[2][NDC], vr[VPT];
-  load_k(ka, 0);
-  load_v(vr, 0);
+  uint4 ka[2][NDC], vr[VPT][2];
+  int64_t hs[2];
+  halves(hs, 0);
+  load_k(ka, hs, 0);
+  load_v(vr, hs, 0);
   for (int j = 0; j < nkt; ++j) {
     const int t0 = j * KT;
     const int buf = j & 1;
@@ -146,11 +187,14 @@ __global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
 #pragma unroll
       for (int c = 0; c < NDC; ++c) kc[kb][c] = ka[kb][c];
     if (j + 1 < nkt) {
-      load_k(ka, t0 + KT);
-      load_v(vr, t0 + KT);
+      halves(hs, t0 + KT);
+      load_k(ka, hs, t0 + KT);
+      load_v(vr, hs, t0 + KT);
     }
 
-    // ---- S^T for the two 16-key halves
+    // ---- S^T for the two 16-key halves; the causal mask only where the
+    // tile reaches past the tile's first query position
+    const bool need_mask = t0 + KT - 1 > off + tq0;
     float s[2][4];
     float tmax = -INFINITY;
 #pragma unroll
@@ -161,22 +205,23 @@ __global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
         sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, kc[kb][c]), qb[c], sc, 0, 0, 0);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int kp = t0 + 16 * kb + 4 * g + r;
-        s[kb][r] = kp <= qp ? sc[r] * scale_log2 : -INFINITY;
+        s[kb][r] = sc[r] * scale_log2;
+        if (need_mask && t0 + 16 * kb + 4 * g + r > qp) s[kb][r] = -INFINITY;
         tmax = fmaxf(tmax, s[kb][r]);
       }
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
     const float m_new = fmaxf(m_run, tmax);  // finite: key 0 is never masked
-    const float alpha = exp2f(m_run - m_new);
+    // exp2 on the hardware instruction (arguments <= 0; results below 2^-126 flush to 0)
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
     float psum = 0.f;
     float p[2][4];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        p[kb][r] = exp2f(s[kb][r] - m_new);
+        p[kb][r] = __builtin_amdgcn_exp2f(s[kb][r] - m_new);
         psum += p[kb][r];
       }
     psum += __shfl_xor(psum, 16, 64);
@@ -219,14 +264,14 @@ __global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
   }
 }
 
-template <int D>
+template <int D, bool PAGED>
 bool launch_prefill(int G, dim3 grid, hipStream_t st, const uint16_t* q, const uint16_t* k, const uint16_t* v,
                     const int32_t* cu_q, const int32_t* cu_k, const int32_t* bt, int64_t bts, int BS,
                     int64_t num_slots, uint16_t* out, int Hkv, int qtiles, float sl2) {
-#define LFS_PG(GG)                                                                                         \
-  case GG:                                                                                                 \
-    hipLaunchKernelGGL((prefill_attention_kernel<D, GG>), grid, dim3(64 * GG), 0, st, q, k, v, cu_q, cu_k, \
-                       bt, bts, BS, num_slots, out, Hkv, qtiles, sl2);                                     \
+#define LFS_PG(GG)                                                                                        \
+  case GG:                                                                                                \
+    hipLaunchKernelGGL((prefill_attention_kernel<D, GG, PAGED>), grid, dim3(64 * GG), 0, st, q, k, v, cu_q, \
+                       cu_k, bt, bts, BS, num_slots, out, Hkv, qtiles, sl2);                              \
     return true;
   switch (G) {
     LFS_PG(1) LFS_PG(2) LFS_PG(3) LFS_PG(4) LFS_PG(5) LFS_PG(6) LFS_PG(7) LFS_PG(8)
@@ -255,7 +300,8 @@ extern "C" int lfs_prefill_attention(const void* q, const void* k, const void* v
   LFS_REQUIRE(((((uintptr_t)q) | ((uintptr_t)k) | ((uintptr_t)v) | ((uintptr_t)out)) & 15u) == 0,
               "prefill_attention: q, k, v and out must be 16-byte aligned");
   if (block_tables != nullptr) {
-    LFS_REQUIRE(block_size > 0 && num_slots > 0 && bt_stride > 0, "prefill_attention: bad paged KV geometry");
+    LFS_REQUIRE(block_size > 0 && block_size % 16 == 0 && num_slots >= block_size && bt_stride > 0,
+                "prefill_attention: bad paged KV geometry (block_size must be a multiple of 16)");
   }
   const int64_t qtiles = ((int64_t)max_seqlen_q + QT - 1) / QT;
   LFS_REQUIRE(B * qtiles < (1ll << 31) && Hkv < 65536, "prefill_attention: grid too large");
@@ -263,13 +309,19 @@ extern "C" int lfs_prefill_attention(const void* q, const void* k, const void* v
   const float sl2 = scale * 1.4426950408889634f;
   hipStream_t st = (hipStream_t)stream;
   const int G = Hq / Hkv;
-  const bool ok = D == 64
-      ? launch_prefill<64>(G, grid, st, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, cu_seqlens_q,
-                           cu_seqlens_k, block_tables, bt_stride, block_size, num_slots, (uint16_t*)out, Hkv,
-                           (int)qtiles, sl2)
-      : launch_prefill<128>(G, grid, st, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
-                            cu_seqlens_q, cu_seqlens_k, block_tables, bt_stride, block_size, num_slots,
-                            (uint16_t*)out, Hkv, (int)qtiles, sl2);
+  const uint16_t *qq = (const uint16_t*)q, *kk = (const uint16_t*)k, *vv = (const uint16_t*)v;
+  uint16_t* oo = (uint16_t*)out;
+  bool ok;
+  if (block_tables != nullptr)
+    ok = D == 64 ? launch_prefill<64, true>(G, grid, st, qq, kk, vv, cu_seqlens_q, cu_seqlens_k, block_tables,
+                                            bt_stride, block_size, num_slots, oo, Hkv, (int)qtiles, sl2)
+                 : launch_prefill<128, true>(G, grid, st, qq, kk, vv, cu_seqlens_q, cu_seqlens_k, block_tables,
+                                             bt_stride, block_size, num_slots, oo, Hkv, (int)qtiles, sl2);
+  else
+    ok = D == 64 ? launch_prefill<64, false>(G, grid, st, qq, kk, vv, cu_seqlens_q, cu_seqlens_k, nullptr, 0, 0,
+                                             num_slots, oo, Hkv, (int)qtiles, sl2)
+                 : launch_prefill<128, false>(G, grid, st, qq, kk, vv, cu_seqlens_q, cu_seqlens_k, nullptr, 0, 0,
+                                              num_slots, oo, Hkv, (int)qtiles, sl2);
   LFS_REQUIRE(ok, "prefill_attention: unsupported group size %d", G);
   return check_launch("prefill_attention");
 }

@@ -5,7 +5,8 @@ bf16 inputs (P is rounded to bf16 for the P.V MFMA, accumulation is fp32).
 Cases: D 64 and 128, GQA group sizes 1-8, sequence lengths across the
 16-query and 32-key tile boundaries (1, 15, 16, 17, 31, 33, ...), contiguous
 keys, paged keys with cached prefixes (lq < lk) at block sizes 16 and 256,
-and block tables with -1 padding past each sequence.
+block tables with -1 padding past each sequence, and a pool whose slots past
+every context hold NaN.
 """
 import numpy as np
 import pytest
@@ -77,6 +78,41 @@ def test_prefill_paged_cached_prefix(BS, Hq, Hkv, D):
     ref = P.prefill_attention(f64(q), f64(kc), f64(vc), cu_q.cpu().numpy(), cu_k.cpu().numpy(), 0.125,
                               block_tables=bt)
     assert_close(f64(o), ref, f"paged BS={BS} Hq={Hq} Hkv={Hkv} D={D}")
+
+
+@pytest.mark.parametrize("BS", [16, 64])
+def test_prefill_paged_pool_poisoned_past_context(BS):
+    """Pool slots that hold no key of any sequence (tails of the last
+    blocks, unused blocks) are NaN: keys past a context are masked, and
+    their V rows must not reach the output either (0 * NaN)."""
+    rng = np.random.default_rng(BS + 7)
+    Hq, Hkv, D = 12, 4, 64
+    lens_k = [37, 20, 5, 70]
+    lens_q = [37, 3, 5, 10]
+    B = len(lens_k)
+    nblk = [-(-L // BS) for L in lens_k]
+    NB = sum(nblk) + 3
+    perm = rng.permutation(NB)
+    bt = np.full((B, max(nblk) + 1), -1, np.int32)
+    kc = torch.full((NB, BS, Hkv, D), float("nan"), dtype=torch.bfloat16, device=DEV)
+    vc = torch.full((NB, BS, Hkv, D), float("nan"), dtype=torch.bfloat16, device=DEV)
+    pos = 0
+    for i, n in enumerate(nblk):
+        bt[i, :n] = perm[pos:pos + n]
+        pos += n
+        for t in range(lens_k[i]):  # only the context's own slots hold data
+            blk, o = bt[i, t // BS], t % BS
+            kc[blk, o] = bf16(rng, Hkv, D)
+            vc[blk, o] = bf16(rng, Hkv, D)
+    cu_q = torch.tensor(np.concatenate([[0], np.cumsum(lens_q)]), dtype=torch.int32, device=DEV)
+    cu_k = torch.tensor(np.concatenate([[0], np.cumsum(lens_k)]), dtype=torch.int32, device=DEV)
+    q = bf16(rng, int(sum(lens_q)), Hq, D)
+    o = K.flash_attn_varlen_func(q, kc, vc, cu_q, cu_k, max(lens_q), max(lens_k), 0.125,
+                                 block_table=torch.from_numpy(bt).to(DEV))
+    assert torch.isfinite(o.float()).all(), "NaN from slots past a context"
+    ref = P.prefill_attention(f64(q), np.nan_to_num(f64(kc)), np.nan_to_num(f64(vc)), cu_q.cpu().numpy(),
+                              cu_k.cpu().numpy(), 0.125, block_tables=bt)
+    assert_close(f64(o), ref, f"poisoned pool BS={BS}")
 
 
 def test_prefill_long_prompt_and_graph_grid():
