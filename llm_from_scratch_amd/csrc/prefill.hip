@@ -35,9 +35,11 @@ namespace {
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-constexpr int KT = 32;          // keys per tile
-constexpr int QT = 16;          // query tokens per workgroup
-constexpr int VT_PITCH = 72;    // bytes per dim row of the transposed V tile (32 keys + pad)
+constexpr int KT = 64;               // keys per tile
+constexpr int NH = KT / 16;          // 16-key halves (S MFMA row blocks) per tile
+constexpr int NKS = KT / 32;         // 32-key MFMA k steps of P.V per tile
+constexpr int QT = 16;               // query tokens per workgroup
+constexpr int VT_PITCH = 2 * KT + 8; // bytes per dim row of the transposed V tile (+ pad)
 
 template <int D, int G, bool PAGED>
 __global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
@@ -50,10 +52,22 @@ __global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
   constexpr int CPK = D / 8;                         // 16-byte chunks of a key row
   constexpr int VUN = KT / 2 * CPK;                  // (key pair, chunk) units of a V tile
   constexpr int VPT = (VUN + 64 * G - 1) / (64 * G); // units per thread
+  constexpr int KUN = KT * CPK;                      // 16-byte chunks of a K tile
+  constexpr int KPT = (KUN + 64 * G - 1) / (64 * G); // chunks per thread
   __shared__ __attribute__((aligned(16))) uint8_t vt[2][D * VT_PITCH];
+  __shared__ __attribute__((aligned(16))) uint8_t kt[2][KT * 2 * D];
 
-  const int i = blockIdx.x / qtiles, tq0 = (blockIdx.x % qtiles) * QT;
-  const int kh = blockIdx.y;
+  // Workgroup ids are dealt round-robin to the 8 XCDs (id % 8): remap so
+  // that each XCD takes a contiguous range of (sequence, kv head) pairs --
+  // all query tiles of a pair read the same K / V, which then stays in that
+  // XCD's L2 -- and walk a pair's query tiles from the last (longest
+  // causal range) to the first.
+  const int nwg = gridDim.x * gridDim.y;
+  int wid = blockIdx.y * gridDim.x + blockIdx.x;
+  if ((nwg & 7) == 0) wid = (wid & 7) * (nwg >> 3) + (wid >> 3);
+  const int pair = wid / qtiles;
+  const int i = pair / Hkv, kh = pair - i * Hkv;
+  const int tq0 = (qtiles - 1 - (wid - pair * qtiles)) * QT;
   const int q0 = cu_q[i], lq = cu_q[i + 1] - q0;
   if (tq0 >= lq) return;
   const int k0 = cu_k[i], lk = cu_k[i + 1] - k0;
@@ -77,7 +91,7 @@ __global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
     if (blk < 0 || (int64_t)blk * BS >= num_slots) return 0;
     return (int64_t)blk * BS + tc % BS;
   };
-  auto key_elem = [&](const int64_t (&hs)[2], int t0, int kx) -> int64_t {  // key t0 + kx, kx < 32
+  auto key_elem = [&](const int64_t (&hs)[NH], int t0, int kx) -> int64_t {  // key t0 + kx, kx < KT
     const int hf = kx >> 4;
     if constexpr (PAGED) {
       // half base = slot of key min(t0 + 16 hf, lk - 1)
@@ -103,20 +117,35 @@ __global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
   // keys up to the last query of the tile
   const int nkt = (min(lk, off + tq0 + QT) + KT - 1) / KT;
 
-  auto halves = [&](int64_t (&hs)[2], int t0) {
-    if constexpr (PAGED) {
-      hs[0] = half_slot(t0);
-      hs[1] = half_slot(t0 + 16);
-    } else {
-      hs[0] = hs[1] = 0;
+  auto halves = [&](int64_t (&hs)[NH], int t0) {
+#pragma unroll
+    for (int hf = 0; hf < NH; ++hf) {
+      if constexpr (PAGED) hs[hf] = half_slot(t0 + 16 * hf);
+      else hs[hf] = 0;
     }
   };
-  auto load_k = [&](uint4 (&ka)[2][NDC], const int64_t (&hs)[2], int t0) {
+  // K tile in LDS: key rows of 2D bytes, 16-byte chunk c of row r at chunk
+  // slot c ^ f(r) -- f(r) = ((r >> 1) & 7) ^ ((r & 1) << 2) for D = 64 (the
+  // sixteen rows of one operand read, chunks g or g + 4, then touch every
+  // bank once), r & 15 for D = 128
+  auto kswz = [](int r, int c) -> int {
+    const int f = D == 64 ? (((r >> 1) & 7) ^ ((r & 1) << 2)) : (r & 15);
+    return r * 2 * D + ((c ^ f) << 4);
+  };
+  // chunk u of the tile: key u / CPK, chunk u % CPK (a row per CPK lanes)
+  auto load_k = [&](uint4 (&kr)[KPT], const int64_t (&hs)[NH], int t0) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const int64_t o = key_elem(hs, t0, 16 * kb + c16);
+    for (int e = 0; e < KPT; ++e) {
+      const int u = threadIdx.x + 64 * G * e;
+      kr[e] = make_uint4(0, 0, 0, 0);
+      if (u < KUN) kr[e] = *reinterpret_cast<const uint4*>(k + key_elem(hs, t0, u / CPK) + (u % CPK) * 8);
+    }
+  };
+  auto store_kt = [&](const uint4 (&kr)[KPT], int buf) {
 #pragma unroll
-      for (int c = 0; c < NDC; ++c) ka[kb][c] = *reinterpret_cast<const uint4*>(k + o + c * 32 + g * 8);
+    for (int e = 0; e < KPT; ++e) {
+      const int u = threadIdx.x + 64 * G * e;
+      if (u < KUN) *reinterpret_cast<uint4*>(&kt[buf][kswz(u / CPK, u % CPK)]) = kr[e];
     }
   };
   // V unit u of a tile: key pair kp (keys 2kp, 2kp + 1), 16-byte chunk cc of
@@ -128,7 +157,7 @@ __global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
     const int kpl = (u >> 3) % (KT / 2);
     kp = (kpl + 8 * ((u & 7) >> 2)) % (KT / 2);
   };
-  auto load_v = [&](uint4 (&vr)[VPT][2], const int64_t (&hs)[2], int t0) {
+  auto load_v = [&](uint4 (&vr)[VPT][2], const int64_t (&hs)[NH], int t0) {
 #pragma unroll
     for (int e = 0; e < VPT; ++e) {
       const int u = threadIdx.x + 64 * G * e;
@@ -169,40 +198,40 @@ __global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
   for (int db = 0; db < NDB; ++db) o[db] = v4f{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
 
-  uint4 ka[2][NDC], vr[VPT][2];
-  int64_t hs[2];
+  uint4 kr[KPT], vr[VPT][2];
+  int64_t hs[NH];
   halves(hs, 0);
-  load_k(ka, hs, 0);
+  load_k(kr, hs, 0);
   load_v(vr, hs, 0);
   for (int j = 0; j < nkt; ++j) {
     const int t0 = j * KT;
     const int buf = j & 1;
+    store_kt(kr, buf);
     store_vt(vr, buf);
-    // V^T tile j visible to every wave.  The buffer written next (tile j+1)
-    // was last read in tile j-1, which every wave finished before this barrier.
+    // K and V^T of tile j visible to every wave.  The buffers written next
+    // (tile j+1) were last read in tile j-1, which every wave finished
+    // before this barrier.
     __syncthreads();
-    uint4 kc[2][NDC];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int c = 0; c < NDC; ++c) kc[kb][c] = ka[kb][c];
     if (j + 1 < nkt) {
       halves(hs, t0 + KT);
-      load_k(ka, hs, t0 + KT);
+      load_k(kr, hs, t0 + KT);
       load_v(vr, hs, t0 + KT);
     }
+    const uint8_t* kb8 = kt[buf];
 
-    // ---- S^T for the two 16-key halves; the causal mask only where the
-    // tile reaches past the tile's first query position
+    // ---- S^T for the 16-key halves; the causal mask only where the tile
+    // reaches past the tile's first query position
     const bool need_mask = t0 + KT - 1 > off + tq0;
-    float s[2][4];
+    float s[NH][4];
     float tmax = -INFINITY;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < NH; ++kb) {
       v4f sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int c = 0; c < NDC; ++c)
-        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, kc[kb][c]), qb[c], sc, 0, 0, 0);
+      for (int c = 0; c < NDC; ++c) {
+        const uint4 kf = *reinterpret_cast<const uint4*>(kb8 + kswz(16 * kb + c16, 4 * c + g));
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, kf), qb[c], sc, 0, 0, 0);
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         s[kb][r] = sc[r] * scale_log2;
@@ -216,9 +245,9 @@ __global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
     // exp2 on the hardware instruction (arguments <= 0; results below 2^-126 flush to 0)
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
     float psum = 0.f;
-    float p[2][4];
+    float p[NH][4];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < NH; ++kb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         p[kb][r] = __builtin_amdgcn_exp2f(s[kb][r] - m_new);
@@ -229,23 +258,28 @@ __global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
     l_run = l_run * alpha + psum;
     m_run = m_new;
 
-    // ---- O^T = O^T * alpha + V^T P^T
-    v8bf pb;
+    // ---- O^T = O^T * alpha + V^T P^T, one MFMA k step per 32 keys
+    v8bf pb[NKS];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      pb[r] = (__bf16)p[0][r];
-      pb[4 + r] = (__bf16)p[1][r];
-    }
+    for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pb[ks][r] = (__bf16)p[2 * ks][r];
+        pb[ks][4 + r] = (__bf16)p[2 * ks + 1][r];
+      }
     const uint8_t* vb = vt[buf];
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
       const int dim = db * 16 + c16;
-      const uint2 lo = *reinterpret_cast<const uint2*>(vb + dim * VT_PITCH + (4 * g) * 2);
-      const uint2 hi = *reinterpret_cast<const uint2*>(vb + dim * VT_PITCH + (16 + 4 * g) * 2);
-      const uint4 w = make_uint4(lo.x, lo.y, hi.x, hi.y);
 #pragma unroll
       for (int r = 0; r < 4; ++r) o[db][r] *= alpha;
-      o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, w), pb, o[db], 0, 0, 0);
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        const uint2 lo = *reinterpret_cast<const uint2*>(vb + dim * VT_PITCH + (32 * ks + 4 * g) * 2);
+        const uint2 hi = *reinterpret_cast<const uint2*>(vb + dim * VT_PITCH + (32 * ks + 16 + 4 * g) * 2);
+        const uint4 w = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, w), pb[ks], o[db], 0, 0, 0);
+      }
     }
   }
 
