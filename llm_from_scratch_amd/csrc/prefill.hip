@@ -9,7 +9,7 @@
 // block_table[i][t / BS] * BS + t % BS of the KV pool (paged mode, a
 // prefix-cache hit: the cached blocks and the just-stored new tokens).
 //
-// One workgroup per (sequence, tile of 16 query tokens, kv head), one wave
+// One workgroup per (sequence, tile of 16 or 32 query tokens, kv head), one wave
 // per query head of the kv head's group (G waves).  Per tile of 32 keys:
 //   S^T = K Q^T   v_mfma_f32_16x16x32_bf16, K as the A operand loaded from
 //                 HBM in operand layout (lane l: key l % 16, dims
@@ -38,11 +38,12 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int KT = 64;               // keys per tile
 constexpr int NH = KT / 16;          // 16-key halves (S MFMA row blocks) per tile
 constexpr int NKS = KT / 32;         // 32-key MFMA k steps of P.V per tile
-constexpr int QT = 16;               // query tokens per workgroup
+constexpr int QT = 16;               // query tokens per wave (one MFMA column block)
 constexpr int VT_PITCH = 2 * KT + 8; // bytes per dim row of the transposed V tile (+ pad)
 
-template <int D, int G, bool PAGED>
-__global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
+// QW: 16-query sub-tiles per workgroup (G * QW waves share each K / V tile)
+template <int D, int G, bool PAGED, int QW>
+__global__ __launch_bounds__(64 * G * QW) void prefill_attention_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k, const int32_t* __restrict__ bt,
     int64_t bt_stride, int BS, int64_t num_slots, uint16_t* __restrict__ out, int Hkv, int qtiles,
@@ -51,9 +52,10 @@ __global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
   constexpr int NDB = D / 16;                        // 16-dim blocks of O^T
   constexpr int CPK = D / 8;                         // 16-byte chunks of a key row
   constexpr int VUN = KT / 2 * CPK;                  // (key pair, chunk) units of a V tile
-  constexpr int VPT = (VUN + 64 * G - 1) / (64 * G); // units per thread
+  constexpr int NT = 64 * G * QW;                    // threads
+  constexpr int VPT = (VUN + NT - 1) / NT;           // units per thread
   constexpr int KUN = KT * CPK;                      // 16-byte chunks of a K tile
-  constexpr int KPT = (KUN + 64 * G - 1) / (64 * G); // chunks per thread
+  constexpr int KPT = (KUN + NT - 1) / NT;           // chunks per thread
   __shared__ __attribute__((aligned(16))) uint8_t vt[2][D * VT_PITCH];
   __shared__ __attribute__((aligned(16))) uint8_t kt[2][KT * 2 * D];
 
@@ -67,13 +69,17 @@ __global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
   if ((nwg & 7) == 0) wid = (wid & 7) * (nwg >> 3) + (wid >> 3);
   const int pair = wid / qtiles;
   const int i = pair / Hkv, kh = pair - i * Hkv;
-  const int tq0 = (qtiles - 1 - (wid - pair * qtiles)) * QT;
+  const int wq0 = (qtiles - 1 - (wid - pair * qtiles)) * QT * QW;  // the workgroup's first query
   const int q0 = cu_q[i], lq = cu_q[i + 1] - q0;
-  if (tq0 >= lq) return;
+  if (wq0 >= lq) return;  // the whole workgroup
   const int k0 = cu_k[i], lk = cu_k[i + 1] - k0;
   const int off = lk - lq;  // position of query token 0
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int h = kh * G + wave, Hq = Hkv * G;
+  // wave -> (query head of the group, 16-query sub-tile); a sub-tile past lq
+  // still runs the loop (the barriers) and stores nothing
+  const int sub = wave / G;
+  const int tq0 = wq0 + QT * sub;
+  const int h = kh * G + (wave - sub * G), Hq = Hkv * G;
   const int c16 = lane & 15, g = lane >> 4;
   const int64_t row = (int64_t)Hkv * D;  // elements per token row of k / v
   const int64_t hoff = (int64_t)kh * D;
@@ -115,7 +121,7 @@ __global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
   // this lane's query position; rows past lq are computed (finite) and not stored
   const int qp = min(off + tq0 + c16, lk - 1);
   // keys up to the last query of the tile
-  const int nkt = (min(lk, off + tq0 + QT) + KT - 1) / KT;
+  const int nkt = (min(lk, off + wq0 + QT * QW) + KT - 1) / KT;
 
   auto halves = [&](int64_t (&hs)[NH], int t0) {
 #pragma unroll
@@ -136,7 +142,7 @@ __global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
   auto load_k = [&](uint4 (&kr)[KPT], const int64_t (&hs)[NH], int t0) {
 #pragma unroll
     for (int e = 0; e < KPT; ++e) {
-      const int u = threadIdx.x + 64 * G * e;
+      const int u = threadIdx.x + NT * e;
       kr[e] = make_uint4(0, 0, 0, 0);
       if (u < KUN) kr[e] = *reinterpret_cast<const uint4*>(k + key_elem(hs, t0, u / CPK) + (u % CPK) * 8);
     }
@@ -144,7 +150,7 @@ __global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
   auto store_kt = [&](const uint4 (&kr)[KPT], int buf) {
 #pragma unroll
     for (int e = 0; e < KPT; ++e) {
-      const int u = threadIdx.x + 64 * G * e;
+      const int u = threadIdx.x + NT * e;
       if (u < KUN) *reinterpret_cast<uint4*>(&kt[buf][kswz(u / CPK, u % CPK)]) = kr[e];
     }
   };
@@ -160,7 +166,7 @@ __global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
   auto load_v = [&](uint4 (&vr)[VPT][2], const int64_t (&hs)[NH], int t0) {
 #pragma unroll
     for (int e = 0; e < VPT; ++e) {
-      const int u = threadIdx.x + 64 * G * e;
+      const int u = threadIdx.x + NT * e;
       vr[e][0] = vr[e][1] = make_uint4(0, 0, 0, 0);
       if (u < VUN) {
         int kp, cc;
@@ -175,7 +181,7 @@ __global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
   auto store_vt = [&](const uint4 (&vr)[VPT][2], int buf) {
 #pragma unroll
     for (int e = 0; e < VPT; ++e) {
-      const int u = threadIdx.x + 64 * G * e;
+      const int u = threadIdx.x + NT * e;
       if (u < VUN) {
         int kp, cc;
         vunit(u, kp, cc);
@@ -298,14 +304,14 @@ __global__ __launch_bounds__(64 * G) void prefill_attention_kernel(
   }
 }
 
-template <int D, bool PAGED>
+template <int D, bool PAGED, int QW>
 bool launch_prefill(int G, dim3 grid, hipStream_t st, const uint16_t* q, const uint16_t* k, const uint16_t* v,
                     const int32_t* cu_q, const int32_t* cu_k, const int32_t* bt, int64_t bts, int BS,
                     int64_t num_slots, uint16_t* out, int Hkv, int qtiles, float sl2) {
-#define LFS_PG(GG)                                                                                        \
-  case GG:                                                                                                \
-    hipLaunchKernelGGL((prefill_attention_kernel<D, GG, PAGED>), grid, dim3(64 * GG), 0, st, q, k, v, cu_q, \
-                       cu_k, bt, bts, BS, num_slots, out, Hkv, qtiles, sl2);                              \
+#define LFS_PG(GG)                                                                                          \
+  case GG:                                                                                                  \
+    hipLaunchKernelGGL((prefill_attention_kernel<D, GG, PAGED, QW>), grid, dim3(64 * GG * QW), 0, st, q, k, \
+                       v, cu_q, cu_k, bt, bts, BS, num_slots, out, Hkv, qtiles, sl2);                       \
     return true;
   switch (G) {
     LFS_PG(1) LFS_PG(2) LFS_PG(3) LFS_PG(4) LFS_PG(5) LFS_PG(6) LFS_PG(7) LFS_PG(8)
@@ -337,25 +343,44 @@ extern "C" int lfs_prefill_attention(const void* q, const void* k, const void* v
     LFS_REQUIRE(block_size > 0 && block_size % 16 == 0 && num_slots >= block_size && bt_stride > 0,
                 "prefill_attention: bad paged KV geometry (block_size must be a multiple of 16)");
   }
-  const int64_t qtiles = ((int64_t)max_seqlen_q + QT - 1) / QT;
+  // Two 16-query sub-tiles per workgroup (each K / V tile feeds twice the
+  // queries) when that grid still fills every CU several times over;
+  // otherwise one, for finer load balance (measured: 16 x 2048-token
+  // prompts 301 vs 322 us, 16 x 512 queries over 2048 paged keys 220 vs 194 us).
+  const int G = Hq / Hkv;
+  const int64_t qtiles2 = ((int64_t)max_seqlen_q + 2 * QT - 1) / (2 * QT);
+  static int cu_cache[64] = {0};  // compute units per device, read once
+  int cus = 256, dev = 0;
+  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
+    if (cu_cache[dev] == 0) {
+      int n = 0;
+      cu_cache[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0
+                          ? n : 256;
+    }
+    cus = cu_cache[dev];
+  }
+  const int QWs = B * qtiles2 * Hkv >= 8ll * cus ? 2 : 1;
+  const int64_t qtiles = ((int64_t)max_seqlen_q + QT * QWs - 1) / (QT * QWs);
   LFS_REQUIRE(B * qtiles < (1ll << 31) && Hkv < 65536, "prefill_attention: grid too large");
   const dim3 grid((unsigned)(B * qtiles), (unsigned)Hkv);
   const float sl2 = scale * 1.4426950408889634f;
   hipStream_t st = (hipStream_t)stream;
-  const int G = Hq / Hkv;
   const uint16_t *qq = (const uint16_t*)q, *kk = (const uint16_t*)k, *vv = (const uint16_t*)v;
   uint16_t* oo = (uint16_t*)out;
+  const int32_t* bt = block_tables;
+  const int64_t bts = bt != nullptr ? bt_stride : 0;
+  const int BS = bt != nullptr ? block_size : 0;
+  const int qt = (int)qtiles;
+#define LFS_PF(DD, PG, QQ) \
+  launch_prefill<DD, PG, QQ>(G, grid, st, qq, kk, vv, cu_seqlens_q, cu_seqlens_k, bt, bts, BS, num_slots, oo, Hkv, qt, sl2)
   bool ok;
-  if (block_tables != nullptr)
-    ok = D == 64 ? launch_prefill<64, true>(G, grid, st, qq, kk, vv, cu_seqlens_q, cu_seqlens_k, block_tables,
-                                            bt_stride, block_size, num_slots, oo, Hkv, (int)qtiles, sl2)
-                 : launch_prefill<128, true>(G, grid, st, qq, kk, vv, cu_seqlens_q, cu_seqlens_k, block_tables,
-                                             bt_stride, block_size, num_slots, oo, Hkv, (int)qtiles, sl2);
+  if (bt != nullptr)
+    ok = D == 64 ? (QWs == 2 ? LFS_PF(64, true, 2) : LFS_PF(64, true, 1))
+                 : (QWs == 2 ? LFS_PF(128, true, 2) : LFS_PF(128, true, 1));
   else
-    ok = D == 64 ? launch_prefill<64, false>(G, grid, st, qq, kk, vv, cu_seqlens_q, cu_seqlens_k, nullptr, 0, 0,
-                                             num_slots, oo, Hkv, (int)qtiles, sl2)
-                 : launch_prefill<128, false>(G, grid, st, qq, kk, vv, cu_seqlens_q, cu_seqlens_k, nullptr, 0, 0,
-                                              num_slots, oo, Hkv, (int)qtiles, sl2);
+    ok = D == 64 ? (QWs == 2 ? LFS_PF(64, false, 2) : LFS_PF(64, false, 1))
+                 : (QWs == 2 ? LFS_PF(128, false, 2) : LFS_PF(128, false, 1));
+#undef LFS_PF
   LFS_REQUIRE(ok, "prefill_attention: unsupported group size %d", G);
   return check_launch("prefill_attention");
 }

@@ -130,6 +130,34 @@ def test_prefill_long_prompt_and_graph_grid():
     assert_close(f64(o), ref, "long prompt")
 
 
+def test_prefill_large_grid_two_subtiles_vs_torch_fp32():
+    """A grid large enough for two 16-query sub-tiles per workgroup (G * 2
+    waves sharing each K / V tile): against causal attention computed per
+    sequence in float32 with torch on the GPU (the float64 oracle is too
+    slow at this size)."""
+    g = torch.Generator(device=DEV).manual_seed(13)
+    B, L, Hq, Hkv, D = 8, 1024, 16, 8, 64
+    q = torch.randn(B * L, Hq, D, generator=g, device=DEV).to(torch.bfloat16)
+    k = torch.randn(B * L, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
+    v = torch.randn(B * L, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
+    cu = torch.arange(0, (B + 1) * L, L, dtype=torch.int32, device=DEV)
+    o = K.flash_attn_varlen_func(q, k, v, cu, cu, L, L)
+    G = Hq // Hkv
+    mask = torch.ones(L, L, device=DEV, dtype=torch.bool).tril()
+    worst = 0.0
+    for b in range(B):
+        sl = slice(b * L, (b + 1) * L)
+        qf = q[sl].float().permute(1, 0, 2).contiguous()                      # [Hq, L, D]
+        kf = k[sl].float().repeat_interleave(G, 1).permute(1, 2, 0).contiguous()  # [Hq, D, L]
+        vf = v[sl].float().repeat_interleave(G, 1).permute(1, 0, 2).contiguous()  # [Hq, L, D]
+        s = torch.matmul(qf, kf) / D ** 0.5
+        s = s.masked_fill(~mask, float("-inf"))
+        ref = torch.matmul(torch.softmax(s, -1), vf).permute(1, 0, 2)
+        err = (o[sl].float() - ref).abs()
+        assert bool((err <= ATOL + RTOL * ref.abs()).all()), f"sequence {b}: worst {err.max().item():.4g}"
+        worst = max(worst, err.max().item())
+
+
 def test_prefill_argument_errors():
     q = torch.zeros(4, 8, 64, dtype=torch.bfloat16, device=DEV)
     kv = torch.zeros(4, 2, 64, dtype=torch.bfloat16, device=DEV)
