@@ -28,6 +28,8 @@
  *                           counterpart
  *   lfs_fp8_gemm_splitk     the same GEMM split over K for small M (the
  *                           decode-step linears)
+ *   lfs_fp8_gemm_skinny     the same GEMM for M <= 128 (decode batches):
+ *                           K split across the waves of a workgroup
  *   lfs_store_kvcache       the KV slot write of the attention layer that
  *                           engine/model_runner.py:8 imports (absent from the
  *                           reference); slot contract model_runner.py:226-230,
@@ -83,7 +85,7 @@
 extern "C" {
 #endif
 
-#define LFS_ABI_VERSION 6
+#define LFS_ABI_VERSION 7
 
 /* argument errors (negative); launch errors are positive hipError_t values */
 #define LFS_EINVAL (-1)
@@ -150,6 +152,15 @@ int64_t lfs_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t sp
 int lfs_fp8_gemm_splitk(const void* a, const float* a_s, const void* b, const float* b_s,
                         const float* bias, int64_t bias_ld, void* c, int64_t M, int64_t N, int64_t K,
                         int32_t splits, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * fp8_gemm for decode-sized batches, M <= 128: the same result as
+ * lfs_fp8_gemm up to fp32 summation order (the K blocks are split over the
+ * four waves of a workgroup and the partials added through LDS, in wave
+ * order).  One workgroup per 32 output columns; no workspace.
+ */
+int lfs_fp8_gemm_skinny(const void* a, const float* a_s, const void* b, const float* b_s, const float* bias,
+                        int64_t bias_ld, void* c, int64_t M, int64_t N, int64_t K, void* stream);
 
 /*
  * store_kvcache: for t < T with slot = slot_mapping[t] != -1,

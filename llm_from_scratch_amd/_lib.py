@@ -11,7 +11,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "liblfs_kernels.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _c_i64, _c_i32, _c_p, _c_f = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p, ctypes.c_float
 
@@ -27,6 +27,8 @@ SIGNATURES = {
     "lfs_fp8_gemm_workspace_bytes": (ctypes.c_int64, [_c_i64, _c_i64, _c_i64, _c_i32]),
     "lfs_fp8_gemm_splitk": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
                                            _c_i32, _c_p, _c_i64, _c_p]),
+    "lfs_fp8_gemm_skinny": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
+                                           _c_p]),
     "lfs_store_kvcache": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_i32,
                                          _c_i32, _c_i64, _c_p]),
     "lfs_paged_decode_workspace_bytes": (ctypes.c_int64, [_c_i64, _c_i32, _c_i32, _c_i32, _c_i32]),

@@ -398,6 +398,130 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
 }
 
 // ---------------------------------------------------------------------------
+// Skinny GEMM for decode-sized M (<= 128): one workgroup per 32 output
+// columns and all M rows, in WGM groups of four waves; group gm owns row
+// tiles gm*MTW .. gm*MTW + MTW - 1, and its wave kw takes K blocks kw,
+// kw+4, ... (each block: MTW x 2 MFMAs, the B fragments as the first operand
+// so a lane ends with one activation row and four weight columns, i.e. one
+// a_s * b_s product per lane and row tile; the next block's fragments are
+// loaded before the current block's MFMAs).  The four partial sums of a
+// group are added through LDS in wave order, wave kw finishing row tiles
+// kw, kw + 4, ... of its group (bias, bf16 rounding).  At M = 128 and
+// N = 1280 that is 40 workgroups where the 128 x 128 tile kernel has 10,
+// with no split-K workspace or second kernel.
+constexpr int SK_BN = 32;
+
+template <int MTW, int WGM>
+__global__ __launch_bounds__(256 * WGM) void fp8_gemm_skinny(
+    const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ B,
+    const float* __restrict__ Bs, const float* __restrict__ bias, int64_t bias_ld, uint16_t* __restrict__ C,
+    int M, int N, int K) {
+  __shared__ __attribute__((aligned(16))) v4f red[WGM][4][MTW][2][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int gm = wave >> 2, kw = wave & 3;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * SK_BN;
+  const int KT = K / BK;
+  const uint8_t* brow[2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) brow[nt] = B + (size_t)min(n0 + 16 * nt + r16, N - 1) * K + g * 16;
+  // activation rows as 32-bit offsets (M * K < 2^31 is checked on the host)
+  uint32_t aoff[MTW], soff[MTW];
+#pragma unroll
+  for (int mt = 0; mt < MTW; ++mt) {
+    const uint32_t m = (uint32_t)min(16 * (gm * MTW + mt) + r16, M - 1);
+    aoff[mt] = m * (uint32_t)K + g * 16;
+    soff[mt] = m * (uint32_t)KT;
+  }
+  const float* bsrow = Bs + (size_t)(n0 / 128) * KT;  // 32 columns share one 128-row scale block
+
+  v4f acc[MTW][2];
+#pragma unroll
+  for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  // operand chunks g and g + 4 of the 128-byte K block (both operands)
+  auto ld = [](const uint8_t* p) -> v8i {
+    const u32x4 lo = *reinterpret_cast<const u32x4*>(p);
+    const u32x4 hi = *reinterpret_cast<const u32x4*>(p + 64);
+    return __builtin_bit_cast(v8i, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
+  // two register buffers, filled alternately (no copies between them)
+  v8i bf0[2], af0[MTW], bf1[2], af1[MTW];
+  float sa0[MTW], sa1[MTW], sb0 = 0.f, sb1 = 0.f;
+  auto load_block = [&](v8i (&bf)[2], v8i (&af)[MTW], float (&sa)[MTW], float& sb, int kb) {
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) bf[nt] = ld(brow[nt] + (size_t)kb * BK);
+#pragma unroll
+    for (int mt = 0; mt < MTW; ++mt) {
+      af[mt] = ld(A + aoff[mt] + (uint32_t)kb * BK);
+      sa[mt] = As[soff[mt] + kb];
+    }
+    sb = bsrow[kb];
+  };
+  auto compute = [&](const v8i (&bf)[2], const v8i (&af)[MTW], const float (&sa)[MTW], float sb) {
+#pragma unroll
+    for (int mt = 0; mt < MTW; ++mt) {
+      const float sc = sa[mt] * sb;
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const v4f t = mfma_fp8(bf[nt], af[mt]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[mt][nt][r] = fmaf(t[r], sc, acc[mt][nt][r]);
+      }
+    }
+  };
+  if (kw < KT) load_block(bf0, af0, sa0, sb0, kw);
+  for (int kb = kw; kb < KT; kb += 8) {
+    if (kb + 4 < KT) load_block(bf1, af1, sa1, sb1, kb + 4);
+    compute(bf0, af0, sa0, sb0);
+    if (kb + 4 >= KT) break;
+    if (kb + 8 < KT) load_block(bf0, af0, sa0, sb0, kb + 8);
+    compute(bf1, af1, sa1, sb1);
+  }
+
+  // ---- the four partials of the group, summed in wave order
+#pragma unroll
+  for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) red[gm][kw][mt][nt][lane] = acc[mt][nt];
+  __syncthreads();
+  for (int mt = kw; mt < MTW; mt += 4) {
+    const int m = 16 * (gm * MTW + mt) + r16;
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      v4f s = red[gm][0][mt][nt][lane];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) {
+        const v4f x = red[gm][w][mt][nt][lane];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s[r] += x[r];
+      }
+      const int col = n0 + 16 * nt + 4 * g;
+      if (m >= M) continue;
+      float bv[4] = {0.f, 0.f, 0.f, 0.f};
+      if (bias != nullptr) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (col + r < N) bv[r] = bias_ld == 0 ? bias[col + r] : bias[(int64_t)m * bias_ld + col + r];
+      }
+      uint16_t* dst = C + (size_t)m * N + col;
+      if (col + 3 < N && (N & 3) == 0) {
+        uint2 o;
+        o.x = pack_bf16x2(s[0] + bv[0], s[1] + bv[1]);
+        o.y = pack_bf16x2(s[2] + bv[2], s[3] + bv[3]);
+        *reinterpret_cast<uint2*>(dst) = o;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (col + r < N) dst[r] = (uint16_t)f32_to_bf16(s[r] + bv[r]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // 256x256 tile, 8 waves (2 x 4), 128 x 64 per wave (8 x 4 MFMA tiles).
 //
 // Half the global->LDS bytes per flop of the 128x128 tile and 3/4 of its LDS
@@ -754,4 +878,29 @@ extern "C" int lfs_fp8_grouped_gemm(const void* a, const float* a_s, int64_t a_r
                      (uint16_t*)c, (int)M, (int)N, (int)K, (int)num_tiles, (int)tiles_n, c_f32, (int)(K / 128),
                      ldb, (int)ldbs, grp);
   return check_launch("fp8_grouped_gemm");
+}
+
+extern "C" int lfs_fp8_gemm_skinny(const void* a, const float* a_s, const void* b, const float* b_s,
+                                   const float* bias, int64_t bias_ld, void* c, int64_t M, int64_t N, int64_t K,
+                                   void* stream) {
+  LFS_REQUIRE(M >= 0 && N >= 0 && K >= 0, "fp8_gemm_skinny: negative shape");
+  LFS_REQUIRE(M <= 128, "fp8_gemm_skinny: M=%lld must be <= 128", (long long)M);
+  LFS_REQUIRE(K % 128 == 0, "fp8_gemm_skinny: K=%lld must be a multiple of 128", (long long)K);
+  LFS_REQUIRE(N < (1ll << 31) && K < (1ll << 24), "fp8_gemm_skinny: shape too large");
+  if (M == 0 || N == 0) return 0;
+  LFS_REQUIRE(K > 0 && a && a_s && b && b_s && c, "fp8_gemm_skinny: null pointer");
+  LFS_REQUIRE((((uintptr_t)a | (uintptr_t)b) & 15u) == 0, "fp8_gemm_skinny: a and b must be 16-byte aligned");
+  LFS_REQUIRE(bias_ld == 0 || (bias != nullptr && bias_ld >= N), "fp8_gemm_skinny: bias_ld must be 0 or >= N");
+  const dim3 grid((unsigned)((N + SK_BN - 1) / SK_BN));
+  hipStream_t st = (hipStream_t)stream;
+  const int mt = (int)((M + 15) / 16);
+#define LFS_SK(MTW, WGM)                                                                                   \
+  hipLaunchKernelGGL((fp8_gemm_skinny<MTW, WGM>), grid, dim3(256 * WGM), 0, st, (const uint8_t*)a, a_s,     \
+                     (const uint8_t*)b, b_s, bias, bias_ld, (uint16_t*)c, (int)M, (int)N, (int)K)
+  if (mt <= 1) LFS_SK(1, 1);
+  else if (mt <= 2) LFS_SK(2, 1);
+  else if (mt <= 4) LFS_SK(4, 1);
+  else LFS_SK(4, 2);
+#undef LFS_SK
+  return check_launch("fp8_gemm_skinny");
 }

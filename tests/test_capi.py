@@ -57,6 +57,10 @@ def test_argument_errors_are_reported_without_launch(lib):
     assert rc == -1 and b"workspace" in lib.lfs_last_error()
     rc = lib.lfs_fp8_gemm(16, 16, 16, 16, 16, 4, 16, 8, 8, 128, None)
     assert rc == -1 and b"bias_ld" in lib.lfs_last_error()
+    rc = lib.lfs_fp8_gemm_skinny(16, 16, 16, 16, None, 0, 16, 129, 8, 128, None)
+    assert rc == -1 and b"<= 128" in lib.lfs_last_error()
+    rc = lib.lfs_fp8_gemm_skinny(16, 16, 16, 16, None, 0, 16, 8, 8, 100, None)
+    assert rc == -1 and b"multiple of 128" in lib.lfs_last_error()
     rc = lib.lfs_add_rmsnorm(None, None, None, None, None, None, None, 4, 100, 1e-5, None)
     assert rc == -1 and b"multiple of 8" in lib.lfs_last_error()
     rc = lib.lfs_add_rmsnorm(None, None, None, None, None, 16, 16, 4, 200, 1e-5, None)

@@ -45,30 +45,6 @@ def test_act_quant_cfg1():
     check_act_quant(W.activation(256, 512, seed=0, outliers=False).to(DEV))
 
 
-@pytest.mark.parametrize("splits", [2, 3, 5, 7])
-def test_fp8_gemm_split_k(splits):
-    """K split over workgroups (fp32 partials + reduction): same oracle,
-    ragged M/N, a K count that does not divide evenly, bias vector and
-    per-row bias matrix."""
-    rng = np.random.default_rng(40 + splits)
-    M, N, Kd = 300, 400, 640
-    ac = rng.integers(0, 256, (M, Kd), dtype=np.uint8)
-    bc = rng.integers(0, 256, (N, Kd), dtype=np.uint8)
-    ac[(ac & 0x7F) == 0x7F] = 0
-    bc[(bc & 0x7F) == 0x7F] = 0
-    a = torch.from_numpy(ac).view(torch.float8_e4m3fn).to(DEV)
-    b = torch.from_numpy(bc).view(torch.float8_e4m3fn).to(DEV)
-    a_s = torch.from_numpy(rng.uniform(1e-3, 1e-2, (M, Kd // 128)).astype(np.float32)).to(DEV)
-    b_s = torch.from_numpy(rng.uniform(1e-3, 1e-2, (-(-N // 128), Kd // 128)).astype(np.float32)).to(DEV)
-    bias = torch.from_numpy(rng.standard_normal(N).astype(np.float32)).to(DEV)
-    bm = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32)).to(DEV)
-    for bb, what in ((None, "nobias"), (bias, "bias"), (bm, "bias matrix")):
-        got = K.fp8_gemm(a, a_s, b, b_s, bb, splits=splits)
-        assert_close(f32(got), gemm_oracle(a, a_s, b, b_s, bb), f"splits={splits} {what}")
-        one = K.fp8_gemm(a, a_s, b, b_s, bb, splits=1)
-        assert np.abs(f32(got) - f32(one)).max() <= 2e-2 + 1e-2 * np.abs(f32(one)).max()
-
-
 @pytest.mark.parametrize("M", [1, 16, 128, 4096])
 @pytest.mark.parametrize("Kd", [1024, 4096, 2048])
 def test_act_quant_cfg2_outliers(M, Kd):
@@ -240,6 +216,49 @@ def test_fp8_gemm_split_k(splits):
         assert_close(f32(got), gemm_oracle(a, a_s, b, b_s, bb), f"splits={splits} {what}")
         one = K.fp8_gemm(a, a_s, b, b_s, bb, splits=1)
         assert np.abs(f32(got) - f32(one)).max() <= 2e-2 + 1e-2 * np.abs(f32(one)).max()
+
+
+@pytest.mark.parametrize("M,N,Kd", [(1, 768, 768), (5, 1282, 128), (17, 250, 384), (33, 96, 1024),
+                                    (100, 4096, 768), (128, 1280, 768), (128, 31, 512)])
+def test_fp8_gemm_skinny(M, N, Kd):
+    """The decode-batch kernel (M <= 128, K blocks split over the four
+    waves of a workgroup): every byte pattern but NaN, distinct scales,
+    ragged M and N (N not a multiple of 32 or of 4), 1 to 8 K blocks (fewer
+    than and not a multiple of the four waves), bias vector and per-row bias
+    matrix; against the oracle and the 128 x 128 tile kernel."""
+    assert K.use_skinny_gemm(M, N, Kd)
+    rng = np.random.default_rng(M * 7 + N + Kd)
+    ac = rng.integers(0, 256, (M, Kd), dtype=np.uint8)
+    bc = rng.integers(0, 256, (N, Kd), dtype=np.uint8)
+    ac[(ac & 0x7F) == 0x7F] = 0
+    bc[(bc & 0x7F) == 0x7F] = 0
+    a = torch.from_numpy(ac).view(torch.float8_e4m3fn).to(DEV)
+    b = torch.from_numpy(bc).view(torch.float8_e4m3fn).to(DEV)
+    a_s = torch.from_numpy(rng.uniform(1e-3, 1e-2, (M, Kd // 128)).astype(np.float32)).to(DEV)
+    b_s = torch.from_numpy(rng.uniform(1e-3, 1e-2, (-(-N // 128), Kd // 128)).astype(np.float32)).to(DEV)
+    bias = torch.from_numpy(rng.standard_normal(N).astype(np.float32)).to(DEV)
+    bm = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32)).to(DEV)
+    for bb, what in ((None, "nobias"), (bias, "bias"), (bm, "bias matrix")):
+        got = K.fp8_gemm(a, a_s, b, b_s, bb)
+        assert_close(f32(got), gemm_oracle(a, a_s, b, b_s, bb), f"skinny {M}x{N}x{Kd} {what}")
+        tile = K.fp8_gemm(a, a_s, b, b_s, bb, splits=1)
+        assert np.abs(f32(got) - f32(tile)).max() <= 2e-2 + 1e-2 * np.abs(f32(tile)).max()
+
+
+def test_fp8_gemm_skinny_exact_small_integers():
+    """Small-integer codes with unit scales: every partial sum is an exact
+    fp32 integer, so the wave-split sum is bit-exact in any order."""
+    rng = np.random.default_rng(22)
+    M, N, Kd = 100, 200, 1024
+    assert K.use_skinny_gemm(M, N, Kd)
+    ints = np.arange(-8, 9, dtype=np.float32)
+    a = torch.from_numpy(F.e4m3_encode(rng.choice(ints, (M, Kd)))).view(torch.float8_e4m3fn).to(DEV)
+    b = torch.from_numpy(F.e4m3_encode(rng.choice(ints, (N, Kd)))).view(torch.float8_e4m3fn).to(DEV)
+    a_s = torch.ones(M, Kd // 128, device=DEV)
+    b_s = torch.ones(-(-N // 128), Kd // 128, device=DEV)
+    c = K.fp8_gemm(a, a_s, b, b_s)
+    exact = F.e4m3_decode(codes(a)).astype(np.int64) @ F.e4m3_decode(codes(b)).astype(np.int64).T
+    np.testing.assert_array_equal(f32(c), F.bf16_round(exact.astype(np.float32)))
 
 
 @pytest.mark.parametrize("M,N,Kd", [(4000, 4042, 1152), (4096, 4040, 640)])
