@@ -85,7 +85,7 @@
 extern "C" {
 #endif
 
-#define LFS_ABI_VERSION 7
+#define LFS_ABI_VERSION 8
 
 /* argument errors (negative); launch errors are positive hipError_t values */
 #define LFS_EINVAL (-1)
@@ -188,6 +188,11 @@ int lfs_store_kvcache(const void* key, int64_t k_stride_t, const void* value, in
  * parallel and merged by log-sum-exp; the grid depends only on B and
  * max_blocks (not on the lengths), so the call is graph-capturable.
  * workspace: at least lfs_paged_decode_workspace_bytes(...) bytes.
+ * Optionally (q_out and q_scale both non-NULL) also the act_quant of each
+ * output row, the output projection's FP8 input: q_out e4m3fn [B, Hq*D],
+ * q_scale fp32 [B, Hq*D/128], bit-identical to lfs_act_quant(out, 128)
+ * (needs Hq*D % 128 == 0, Hq*D <= 8192); the merge then runs one workgroup
+ * per sequence instead of one per (head, sequence).
  * D in {64, 128}; Hq % Hkv == 0, Hq/Hkv <= 8; block_size a multiple of 16.
  */
 int64_t lfs_paged_decode_workspace_bytes(int64_t B, int32_t num_q_heads, int32_t head_dim,
@@ -198,7 +203,7 @@ int lfs_paged_decode(const void* q, const void* k_cache, const void* v_cache,
                      void* out, void* workspace, int64_t workspace_bytes, int64_t B,
                      int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                      int32_t block_size, int64_t num_blocks, int32_t max_blocks, float scale,
-                     int32_t blocks_per_split, void* stream);
+                     int32_t blocks_per_split, void* q_out, float* q_scale, void* stream);
 
 /*
  * Varlen causal prefill attention, GQA (G = Hq / Hkv):

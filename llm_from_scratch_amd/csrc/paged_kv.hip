@@ -16,7 +16,9 @@
 //   output is written directly.
 // phase 2 (paged_decode_merge, one workgroup per (head, sequence)):
 //   log-sum-exp merge of the chunks, normalise, bf16.  Padding rows
-//   (context_len 0) get zeros.
+//   (context_len 0) get zeros.  paged_decode_merge_quant (one workgroup per
+//   sequence) does the same and also writes the act_quant codes and scales
+//   of the bf16 output row (the output projection's FP8 input).
 #include "common.h"
 
 namespace lfs {
@@ -363,6 +365,94 @@ __global__ __launch_bounds__(128) void paged_decode_merge(
   out[((int64_t)b * Hq + h) * D + d] = (uint16_t)f32_to_bf16(res);
 }
 
+// Phase 2 fused with the output projection's act_quant: one workgroup per
+// sequence merges every head (or re-reads the rows the split kernel wrote
+// for a single-chunk context; zeros for context 0), writes the bf16 output,
+// and quantises the row per 128-value group with act_quant's formula and
+// rounding (the codes equal act_quant of the bf16 output bit for bit).
+constexpr int MQ_MAXE = 8192;  // Hq * D per sequence
+constexpr int MQ_MAXH = 128;
+constexpr int MQ_MAXW = 4096;  // (split, head) weights staged in LDS
+
+__global__ __launch_bounds__(256) void paged_decode_merge_quant(
+    const float* __restrict__ ws_o, const float* __restrict__ ws_ml, const int64_t* __restrict__ ctx_lens,
+    uint16_t* __restrict__ out, uint8_t* __restrict__ qo, float* __restrict__ qs, int Hq, int D, int BS,
+    int max_blocks, int bps, int max_splits) {
+  __shared__ float hDen[MQ_MAXH];
+  __shared__ float wts[MQ_MAXW];  // [split][head]: exp2(m - M_head), then the per-head sums
+  __shared__ __attribute__((aligned(16))) uint16_t vals[MQ_MAXE];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const int64_t Lc = min(ctx_lens[b], (int64_t)max_blocks * BS);
+  const int64_t chunk = (int64_t)bps * BS;
+  const int ns = (int)((Lc + chunk - 1) / chunk);
+  const int E = Hq * D;
+  uint16_t* orow = out + (int64_t)b * E;
+  if (ns > 1) {
+    const int64_t pbase = (int64_t)b * max_splits;
+    // (m, l) of every (split, head) in one parallel step; the per-head max,
+    // weights and denominators from LDS (the unfused merge's arithmetic)
+    const bool staged = ns * Hq <= MQ_MAXW;
+    if (staged) {
+      for (int x = tid; x < ns * Hq; x += 256) wts[x] = ws_ml[(pbase * Hq + x) * 2];
+      __syncthreads();
+    }
+    auto mval = [&](int sp, int h) -> float { return staged ? wts[sp * Hq + h] : ws_ml[((pbase + sp) * Hq + h) * 2]; };
+    for (int h = tid; h < Hq; h += 256) {
+      float M = -INFINITY;
+      for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, mval(sp, h));
+      float den = 0.f;
+      if (M != -INFINITY)
+        for (int sp = 0; sp < ns; ++sp) {
+          const float w = exp2f(mval(sp, h) - M);
+          den = fmaf(w, ws_ml[((pbase + sp) * Hq + h) * 2 + 1], den);
+          if (staged) wts[sp * Hq + h] = w;  // this thread alone reads / writes head h's entries
+        }
+      else if (staged)
+        for (int sp = 0; sp < ns; ++sp) wts[sp * Hq + h] = 0.f;
+      hDen[h] = M != -INFINITY ? den : 0.f;
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += 256) {
+      const int h = e / D, d = e - h * D;
+      const float den = hDen[h];
+      float num = 0.f;
+      if (staged) {
+        for (int sp = 0; sp < ns; ++sp) num = fmaf(wts[sp * Hq + h], ws_o[((pbase + sp) * Hq + h) * D + d], num);
+      } else {
+        float M = -INFINITY;
+        for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, mval(sp, h));
+        if (M != -INFINITY)
+          for (int sp = 0; sp < ns; ++sp)
+            num = fmaf(exp2f(mval(sp, h) - M), ws_o[((pbase + sp) * Hq + h) * D + d], num);
+      }
+      const uint16_t v = (uint16_t)f32_to_bf16(den > 0.f ? num / den : 0.f);
+      orow[e] = v;
+      vals[e] = v;
+    }
+  } else if (ns == 1) {
+    for (int e = tid; e < E; e += 256) vals[e] = orow[e];  // written by the split kernel
+  } else {
+    for (int e = tid; e < E; e += 256) {
+      orow[e] = 0;
+      vals[e] = 0;
+    }
+  }
+  __syncthreads();
+  // act_quant of the row: 16 lanes per 128-value group, 8 values per lane
+  // (E / 8 is a multiple of 16, so a group's lanes are all in or all out)
+  for (int c8 = tid; c8 < E / 8; c8 += 256) {
+    float f[8];
+    unpack8(*reinterpret_cast<const uint4*>(&vals[c8 * 8]), f);
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[i]));
+    amax = group_max<16>(amax);
+    const float sc = scale_from_amax(amax, false);
+    *reinterpret_cast<uint2*>(qo + (int64_t)b * E + c8 * 8) = quant8(f, sc);
+    if ((c8 & 15) == 0) qs[(int64_t)b * (E / 128) + c8 / 16] = sc;
+  }
+}
+
 template <int D, int G>
 void launch_split(dim3 grid, dim3 block, hipStream_t st, const uint16_t* q, const uint16_t* kc,
                   const uint16_t* vc, const int64_t* cl, const int32_t* bt, int64_t bts, float* wo,
@@ -431,7 +521,7 @@ extern "C" int lfs_paged_decode(const void* q, const void* k_cache, const void* 
                                 int64_t workspace_bytes, int64_t B, int32_t num_q_heads,
                                 int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                                 int64_t num_blocks, int32_t max_blocks, float scale,
-                                int32_t blocks_per_split, void* stream) {
+                                int32_t blocks_per_split, void* q_out, float* q_scale, void* stream) {
   const int Hq = num_q_heads, Hkv = num_kv_heads, D = head_dim, BS = block_size;
   LFS_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && BS > 0 && num_blocks >= 0 && max_blocks >= 0,
               "paged_decode: bad shape");
@@ -448,6 +538,9 @@ extern "C" int lfs_paged_decode(const void* q, const void* k_cache, const void* 
   LFS_REQUIRE(((((uintptr_t)q) | ((uintptr_t)k_cache) | ((uintptr_t)v_cache)) & 15u) == 0,
               "paged_decode: q and caches must be 16-byte aligned");
   LFS_REQUIRE(B < 65536, "paged_decode: batch too large");
+  LFS_REQUIRE((q_out == nullptr) == (q_scale == nullptr), "paged_decode: q_out and q_scale go together");
+  LFS_REQUIRE(q_out == nullptr || (Hq * D % 128 == 0 && Hq * D <= MQ_MAXE && Hq <= MQ_MAXH),
+              "paged_decode: the quantised output needs Hq*D %% 128 == 0, Hq*D <= %d", MQ_MAXE);
   const int64_t need = lfs_paged_decode_workspace_bytes(B, Hq, D, max_blocks, blocks_per_split);
   LFS_REQUIRE(workspace_bytes >= need && (need == 0 || workspace),
               "paged_decode: workspace of %lld bytes < required %lld", (long long)workspace_bytes,
@@ -479,6 +572,12 @@ extern "C" int lfs_paged_decode(const void* q, const void* k_cache, const void* 
     LFS_REQUIRE(ok, "paged_decode: unsupported group size %d", G);
     const int rc = check_launch("paged_decode(split)");
     if (rc) return rc;
+  }
+  if (q_out != nullptr) {
+    hipLaunchKernelGGL(paged_decode_merge_quant, dim3((unsigned)B), dim3(256), 0, st, ws_o, ws_ml, context_lens,
+                       (uint16_t*)out, (uint8_t*)q_out, q_scale, Hq, D, BS, max_blocks, blocks_per_split,
+                       max_splits);
+    return check_launch("paged_decode(merge + quant)");
   }
   hipLaunchKernelGGL(paged_decode_merge, dim3((unsigned)Hq, (unsigned)B), dim3((unsigned)D), 0, st,
                      ws_o, ws_ml, context_lens, (uint16_t*)out, Hq, D, BS, max_blocks,

@@ -21,8 +21,8 @@ Interface (nano-vLLM style, as the runner expects):
     logits = model.compute_logits(hidden)             # bf16 [T, vocab]
 
 Kernels per layer: add_rmsnorm (+act_quant) -> qkv FP8 GEMM ->
-qk_norm_rope_store -> paged decode (split + merge) -> act_quant -> output
-FP8 GEMM -> add_rmsnorm (+act_quant) -> moe_route -> gate/up FP8 GEMM ->
+qk_norm_rope_store -> paged decode (split + merge with the act_quant of its
+output) -> output FP8 GEMM -> add_rmsnorm (+act_quant) -> moe_route -> gate/up FP8 GEMM ->
 swiglu_quant -> down FP8 GEMM.  Setting ``model.trace = {}`` makes an
 eager forward record every intermediate (per layer) for parity tests.
 
@@ -144,11 +144,14 @@ class PagedGQAAttention(nn.Module):
                 v = self.v_cache.view(flat)[ctx.slot_mapping]
                 o = kernels.flash_attn_varlen_func(q, k, v, ctx.cu_seqlens_q, ctx.cu_seqlens_k,
                                                    ctx.max_seqlen_q, ctx.max_seqlen_k, self.scale)
+            o = o.reshape(T, -1)
+            out = self.output_proj(o)
         else:
-            o = kernels.paged_attention_decode(q, self.k_cache, self.v_cache, ctx.context_lens,
-                                               ctx.block_tables, self.scale)
-        o = o.reshape(T, -1)
-        out = self.output_proj(o)
+            # the merge also writes the output projection's FP8 input (act_quant fused)
+            o, oq, os_ = kernels.paged_attention_decode(q, self.k_cache, self.v_cache, ctx.context_lens,
+                                                        ctx.block_tables, self.scale, quant=True)
+            o = o.reshape(T, -1)
+            out = self.output_proj.gemm(oq, os_)
         if trace is not None:
             trace.update(qkv=qkv, q=q, att_o=o, att_out=out)
         return out

@@ -263,7 +263,7 @@ def paged_decode_workspace_bytes(batch: int, num_q_heads: int, head_dim: int, ma
 def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                            context_lens: torch.Tensor, block_tables: torch.Tensor,
                            scale: Optional[float] = None, blocks_per_split: Optional[int] = None,
-                           workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                           workspace: Optional[torch.Tensor] = None, quant: bool = False):
     """One decode step of GQA attention over a paged KV pool.
 
     q: bf16 [B, Hq, D]; caches bf16 [num_blocks, block_size, Hkv, D];
@@ -273,7 +273,10 @@ def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     The grid depends only on B and max_blocks, so the call can be captured
     in a HIP graph (pass a preallocated ``workspace`` of
     ``paged_decode_workspace_bytes`` bytes to keep the capture free of
-    allocations).
+    allocations).  With ``quant`` the merge also quantises each output row
+    for the next FP8 linear and the call returns (o, codes e4m3fn
+    [B, Hq*D], scales fp32 [B, Hq*D/128]), the codes equal to
+    act_quant(o.view(B, -1)) bit for bit.
     """
     assert q.dim() == 3 and q.is_contiguous(), "q must be contiguous [B, Hq, D]"
     assert k_cache.is_contiguous() and v_cache.is_contiguous() and k_cache.shape == v_cache.shape
@@ -297,13 +300,17 @@ def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     if workspace is None:
         workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=q.device)
     o = torch.empty_like(q)
+    oq = os_ = None
+    if quant:
+        oq = torch.empty(B, Hq * D, dtype=FP8, device=q.device)
+        os_ = torch.empty(B, Hq * D // 128, dtype=torch.float32, device=q.device)
     rc = _lib.load().lfs_paged_decode(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(context_lens),
                                       _ptr(block_tables), block_tables.stride(0), _ptr(o),
                                       _ptr(workspace), workspace.numel() * workspace.element_size(),
                                       B, Hq, Hkv, D, BS, NB, max_blocks, float(scale), bps,
-                                      _stream(q))
+                                      _ptr(oq), _ptr(os_), _stream(q))
     _lib.check(rc, "paged_attention_decode")
-    return o
+    return (o, oq, os_) if quant else o
 
 
 def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,

@@ -45,11 +45,14 @@ def test_argument_errors_are_reported_without_launch(lib):
     rc = lib.lfs_fp8_gemm(None, None, None, None, None, 0, None, 4, 4, 100, None)
     assert rc == -1 and b"multiple of 128" in lib.lfs_last_error()
     rc = lib.lfs_paged_decode(None, None, None, None, None, 4, None, None, 0, 2, 16, 4, 96, 256, 8, 4,
-                              0.1, 1, None)
+                              0.1, 1, None, None, None)
     assert rc == -1 and b"head_dim" in lib.lfs_last_error()
     rc = lib.lfs_paged_decode(None, None, None, None, None, 4, None, None, 0, 2, 12, 5, 64, 256, 8, 4,
-                              0.1, 1, None)
+                              0.1, 1, None, None, None)
     assert rc == -1 and b"multiple of num_kv_heads" in lib.lfs_last_error()
+    rc = lib.lfs_paged_decode(16, 16, 16, 16, 16, 4, 16, 16, 1 << 20, 2, 12, 4, 64, 256, 8, 4,
+                              0.1, 1, 16, None, None)
+    assert rc == -1 and b"go together" in lib.lfs_last_error()
     with pytest.raises(ValueError, match="block_size"):
         _lib.check(lib.lfs_weight_quant(None, None, None, 8, 8, 7, None), "weight_quant")
     # split-K needs its workspace (non-null dummy pointers: the check comes first)

@@ -170,6 +170,37 @@ def test_paged_decode_shapes(Hq, Hkv, D, BS):
     assert_close(got[0], np.repeat(v0, G, axis=0), "L=1")
 
 
+@pytest.mark.parametrize("Hq,Hkv,D,BS", [(12, 4, 64, 256), (16, 2, 128, 32), (6, 2, 64, 48)])
+def test_paged_decode_fused_quant_equals_act_quant(Hq, Hkv, D, BS):
+    """The merge's act_quant of each output row: codes and scales equal
+    act_quant of the bf16 output bit for bit, for single-chunk, multi-chunk
+    and padding rows alike; the bf16 output equals the unfused call's."""
+    rng = np.random.default_rng(Hq + D + BS)
+    B, NB = 7, 128
+    lens = np.array([1, 0, BS, BS + 1, 3 * BS - 1, 5, 2 * BS], np.int64)
+    maxb = int((-(-lens // BS)).max()) + 1
+    perm = rng.permutation(NB)
+    bt = np.full((B, maxb), -1, np.int32)
+    pos = 0
+    for b, L in enumerate(lens):
+        nb = -(-int(L) // BS)
+        bt[b, :nb] = perm[pos:pos + nb]
+        pos += nb
+    g = torch.Generator(device=DEV).manual_seed(17)
+    kc = torch.randn(NB, BS, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
+    vc = torch.randn(NB, BS, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
+    q = torch.randn(B, Hq, D, generator=g, device=DEV).to(torch.bfloat16)
+    cl, btd = torch.from_numpy(lens).to(DEV), torch.from_numpy(bt).to(DEV)
+    for bps in (1, 2):  # chunks of one block: several chunks per row
+        o, oq, os_ = K.paged_attention_decode(q, kc, vc, cl, btd, blocks_per_split=bps, quant=True)
+        plain = K.paged_attention_decode(q, kc, vc, cl, btd, blocks_per_split=bps)
+        assert torch.equal(o, plain)
+        rq, rs = K.act_quant(o.view(B, -1))
+        assert torch.equal(oq.view(torch.uint8), rq.view(torch.uint8)), f"codes bps={bps}"
+        assert torch.equal(os_, rs), f"scales bps={bps}"
+        assert bool((o[1] == 0).all())  # padding row
+
+
 def test_decode_step_store_then_attend():
     """The decode step of the attention layer: write the new token's K/V at
     its slot, then attend over the context including it."""
