@@ -96,30 +96,21 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// One wave: kv head kh of sequence b over context rows [t_begin, t_end)
+// (t_begin a multiple of `tile`, t_end <= Lc).  A range that is the whole
+// context (t_begin == 0, t_end >= Lc) writes the normalised bf16 output;
+// otherwise the unnormalised partial of query head kh*G + g goes to row
+// prow + g of the workspace (o: ws_o[row*D ..], (m, l): ws_ml[row*2 ..]).
+// pw: the wave's private LDS slice (T * GP floats).
 template <int D, int G>
-__global__ __launch_bounds__(256) void paged_decode_split(
+__device__ __forceinline__ void decode_chunk(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
-    const uint16_t* __restrict__ vc, const int64_t* __restrict__ ctx_lens,
-    const int32_t* __restrict__ bt, int64_t bt_stride, float* __restrict__ ws_o,
-    float* __restrict__ ws_ml, uint16_t* __restrict__ out, int Hkv, int BS, int64_t NB,
-    int max_blocks, int bps, int tile, float scale_log2, int max_splits) {
+    const uint16_t* __restrict__ vc, const int32_t* __restrict__ btrow, float* __restrict__ ws_o,
+    float* __restrict__ ws_ml, uint16_t* __restrict__ out, int Hkv, int BS, int64_t NB, int tile,
+    float scale_log2, int b, int kh, int64_t t_begin, int64_t t_end, int64_t Lc, int64_t prow,
+    float* __restrict__ pw, int lane) {
   using Geo = DecodeGeom<D>;
   constexpr int GP = G <= 4 ? 4 : 8;  // padded heads per token in the P slice
-  __shared__ __attribute__((aligned(16))) float p_lds[4][Geo::T * GP];
-
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int kh = blockIdx.z * (blockDim.x >> 6) + wave;
-  if (kh >= Hkv) return;
-  // sequence index fastest: workgroups are dealt round-robin to the 8 XCDs,
-  // so consecutive ids must not be the splits of one sequence (split s would
-  // always land on XCD s mod 8, and short contexts leave the high splits
-  // empty, i.e. whole XCDs idle)
-  const int b = blockIdx.x, split = blockIdx.y;
-  const int64_t Lc = min(ctx_lens[b], (int64_t)max_blocks * BS);
-  const int64_t chunk = (int64_t)bps * BS;
-  const int64_t t_begin = (int64_t)split * chunk;
-  const int64_t t_end = min(Lc, t_begin + chunk);
-  if (t_begin >= t_end) return;
   const int Hq = Hkv * G;
   const int64_t row = (int64_t)Hkv * D;
 
@@ -138,8 +129,6 @@ __global__ __launch_bounds__(256) void paged_decode_split(
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
-  float* pw = p_lds[wave];
-  const int32_t* btrow = bt + (int64_t)b * bt_stride;
 
   const int ntiles = (int)((t_end - t_begin + tile - 1) / tile);
   // tile i of the chunk: valid row count (0 for a skipped block) and the
@@ -318,46 +307,208 @@ __global__ __launch_bounds__(256) void paged_decode_split(
       }
     }
   } else {
-    const int64_t pbase = (int64_t)b * max_splits + split;
     if (ts == 0) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        float* dst = ws_o + (pbase * Hq + kh * G + g) * D + dc * 8;
+        float* dst = ws_o + (prow + g) * D + dc * 8;
         *reinterpret_cast<float4*>(dst) = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
         *reinterpret_cast<float4*>(dst + 4) = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
       }
     }
     if (lane < G) {
-      ws_ml[(pbase * Hq + kh * G + lane) * 2 + 0] = m_run;
-      ws_ml[(pbase * Hq + kh * G + lane) * 2 + 1] = l_run;
+      ws_ml[(prow + lane) * 2 + 0] = m_run;
+      ws_ml[(prow + lane) * 2 + 1] = l_run;
+    }
+  }
+}
+
+// Fixed chunks: one wave per (sequence, kv head, chunk of bps blocks), four
+// kv heads of one sequence and chunk per workgroup.  Grid x = (sequence,
+// kv-head group), group fastest; y = split.
+// Sequence before split: workgroups are dealt round-robin to the 8 XCDs,
+// so consecutive ids must not be the splits of one sequence (split s would
+// always land on XCD s mod 8, and short contexts leave the high splits
+// empty, i.e. whole XCDs idle).  Group fastest: the groups of one token
+// row (Hkv*D*2 bytes) are read at about the same time, not one half of
+// every row in the first half of the launch and the rest in the second
+// (cfg4, 2 groups: 1626 -> 1523 us).
+template <int D, int G>
+__global__ __launch_bounds__(256) void paged_decode_split(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, const int64_t* __restrict__ ctx_lens,
+    const int32_t* __restrict__ bt, int64_t bt_stride, float* __restrict__ ws_o,
+    float* __restrict__ ws_ml, uint16_t* __restrict__ out, int Hkv, int BS, int64_t NB,
+    int max_blocks, int bps, int tile, float scale_log2, int max_splits, int nz) {
+  using Geo = DecodeGeom<D>;
+  constexpr int GP = G <= 4 ? 4 : 8;
+  __shared__ __attribute__((aligned(16))) float p_lds[4][Geo::T * GP];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int kh = (int)(blockIdx.x % nz) * (blockDim.x >> 6) + wave;
+  if (kh >= Hkv) return;
+  const int b = (int)(blockIdx.x / nz), split = blockIdx.y;
+  const int64_t Lc = min(ctx_lens[b], (int64_t)max_blocks * BS);
+  const int64_t chunk = (int64_t)bps * BS;
+  const int64_t t_begin = (int64_t)split * chunk;
+  const int64_t t_end = min(Lc, t_begin + chunk);
+  if (t_begin >= t_end) return;
+  const int64_t prow = ((int64_t)b * max_splits + split) * (Hkv * G) + kh * G;
+  decode_chunk<D, G>(q, kc, vc, bt + (int64_t)b * bt_stride, ws_o, ws_ml, out, Hkv, BS, NB, tile,
+                     scale_log2, b, kh, t_begin, t_end, Lc, prow, p_lds[wave], lane);
+}
+
+// Balanced split: a fixed grid of nwg workgroups (wpg waves each, one kv
+// head per wave) shares the work evenly, whatever the context lengths.
+// Work units are (sequence b, kv-head group, tile) triples in that order,
+// n_b = ceil(L_b / tile) tiles per (sequence, group), where L_b is the
+// clamped context length; workgroup w takes the units [w*Ct, (w+1)*Ct),
+// Ct = ceil(total / nwg), and its waves walk the same tiles for the heads of
+// the group (so a workgroup reads wpg adjacent head slices of each row
+// together).  A (sequence, group) range that one workgroup covers entirely
+// is written out directly; otherwise workgroup w's partial of pair group
+// pg = b*ngroups + group is slot (w + pg)*wpg + wave -- unique, since along
+// the units both w and pg are non-decreasing and one of them grows at every
+// step from one (pg, w) overlap to the next.  Every workgroup scans the
+// per-sequence tile counts into LDS (B <= BAL_MAXB); workgroup 0 also
+// writes the scan (B+1 ints) to tp_out for the merge.
+constexpr int BAL_MAXB = 8192;
+
+__device__ __forceinline__ int decode_tiles(const int64_t* ctx_lens, int b, int64_t cap, int tile) {
+  const int64_t L = min(ctx_lens[b], cap);
+  return L > 0 ? (int)((L + tile - 1) / tile) : 0;
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(256) void paged_decode_balanced(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, const int64_t* __restrict__ ctx_lens,
+    const int32_t* __restrict__ bt, int64_t bt_stride, float* __restrict__ ws_o,
+    float* __restrict__ ws_ml, int* __restrict__ tp_out, uint16_t* __restrict__ out, int Hkv, int BS,
+    int64_t NB, int max_blocks, int B, int tile, float scale_log2, int ngroups) {
+  using Geo = DecodeGeom<D>;
+  constexpr int GP = G <= 4 ? 4 : 8;
+  __shared__ __attribute__((aligned(16))) float p_lds[4][Geo::T * GP];
+  __shared__ int tp[BAL_MAXB + 1];
+  __shared__ int wsum[4];
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int wave = tid >> 6, lane = tid & 63, wpg = nthr >> 6;
+  const int64_t cap = (int64_t)max_blocks * BS;
+
+  // ---- tp[b] = sum of n_b' for b' < b (each thread a run of sequences)
+  const int per = (B + nthr - 1) / nthr;
+  const int lo = min(B, tid * per), hi = min(B, lo + per);
+  int run = 0;
+  for (int i = lo; i < hi; ++i) {
+    run += decode_tiles(ctx_lens, i, cap, tile);
+    tp[i + 1] = run;
+  }
+  int incl = run;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int v = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += v;
+  }
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  int excl = incl - run;
+  for (int w = 0; w < wave; ++w) excl += wsum[w];
+  for (int i = lo; i < hi; ++i) tp[i + 1] += excl;
+  if (tid == 0) tp[0] = 0;
+  __syncthreads();
+  if (blockIdx.x == 0)
+    for (int i = tid; i <= B; i += nthr) tp_out[i] = tp[i];
+
+  const int64_t total = (int64_t)ngroups * tp[B];
+  const int nwg = gridDim.x;
+  const int64_t Ct = max((int64_t)1, (total + nwg - 1) / nwg);
+  int64_t u = (int64_t)blockIdx.x * Ct;
+  const int64_t u_end = min(total, u + Ct);
+  if (u >= u_end) return;
+  // first sequence: the largest b with ngroups * tp[b] <= u (it has n_b > 0)
+  int b_lo = 0, b_hi = B - 1;
+  while (b_lo < b_hi) {
+    const int mid = (b_lo + b_hi + 1) >> 1;
+    if ((int64_t)ngroups * tp[mid] <= u) b_lo = mid;
+    else b_hi = mid - 1;
+  }
+  int b = b_lo;
+  float* pw = p_lds[wave];
+  while (u < u_end) {
+    const int nb = tp[b + 1] - tp[b];
+    const int64_t base = (int64_t)ngroups * tp[b];
+    const int grp = (int)((u - base) / nb);
+    const int64_t i0 = (u - base) - (int64_t)grp * nb;
+    const int64_t seg_end = min(u_end, base + (int64_t)(grp + 1) * nb);
+    const int kh = grp * wpg + wave;
+    if (kh < Hkv) {
+      const int64_t Lc = min(ctx_lens[b], cap);
+      const int64_t t_begin = i0 * tile;
+      const int64_t t_end = min(Lc, (i0 + (seg_end - u)) * tile);
+      const int64_t slot = ((int64_t)blockIdx.x + (int64_t)b * ngroups + grp) * wpg + wave;
+      decode_chunk<D, G>(q, kc, vc, bt + (int64_t)b * bt_stride, ws_o, ws_ml, out, Hkv, BS, NB, tile,
+                         scale_log2, b, kh, t_begin, t_end, Lc, slot * G, pw, lane);
+    }
+    u = seg_end;
+    if (u >= base + (int64_t)ngroups * nb) {
+      ++b;
+      while (b < B && tp[b + 1] == tp[b]) ++b;  // sequences with no context
     }
   }
 }
 
 // ------------------------------------------------------------ decode merge --
-// One workgroup per (head, sequence), one lane per head dim.  Sequences whose
-// context fits one chunk were finished by the split kernel; padding rows
-// (context 0) get zeros.
+// Where the partials of (sequence b, query head h) live: ns of them, the
+// s-th at workspace row r0 + s * rstep (o at ws_o[row * D], (m, l) at
+// ws_ml[row * 2]).  ns == 1: the split kernel wrote the output itself;
+// ns == 0: no context.
+struct PartMap {
+  int bps, max_splits;  // fixed chunks of bps blocks (bps > 0)
+  const int* tp;        // balanced split (bps == 0): tile-count scan, B + 1 ints
+  int tile, ngroups, wpg, G, nwg, B;
+};
+
+__device__ __forceinline__ int part_span(const PartMap& pm, int b, int h, int Hq, int64_t Lc, int BS,
+                                         int64_t& r0, int64_t& rstep) {
+  if (pm.bps > 0) {
+    const int64_t chunk = (int64_t)pm.bps * BS;
+    r0 = (int64_t)b * pm.max_splits * Hq + h;
+    rstep = Hq;
+    return Lc > 0 ? (int)((Lc + chunk - 1) / chunk) : 0;
+  }
+  r0 = 0;
+  rstep = (int64_t)pm.wpg * pm.G;
+  const int nb = pm.tp[b + 1] - pm.tp[b];
+  if (nb == 0) return 0;
+  const int kh = h / pm.G, g = h - kh * pm.G;
+  const int grp = kh / pm.wpg, wv = kh - grp * pm.wpg;
+  const int64_t total = (int64_t)pm.ngroups * pm.tp[pm.B];
+  const int64_t Ct = max((int64_t)1, (total + pm.nwg - 1) / pm.nwg);
+  const int64_t start = (int64_t)pm.ngroups * pm.tp[b] + (int64_t)grp * nb;
+  const int64_t wf = start / Ct, wl = (start + nb - 1) / Ct;
+  r0 = ((wf + (int64_t)b * pm.ngroups + grp) * pm.wpg + wv) * pm.G + g;
+  return (int)(wl - wf + 1);
+}
+
+// One workgroup per (head, sequence), one lane per head dim.
 __global__ __launch_bounds__(128) void paged_decode_merge(
     const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
     const int64_t* __restrict__ ctx_lens, uint16_t* __restrict__ out, int Hq, int D, int BS,
-    int max_blocks, int bps, int max_splits) {
+    int max_blocks, PartMap pm) {
   const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
   const int64_t Lc = min(ctx_lens[b], (int64_t)max_blocks * BS);
-  const int64_t chunk = (int64_t)bps * BS;
-  const int ns = (int)((Lc + chunk - 1) / chunk);
+  int64_t r0, rs;
+  const int ns = part_span(pm, b, h, Hq, Lc, BS, r0, rs);
   if (ns == 1 || d >= D) return;
   float res = 0.f;
   if (ns > 1) {
-    const int64_t pbase = (int64_t)b * max_splits;
     float M = -INFINITY;
-    for (int s = 0; s < ns; ++s) M = fmaxf(M, ws_ml[((pbase + s) * Hq + h) * 2]);
+    for (int s = 0; s < ns; ++s) M = fmaxf(M, ws_ml[(r0 + s * rs) * 2]);
     float num = 0.f, den = 0.f;
     if (M != -INFINITY) {
       for (int s = 0; s < ns; ++s) {
-        const float w = exp2f(ws_ml[((pbase + s) * Hq + h) * 2] - M);
-        den = fmaf(w, ws_ml[((pbase + s) * Hq + h) * 2 + 1], den);
-        num = fmaf(w, ws_o[((pbase + s) * Hq + h) * D + d], num);
+        const int64_t r = r0 + s * rs;
+        const float w = exp2f(ws_ml[r * 2] - M);
+        den = fmaf(w, ws_ml[r * 2 + 1], den);
+        num = fmaf(w, ws_o[r * D + d], num);
       }
     }
     res = den > 0.f ? num / den : 0.f;
@@ -367,9 +518,10 @@ __global__ __launch_bounds__(128) void paged_decode_merge(
 
 // Phase 2 fused with the output projection's act_quant: one workgroup per
 // sequence merges every head (or re-reads the rows the split kernel wrote
-// for a single-chunk context; zeros for context 0), writes the bf16 output,
-// and quantises the row per 128-value group with act_quant's formula and
-// rounding (the codes equal act_quant of the bf16 output bit for bit).
+// for a head whose context one chunk covered; zeros for context 0), writes
+// the bf16 output, and quantises the row per 128-value group with
+// act_quant's formula and rounding (the codes equal act_quant of the bf16
+// output bit for bit).
 constexpr int MQ_MAXE = 8192;  // Hq * D per sequence
 constexpr int MQ_MAXH = 128;
 constexpr int MQ_MAXW = 4096;  // (split, head) weights staged in LDS
@@ -377,34 +529,52 @@ constexpr int MQ_MAXW = 4096;  // (split, head) weights staged in LDS
 __global__ __launch_bounds__(256) void paged_decode_merge_quant(
     const float* __restrict__ ws_o, const float* __restrict__ ws_ml, const int64_t* __restrict__ ctx_lens,
     uint16_t* __restrict__ out, uint8_t* __restrict__ qo, float* __restrict__ qs, int Hq, int D, int BS,
-    int max_blocks, int bps, int max_splits) {
+    int max_blocks, PartMap pm) {
   __shared__ float hDen[MQ_MAXH];
-  __shared__ float wts[MQ_MAXW];  // [split][head]: exp2(m - M_head), then the per-head sums
+  __shared__ int hNs[MQ_MAXH];
+  __shared__ int64_t hR0[MQ_MAXH];
+  __shared__ int s_nsmax;
+  __shared__ float wts[MQ_MAXW];  // [split][head]: m, then exp2(m - M_head)
   __shared__ __attribute__((aligned(16))) uint16_t vals[MQ_MAXE];
   const int b = blockIdx.x, tid = threadIdx.x;
   const int64_t Lc = min(ctx_lens[b], (int64_t)max_blocks * BS);
-  const int64_t chunk = (int64_t)bps * BS;
-  const int ns = (int)((Lc + chunk - 1) / chunk);
   const int E = Hq * D;
   uint16_t* orow = out + (int64_t)b * E;
-  if (ns > 1) {
-    const int64_t pbase = (int64_t)b * max_splits;
+  if (tid == 0) s_nsmax = 0;
+  __syncthreads();
+  int64_t rs = 0;
+  for (int h = tid; h < Hq; h += 256) {
+    int64_t r0;
+    const int ns = part_span(pm, b, h, Hq, Lc, BS, r0, rs);
+    hNs[h] = ns;
+    hR0[h] = r0;
+    atomicMax(&s_nsmax, ns);
+  }
+  rs = pm.bps > 0 ? (int64_t)Hq : (int64_t)pm.wpg * pm.G;
+  __syncthreads();
+  const int nsmax = s_nsmax;
+  if (nsmax > 1) {
     // (m, l) of every (split, head) in one parallel step; the per-head max,
     // weights and denominators from LDS (the unfused merge's arithmetic)
-    const bool staged = ns * Hq <= MQ_MAXW;
+    const bool staged = nsmax * Hq <= MQ_MAXW;
     if (staged) {
-      for (int x = tid; x < ns * Hq; x += 256) wts[x] = ws_ml[(pbase * Hq + x) * 2];
+      for (int x = tid; x < nsmax * Hq; x += 256) {
+        const int sp = x / Hq, h = x - sp * Hq;
+        wts[x] = sp < hNs[h] ? ws_ml[(hR0[h] + sp * rs) * 2] : -INFINITY;
+      }
       __syncthreads();
     }
-    auto mval = [&](int sp, int h) -> float { return staged ? wts[sp * Hq + h] : ws_ml[((pbase + sp) * Hq + h) * 2]; };
+    auto mval = [&](int sp, int h) -> float { return staged ? wts[sp * Hq + h] : ws_ml[(hR0[h] + sp * rs) * 2]; };
     for (int h = tid; h < Hq; h += 256) {
+      const int ns = hNs[h];
+      if (ns <= 1) continue;
       float M = -INFINITY;
       for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, mval(sp, h));
       float den = 0.f;
       if (M != -INFINITY)
         for (int sp = 0; sp < ns; ++sp) {
           const float w = exp2f(mval(sp, h) - M);
-          den = fmaf(w, ws_ml[((pbase + sp) * Hq + h) * 2 + 1], den);
+          den = fmaf(w, ws_ml[(hR0[h] + sp * rs) * 2 + 1], den);
           if (staged) wts[sp * Hq + h] = w;  // this thread alone reads / writes head h's entries
         }
       else if (staged)
@@ -414,22 +584,30 @@ __global__ __launch_bounds__(256) void paged_decode_merge_quant(
     __syncthreads();
     for (int e = tid; e < E; e += 256) {
       const int h = e / D, d = e - h * D;
-      const float den = hDen[h];
-      float num = 0.f;
-      if (staged) {
-        for (int sp = 0; sp < ns; ++sp) num = fmaf(wts[sp * Hq + h], ws_o[((pbase + sp) * Hq + h) * D + d], num);
-      } else {
-        float M = -INFINITY;
-        for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, mval(sp, h));
-        if (M != -INFINITY)
-          for (int sp = 0; sp < ns; ++sp)
-            num = fmaf(exp2f(mval(sp, h) - M), ws_o[((pbase + sp) * Hq + h) * D + d], num);
+      const int ns = hNs[h];
+      if (ns == 1) {  // written by the split kernel
+        vals[e] = orow[e];
+        continue;
+      }
+      float num = 0.f, den = 0.f;
+      if (ns > 1) {
+        den = hDen[h];
+        const int64_t r0 = hR0[h];
+        if (staged) {
+          for (int sp = 0; sp < ns; ++sp) num = fmaf(wts[sp * Hq + h], ws_o[(r0 + sp * rs) * D + d], num);
+        } else {
+          float M = -INFINITY;
+          for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, mval(sp, h));
+          if (M != -INFINITY)
+            for (int sp = 0; sp < ns; ++sp)
+              num = fmaf(exp2f(mval(sp, h) - M), ws_o[(r0 + sp * rs) * D + d], num);
+        }
       }
       const uint16_t v = (uint16_t)f32_to_bf16(den > 0.f ? num / den : 0.f);
       orow[e] = v;
       vals[e] = v;
     }
-  } else if (ns == 1) {
+  } else if (nsmax == 1) {
     for (int e = tid; e < E; e += 256) vals[e] = orow[e];  // written by the split kernel
   } else {
     for (int e = tid; e < E; e += 256) {
@@ -458,8 +636,61 @@ void launch_split(dim3 grid, dim3 block, hipStream_t st, const uint16_t* q, cons
                   const uint16_t* vc, const int64_t* cl, const int32_t* bt, int64_t bts, float* wo,
                   float* wml, uint16_t* out, int Hkv, int BS, int64_t NB, int max_blocks, int bps,
                   int tile, float sl2, int max_splits) {
-  hipLaunchKernelGGL((paged_decode_split<D, G>), grid, block, 0, st, q, kc, vc, cl, bt, bts, wo, wml,
-                     out, Hkv, BS, NB, max_blocks, bps, tile, sl2, max_splits);
+  // grid = (sequence, split, kv-head group) on input; launched with the
+  // group folded into x, fastest
+  const int nz = (int)grid.z;
+  hipLaunchKernelGGL((paged_decode_split<D, G>), dim3(grid.x * grid.z, grid.y, 1), block, 0, st, q, kc, vc, cl,
+                     bt, bts, wo, wml, out, Hkv, BS, NB, max_blocks, bps, tile, sl2, max_splits, nz);
+}
+
+template <int D, int G>
+void launch_balanced(unsigned nwg, dim3 block, hipStream_t st, const uint16_t* q, const uint16_t* kc,
+                     const uint16_t* vc, const int64_t* cl, const int32_t* bt, int64_t bts, float* wo,
+                     float* wml, int* tp, uint16_t* out, int Hkv, int BS, int64_t NB, int max_blocks, int B,
+                     int tile, float sl2, int ngroups) {
+  hipLaunchKernelGGL((paged_decode_balanced<D, G>), dim3(nwg), block, 0, st, q, kc, vc, cl, bt, bts, wo, wml,
+                     tp, out, Hkv, BS, NB, max_blocks, B, tile, sl2, ngroups);
+}
+
+template <int D>
+bool dispatch_balanced(int G, unsigned nwg, dim3 block, hipStream_t st, const uint16_t* q,
+                       const uint16_t* kc, const uint16_t* vc, const int64_t* cl, const int32_t* bt,
+                       int64_t bts, float* wo, float* wml, int* tp, uint16_t* out, int Hkv, int BS,
+                       int64_t NB, int max_blocks, int B, int tile, float sl2, int ngroups) {
+#define LFS_G(GG) \
+  case GG: launch_balanced<D, GG>(nwg, block, st, q, kc, vc, cl, bt, bts, wo, wml, tp, out, Hkv, BS, NB, max_blocks, B, tile, sl2, ngroups); return true;
+  switch (G) {
+    LFS_G(1) LFS_G(2) LFS_G(3) LFS_G(4) LFS_G(5) LFS_G(6) LFS_G(7) LFS_G(8)
+    default: return false;
+  }
+#undef LFS_G
+}
+
+// compute units of the current device (the balanced split's grid)
+int decode_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// balanced split geometry: wpg waves (kv heads) per workgroup, ngroups
+// groups, nwg workgroups -- eight waves per CU (two per SIMD, the kernel's
+// occupancy), one round
+struct BalancedGeom {
+  int wpg, ngroups, nwg;
+};
+BalancedGeom balanced_geom(int Hkv) {
+  BalancedGeom g;
+  g.wpg = Hkv < 4 ? Hkv : 4;
+  g.ngroups = (Hkv + g.wpg - 1) / g.wpg;
+  g.nwg = decode_cu_count() * (8 / g.wpg);
+  return g;
 }
 
 template <int D>
@@ -480,6 +711,12 @@ bool dispatch_g(int G, dim3 grid, dim3 block, hipStream_t st, const uint16_t* q,
 }  // namespace lfs
 
 using namespace lfs;
+
+namespace {
+int paged_decode_merge_launch(float* ws_o, float* ws_ml, const int64_t* context_lens, void* out, void* q_out,
+                              float* q_scale, int64_t B, int Hq, int D, int BS, int max_blocks, const PartMap& pm,
+                              hipStream_t st);
+}
 
 extern "C" int lfs_store_kvcache(const void* key, int64_t k_stride_t, const void* value,
                                  int64_t v_stride_t, void* k_cache, void* v_cache,
@@ -509,8 +746,13 @@ extern "C" int lfs_store_kvcache(const void* key, int64_t k_stride_t, const void
 extern "C" int64_t lfs_paged_decode_workspace_bytes(int64_t B, int32_t num_q_heads,
                                                     int32_t head_dim, int32_t max_blocks,
                                                     int32_t blocks_per_split) {
-  if (B < 0 || num_q_heads <= 0 || head_dim <= 0 || max_blocks < 0 || blocks_per_split <= 0)
-    return -1;
+  if (B < 0 || num_q_heads <= 0 || head_dim <= 0 || max_blocks < 0 || blocks_per_split < 0) return -1;
+  if (blocks_per_split == 0) {
+    // balanced split: partial rows (nwg + B*ngroups)*wpg*G <= (8*CUs + 2*B)*Hq
+    // (wpg*G <= Hq, nwg*wpg <= 8*CUs, ngroups*wpg < 2*Hkv), then B+1 ints
+    const int64_t rows = (8 * (int64_t)decode_cu_count() + 2 * B) * num_q_heads;
+    return 4 * rows * ((int64_t)head_dim + 2) + 4 * (B + 1);
+  }
   const int64_t splits = ((int64_t)max_blocks + blocks_per_split - 1) / blocks_per_split;
   return 4 * B * splits * (int64_t)num_q_heads * ((int64_t)head_dim + 2);
 }
@@ -529,7 +771,9 @@ extern "C" int lfs_paged_decode(const void* q, const void* k_cache, const void* 
   LFS_REQUIRE(Hq % Hkv == 0 && Hq / Hkv <= 8,
               "paged_decode: num_q_heads (%d) must be a multiple of num_kv_heads (%d), ratio <= 8", Hq, Hkv);
   LFS_REQUIRE(BS % 16 == 0, "paged_decode: block_size must be a multiple of 16 (got %d)", BS);
-  LFS_REQUIRE(blocks_per_split > 0, "paged_decode: blocks_per_split must be positive");
+  LFS_REQUIRE(blocks_per_split >= 0, "paged_decode: blocks_per_split must be >= 0 (0: balanced split)");
+  LFS_REQUIRE(blocks_per_split > 0 || B <= BAL_MAXB, "paged_decode: the balanced split (blocks_per_split 0) needs B <= %d",
+              BAL_MAXB);
   LFS_REQUIRE(bt_stride >= max_blocks, "paged_decode: block table stride < max_blocks");
   LFS_REQUIRE(num_blocks >= 1 || max_blocks == 0, "paged_decode: empty KV pool");
   if (B == 0) return 0;
@@ -545,21 +789,49 @@ extern "C" int lfs_paged_decode(const void* q, const void* k_cache, const void* 
   LFS_REQUIRE(workspace_bytes >= need && (need == 0 || workspace),
               "paged_decode: workspace of %lld bytes < required %lld", (long long)workspace_bytes,
               (long long)need);
-  const int max_splits = (max_blocks + blocks_per_split - 1) / blocks_per_split;
-  float* ws_o = (float*)workspace;
-  float* ws_ml = ws_o + (size_t)B * max_splits * Hq * D;
   hipStream_t st = (hipStream_t)stream;
   const int Tmax = D == 64 ? 64 : 32;
   int tile = 16;
   for (int t = Tmax; t >= 16; t >>= 1)
     if (BS % t == 0) { tile = t; break; }
   const float sl2 = scale * 1.4426950408889634f;
+  const int G = Hq / Hkv;
+  PartMap pm{};
+  if (blocks_per_split == 0) {
+    const BalancedGeom bg = balanced_geom(Hkv);
+    const int64_t rows = ((int64_t)bg.nwg + B * bg.ngroups) * bg.wpg * G;
+    LFS_REQUIRE((int64_t)bg.ngroups * B * (((int64_t)max_blocks * BS + tile - 1) / tile) < (1ll << 31),
+                "paged_decode: too many context tiles for the balanced split");
+    float* ws_o = (float*)workspace;
+    float* ws_ml = ws_o + rows * D;
+    int* tp = (int*)(ws_ml + rows * 2);
+    pm = PartMap{0, 0, tp, tile, bg.ngroups, bg.wpg, G, bg.nwg, (int)B};
+    {  // launched also when max_blocks == 0: it then writes the all-zero scan the merge reads
+      const bool ok = D == 64
+          ? dispatch_balanced<64>(G, (unsigned)bg.nwg, dim3(64 * bg.wpg), st, (const uint16_t*)q,
+                                  (const uint16_t*)k_cache, (const uint16_t*)v_cache, context_lens, block_tables,
+                                  bt_stride, ws_o, ws_ml, tp, (uint16_t*)out, Hkv, BS, num_blocks, max_blocks,
+                                  (int)B, tile, sl2, bg.ngroups)
+          : dispatch_balanced<128>(G, (unsigned)bg.nwg, dim3(64 * bg.wpg), st, (const uint16_t*)q,
+                                   (const uint16_t*)k_cache, (const uint16_t*)v_cache, context_lens,
+                                   block_tables, bt_stride, ws_o, ws_ml, tp, (uint16_t*)out, Hkv, BS,
+                                   num_blocks, max_blocks, (int)B, tile, sl2, bg.ngroups);
+      LFS_REQUIRE(ok, "paged_decode: unsupported group size %d", G);
+      const int rc = check_launch("paged_decode(balanced split)");
+      if (rc) return rc;
+    }
+    return paged_decode_merge_launch(ws_o, ws_ml, context_lens, out, q_out, q_scale, B, Hq, D, BS, max_blocks, pm, st);
+  }
+  const int max_splits = (max_blocks + blocks_per_split - 1) / blocks_per_split;
+  float* ws_o = (float*)workspace;
+  float* ws_ml = ws_o + (size_t)B * max_splits * Hq * D;
+  pm = PartMap{blocks_per_split, max_splits, nullptr, tile, 0, 0, G, 0, (int)B};
   if (max_splits > 0) {
     const int wpg = Hkv < 4 ? Hkv : 4;  // waves (kv heads) per workgroup
     const dim3 grid((unsigned)B, (unsigned)max_splits, (unsigned)((Hkv + wpg - 1) / wpg));
-    LFS_REQUIRE(grid.z < 65536u && grid.y < 65536u, "paged_decode: too many kv heads or splits");
+    LFS_REQUIRE(grid.z < 65536u && grid.y < 65536u && (int64_t)grid.x * grid.z < (1ll << 31),
+                "paged_decode: too many kv heads or splits");
     const dim3 block((unsigned)(64 * wpg));
-    const int G = Hq / Hkv;
     const bool ok = D == 64
         ? dispatch_g<64>(G, grid, block, st, (const uint16_t*)q, (const uint16_t*)k_cache,
                          (const uint16_t*)v_cache, context_lens, block_tables, bt_stride, ws_o,
@@ -573,14 +845,20 @@ extern "C" int lfs_paged_decode(const void* q, const void* k_cache, const void* 
     const int rc = check_launch("paged_decode(split)");
     if (rc) return rc;
   }
+  return paged_decode_merge_launch(ws_o, ws_ml, context_lens, out, q_out, q_scale, B, Hq, D, BS, max_blocks, pm, st);
+}
+
+namespace {
+int paged_decode_merge_launch(float* ws_o, float* ws_ml, const int64_t* context_lens, void* out, void* q_out,
+                              float* q_scale, int64_t B, int Hq, int D, int BS, int max_blocks, const PartMap& pm,
+                              hipStream_t st) {
   if (q_out != nullptr) {
     hipLaunchKernelGGL(paged_decode_merge_quant, dim3((unsigned)B), dim3(256), 0, st, ws_o, ws_ml, context_lens,
-                       (uint16_t*)out, (uint8_t*)q_out, q_scale, Hq, D, BS, max_blocks, blocks_per_split,
-                       max_splits);
+                       (uint16_t*)out, (uint8_t*)q_out, q_scale, Hq, D, BS, max_blocks, pm);
     return check_launch("paged_decode(merge + quant)");
   }
   hipLaunchKernelGGL(paged_decode_merge, dim3((unsigned)Hq, (unsigned)B), dim3((unsigned)D), 0, st,
-                     ws_o, ws_ml, context_lens, (uint16_t*)out, Hq, D, BS, max_blocks,
-                     blocks_per_split, max_splits);
+                     ws_o, ws_ml, context_lens, (uint16_t*)out, Hq, D, BS, max_blocks, pm);
   return check_launch("paged_decode(merge)");
 }
+}  // namespace

@@ -241,16 +241,34 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
     _lib.check(rc, "store_kvcache")
 
 
-def default_blocks_per_split(batch: int, num_kv_heads: int, max_blocks: int, block_size: int) -> int:
-    """KV blocks per split-K chunk (shapes only, so the choice is capturable).
+BALANCED_MAX_BATCH = 8192  # the balanced split scans the batch's tile counts in LDS
 
-    The kernel runs one wave per (sequence, kv head, chunk).  Chunks of 256
-    tokens keep the most waves in flight, which is what HBM streaming needs
-    once there are enough (sequence, kv head) pairs (>= 1024); with fewer
-    pairs, 512-token chunks halve the merge work.  Measured on MI355X: cfg4
-    (2048 pairs) is fastest at 256 tokens, cfg3 (256 pairs) at 512."""
+
+def default_blocks_per_split(batch: int, num_kv_heads: int, max_blocks: int, block_size: int) -> int:
+    """Split of the decode context (shapes only, so the choice is capturable).
+
+    0 selects the balanced split: a fixed grid of two 4-wave workgroups per
+    CU, each taking an equal share of the (sequence, kv-head group, tile)
+    work, whatever the context lengths.  Measured on MI355X: cfg4 (B 256,
+    lengths log-uniform to 32k) 1188 us against 1523 us for the best fixed
+    chunking; cfg3 49.6 us against 49.7 us.
+
+    Above BALANCED_MAX_BATCH sequences, fixed chunks of the returned number
+    of blocks, one wave per (sequence, kv head, chunk): with fewer than 1024
+    (sequence, kv head) pairs 512-token chunks (cfg3: 49 us against 66 us at
+    256 tokens); with more, chunks grow until the grid has at most 32768
+    potential waves (cfg4: 2000 / 1826 / 1683 / 1634 us at 1 / 2 / 4 / 8
+    blocks per chunk)."""
+    if batch <= BALANCED_MAX_BATCH:
+        return 0
     base = max(1, 256 // max(block_size, 1))
-    bps = base if batch * num_kv_heads >= 1024 else 2 * base
+    pairs = batch * num_kv_heads
+    if pairs < 1024:
+        bps = 2 * base
+    else:
+        bps = base
+        while pairs * -(-max_blocks // bps) > 32768 and bps < max_blocks:
+            bps *= 2
     return max(1, min(bps, max(max_blocks, 1)))
 
 
@@ -270,10 +288,12 @@ def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     context_lens int64 [B] (0 = padding row, output zeros); block_tables
     int32 [B, max_blocks] padded with -1.  scale defaults to 1/sqrt(D) as
     SDPA (model/attention/GQA.py:130).  Returns bf16 [B, Hq, D].
-    The grid depends only on B and max_blocks, so the call can be captured
-    in a HIP graph (pass a preallocated ``workspace`` of
-    ``paged_decode_workspace_bytes`` bytes to keep the capture free of
-    allocations).  With ``quant`` the merge also quantises each output row
+    ``blocks_per_split`` 0 (the default up to BALANCED_MAX_BATCH sequences)
+    shares the context tiles evenly over a fixed grid; n > 0 splits every
+    context into chunks of n blocks.  Either way the grid depends only on
+    the shapes, so the call can be captured in a HIP graph (pass a
+    preallocated ``workspace`` of ``paged_decode_workspace_bytes`` bytes to
+    keep the capture free of allocations).  With ``quant`` the merge also quantises each output row
     for the next FP8 linear and the call returns (o, codes e4m3fn
     [B, Hq*D], scales fp32 [B, Hq*D/128]), the codes equal to
     act_quant(o.view(B, -1)) bit for bit.
@@ -295,7 +315,7 @@ def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     max_blocks = block_tables.size(1)
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    bps = blocks_per_split or default_blocks_per_split(B, Hkv, max_blocks, BS)
+    bps = default_blocks_per_split(B, Hkv, max_blocks, BS) if blocks_per_split is None else blocks_per_split
     need = paged_decode_workspace_bytes(B, Hq, D, max_blocks, bps)
     if workspace is None:
         workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=q.device)

@@ -53,6 +53,10 @@ def test_argument_errors_are_reported_without_launch(lib):
     rc = lib.lfs_paged_decode(16, 16, 16, 16, 16, 4, 16, 16, 1 << 20, 2, 12, 4, 64, 256, 8, 4,
                               0.1, 1, 16, None, None)
     assert rc == -1 and b"go together" in lib.lfs_last_error()
+    # the balanced split (blocks_per_split 0) is limited to 8192 sequences
+    rc = lib.lfs_paged_decode(16, 16, 16, 16, 16, 4, 16, 16, 1 << 20, 8193, 12, 4, 64, 256, 8, 4,
+                              0.1, 0, None, None, None)
+    assert rc == -1 and b"balanced split" in lib.lfs_last_error()
     with pytest.raises(ValueError, match="block_size"):
         _lib.check(lib.lfs_weight_quant(None, None, None, 8, 8, 7, None), "weight_quant")
     # split-K needs its workspace (non-null dummy pointers: the check comes first)
@@ -122,4 +126,8 @@ def test_workspace_bytes(lib):
     # 4 bytes * B * splits * Hq * (D + 2)
     assert lib.lfs_paged_decode_workspace_bytes(64, 16, 64, 16, 1) == 4 * 64 * 16 * 16 * 66
     assert lib.lfs_paged_decode_workspace_bytes(3, 8, 128, 10, 4) == 4 * 3 * 3 * 8 * 130
-    assert lib.lfs_paged_decode_workspace_bytes(3, 8, 128, 10, 0) == -1
+    assert lib.lfs_paged_decode_workspace_bytes(3, 8, 128, 10, -1) == -1
+    # balanced split (0): (8 * CUs + 2 * B) * Hq partial rows of D + 2 floats, then B + 1 ints
+    v = lib.lfs_paged_decode_workspace_bytes(3, 8, 128, 10, 0)
+    rows, rem = divmod(v - 4 * 4, 4 * 8 * 130)
+    assert rem == 0 and rows - 6 > 0 and (rows - 6) % 8 == 0

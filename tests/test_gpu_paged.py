@@ -134,7 +134,7 @@ def test_paged_decode_split_independence():
     case = W.paged_case("cfg3", seed=5, batch=12)
     kc, vc = W.fill_pool(case, seed=5, device=DEV)
     q = make_q(case, 5)
-    outs = [run_decode(case, kc, vc, q, bps).float() for bps in (1, 2, 3, 16)]
+    outs = [run_decode(case, kc, vc, q, bps).float() for bps in (0, 1, 2, 3, 16)]
     for o in outs[1:]:
         assert_close(o.cpu().numpy(), outs[0].cpu().numpy(), "split")
 
@@ -191,7 +191,7 @@ def test_paged_decode_fused_quant_equals_act_quant(Hq, Hkv, D, BS):
     vc = torch.randn(NB, BS, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
     q = torch.randn(B, Hq, D, generator=g, device=DEV).to(torch.bfloat16)
     cl, btd = torch.from_numpy(lens).to(DEV), torch.from_numpy(bt).to(DEV)
-    for bps in (1, 2):  # chunks of one block: several chunks per row
+    for bps in (0, 1, 2):  # balanced (7 rows over the whole grid), chunks of one and two blocks
         o, oq, os_ = K.paged_attention_decode(q, kc, vc, cl, btd, blocks_per_split=bps, quant=True)
         plain = K.paged_attention_decode(q, kc, vc, cl, btd, blocks_per_split=bps)
         assert torch.equal(o, plain)
@@ -199,6 +199,93 @@ def test_paged_decode_fused_quant_equals_act_quant(Hq, Hkv, D, BS):
         assert torch.equal(oq.view(torch.uint8), rq.view(torch.uint8)), f"codes bps={bps}"
         assert torch.equal(os_, rs), f"scales bps={bps}"
         assert bool((o[1] == 0).all())  # padding row
+
+
+def _short_sequences(B, BS, max_len, seed):
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(0, max_len + 1, B).astype(np.int64)
+    lens[::7] = 0  # padding rows between live ones
+    nblk = -(-lens // BS)
+    NB = int(nblk.sum()) + 1
+    maxb = int(nblk.max()) + 1
+    perm = rng.permutation(NB)
+    bt = np.full((B, maxb), -1, np.int32)
+    pos = 0
+    for b in range(B):
+        bt[b, :nblk[b]] = perm[pos:pos + nblk[b]]
+        pos += int(nblk[b])
+    return lens, bt, NB
+
+
+def test_paged_decode_balanced_many_short_sequences():
+    """Balanced split with many more sequences than threads of a workgroup
+    (the per-thread runs of the tile-count scan) and workgroups that cover
+    several whole sequences plus pieces of their neighbours: every row is
+    within tolerance of the oracle, padding rows are zero, and the fused
+    act_quant codes equal act_quant of the output."""
+    B, Hq, Hkv, D, BS = 2000, 8, 2, 64, 16
+    lens, bt, NB = _short_sequences(B, BS, 90, seed=21)
+    g = torch.Generator(device=DEV).manual_seed(21)
+    kc = torch.randn(NB, BS, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
+    vc = torch.randn(NB, BS, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
+    q = torch.randn(B, Hq, D, generator=g, device=DEV).to(torch.bfloat16)
+    cl, btd = torch.from_numpy(lens).to(DEV), torch.from_numpy(bt).to(DEV)
+    assert K.default_blocks_per_split(B, Hkv, bt.shape[1], BS) == 0
+    o, oq, os_ = K.paged_attention_decode(q, kc, vc, cl, btd, quant=True)
+    plain = K.paged_attention_decode(q, kc, vc, cl, btd)
+    torch.cuda.synchronize()
+    assert torch.equal(o, plain)
+    ref = P.paged_decode(q.float().cpu().numpy(), kc.float().cpu().numpy(), vc.float().cpu().numpy(),
+                         lens, bt, 1 / math.sqrt(D))
+    got = o.float().cpu().numpy()
+    assert_close(got, ref, "balanced, 2000 short sequences")
+    assert np.all(got[lens == 0] == 0)
+    rq, rs = K.act_quant(o.view(B, -1))
+    assert torch.equal(oq.view(torch.uint8), rq.view(torch.uint8))
+    assert torch.equal(os_, rs)
+
+
+def test_paged_decode_large_batch_falls_back_to_fixed_chunks():
+    """Above BALANCED_MAX_BATCH sequences the default is fixed chunks, and an
+    explicit balanced request is refused rather than run."""
+    B, Hq, Hkv, D, BS = K.BALANCED_MAX_BATCH + 8, 4, 1, 64, 16
+    lens, bt, NB = _short_sequences(B, BS, 20, seed=22)
+    g = torch.Generator(device=DEV).manual_seed(22)
+    kc = torch.randn(NB, BS, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
+    vc = torch.randn(NB, BS, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
+    q = torch.randn(B, Hq, D, generator=g, device=DEV).to(torch.bfloat16)
+    cl, btd = torch.from_numpy(lens).to(DEV), torch.from_numpy(bt).to(DEV)
+    assert K.default_blocks_per_split(B, Hkv, bt.shape[1], BS) > 0
+    o = K.paged_attention_decode(q, kc, vc, cl, btd)
+    torch.cuda.synchronize()
+    ref = P.paged_decode(q.float().cpu().numpy(), kc.float().cpu().numpy(), vc.float().cpu().numpy(),
+                         lens, bt, 1 / math.sqrt(D))
+    assert_close(o.float().cpu().numpy(), ref, "fixed chunks, large batch")
+    with pytest.raises(Exception, match="balanced split"):
+        K.paged_attention_decode(q, kc, vc, cl, btd, blocks_per_split=0)
+
+
+def test_paged_decode_balanced_workspace_bound():
+    """The balanced split's partial rows stay inside the byte count that
+    paged_decode_workspace_bytes promises: a workspace of exactly that size,
+    guarded by NaN-filled canaries on both sides, is enough and the canaries
+    survive (cfg4 geometry, the largest partial count per call)."""
+    case = W.paged_case("cfg4", seed=3, batch=48)
+    kc, vc = W.fill_pool(case, seed=3, device=DEV, only_referenced=True)
+    q = make_q(case, 4)
+    cl = torch.from_numpy(case.context_lens).to(DEV)
+    bt = torch.from_numpy(case.block_tables).to(DEV)
+    need = K.paged_decode_workspace_bytes(case.batch, case.num_q_heads, case.head_dim, bt.shape[1], 0)
+    guard = 4096
+    buf = torch.full((need + 2 * guard,), 0xFF, dtype=torch.uint8, device=DEV)
+    ws = buf[guard:guard + need]
+    o = K.paged_attention_decode(q, kc, vc, cl, bt, case.scale, 0, ws)
+    ref = K.paged_attention_decode(q, kc, vc, cl, bt, case.scale, 8)
+    torch.cuda.synchronize()
+    assert bool((buf[:guard] == 0xFF).all()) and bool((buf[guard + need:] == 0xFF).all())
+    assert_close(o.float().cpu().numpy(), ref.float().cpu().numpy(), "balanced vs fixed chunks")
+    del kc, vc
+    torch.cuda.empty_cache()
 
 
 def test_decode_step_store_then_attend():
