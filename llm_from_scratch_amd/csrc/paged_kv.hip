@@ -357,7 +357,8 @@ __global__ __launch_bounds__(256) void paged_decode_split(
 }
 
 // Balanced split: a fixed grid of nwg workgroups (wpg waves each, one kv
-// head per wave) shares the work evenly, whatever the context lengths.
+// head per wave; one workgroup per CU) shares the work evenly, whatever the
+// context lengths.
 // Work units are (sequence b, kv-head group, tile) triples in that order,
 // n_b = ceil(L_b / tile) tiles per (sequence, group), where L_b is the
 // clamped context length; workgroup w takes the units [w*Ct, (w+1)*Ct),
@@ -680,8 +681,11 @@ int decode_cu_count() {
 }
 
 // balanced split geometry: wpg waves (kv heads) per workgroup, ngroups
-// groups, nwg workgroups -- eight waves per CU (two per SIMD, the kernel's
-// occupancy), one round
+// groups, nwg workgroups -- one 4-wave workgroup per CU, one round.  Fewer,
+// longer streams beat filling the kernel's occupancy (two waves per SIMD):
+// measured at 1 / 2 / 3 / 4 / 8 workgroups per CU, cfg3 44.3 / 49.4 / 56.6 /
+// 56.0 / 66.2 us, cfg4 1169 / 1190 / 1202 / 1212 / 1257 us (fewer tile
+// pipelines to ramp up, fewer partials, fewer concurrent DRAM streams).
 struct BalancedGeom {
   int wpg, ngroups, nwg;
 };
@@ -689,7 +693,7 @@ BalancedGeom balanced_geom(int Hkv) {
   BalancedGeom g;
   g.wpg = Hkv < 4 ? Hkv : 4;
   g.ngroups = (Hkv + g.wpg - 1) / g.wpg;
-  g.nwg = decode_cu_count() * (8 / g.wpg);
+  g.nwg = decode_cu_count() * (4 / g.wpg);
   return g;
 }
 
@@ -749,7 +753,7 @@ extern "C" int64_t lfs_paged_decode_workspace_bytes(int64_t B, int32_t num_q_hea
   if (B < 0 || num_q_heads <= 0 || head_dim <= 0 || max_blocks < 0 || blocks_per_split < 0) return -1;
   if (blocks_per_split == 0) {
     // balanced split: partial rows (nwg + B*ngroups)*wpg*G <= (8*CUs + 2*B)*Hq
-    // (wpg*G <= Hq, nwg*wpg <= 8*CUs, ngroups*wpg < 2*Hkv), then B+1 ints
+    // (wpg*G <= Hq, nwg*wpg <= 4*CUs, ngroups*wpg < 2*Hkv), then B+1 ints
     const int64_t rows = (8 * (int64_t)decode_cu_count() + 2 * B) * num_q_heads;
     return 4 * rows * ((int64_t)head_dim + 2) + 4 * (B + 1);
   }

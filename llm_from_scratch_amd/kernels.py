@@ -247,11 +247,11 @@ BALANCED_MAX_BATCH = 8192  # the balanced split scans the batch's tile counts in
 def default_blocks_per_split(batch: int, num_kv_heads: int, max_blocks: int, block_size: int) -> int:
     """Split of the decode context (shapes only, so the choice is capturable).
 
-    0 selects the balanced split: a fixed grid of two 4-wave workgroups per
+    0 selects the balanced split: a fixed grid of one 4-wave workgroup per
     CU, each taking an equal share of the (sequence, kv-head group, tile)
     work, whatever the context lengths.  Measured on MI355X: cfg4 (B 256,
-    lengths log-uniform to 32k) 1188 us against 1523 us for the best fixed
-    chunking; cfg3 49.6 us against 49.7 us.
+    lengths log-uniform to 32k) 1169 us against 1523 us for the best fixed
+    chunking; cfg3 44.3 us against 49.7 us.
 
     Above BALANCED_MAX_BATCH sequences, fixed chunks of the returned number
     of blocks, one wave per (sequence, kv head, chunk): with fewer than 1024
