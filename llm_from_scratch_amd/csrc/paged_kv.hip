@@ -489,7 +489,9 @@ __device__ __forceinline__ int part_span(const PartMap& pm, int b, int h, int Hq
   return (int)(wl - wf + 1);
 }
 
-// One workgroup per (head, sequence), one lane per head dim.
+// One workgroup per (head, sequence), one lane per head dim.  Up to MERGE_NS
+// partials are loaded together (one memory round trip), more in a loop.
+constexpr int MERGE_NS = 16;
 __global__ __launch_bounds__(128) void paged_decode_merge(
     const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
     const int64_t* __restrict__ ctx_lens, uint16_t* __restrict__ out, int Hq, int D, int BS,
@@ -500,7 +502,33 @@ __global__ __launch_bounds__(128) void paged_decode_merge(
   const int ns = part_span(pm, b, h, Hq, Lc, BS, r0, rs);
   if (ns == 1 || d >= D) return;
   float res = 0.f;
-  if (ns > 1) {
+  if (ns > 1 && ns <= MERGE_NS) {
+    // every partial's (m, l, o) loaded in one round trip, then the same
+    // arithmetic in the same order as the loop below (bit-identical)
+    float mv[MERGE_NS], lv[MERGE_NS], ov[MERGE_NS];
+#pragma unroll
+    for (int s = 0; s < MERGE_NS; ++s) {
+      const int64_t r = r0 + (s < ns ? s : 0) * rs;
+      mv[s] = ws_ml[r * 2];
+      lv[s] = ws_ml[r * 2 + 1];
+      ov[s] = ws_o[r * D + d];
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < MERGE_NS; ++s)
+      if (s < ns) M = fmaxf(M, mv[s]);
+    float num = 0.f, den = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int s = 0; s < MERGE_NS; ++s)
+        if (s < ns) {
+          const float w = exp2f(mv[s] - M);
+          den = fmaf(w, lv[s], den);
+          num = fmaf(w, ov[s], num);
+        }
+    }
+    res = den > 0.f ? num / den : 0.f;
+  } else if (ns > 1) {
     float M = -INFINITY;
     for (int s = 0; s < ns; ++s) M = fmaxf(M, ws_ml[(r0 + s * rs) * 2]);
     float num = 0.f, den = 0.f;
