@@ -14,6 +14,18 @@
 namespace lfs {
 
 // ------------------------------------------------------------ act_quant --
+// One lane per 8 consecutive elements (one 16-byte load); a group of GS
+// elements is GS/8 consecutive lanes of one wave, reduced with shuffles.
+// Each thread handles AQ_U chunks a grid-stride apart (the stride is a
+// multiple of 256, so a group's lanes stay together and all in or all out),
+// issuing their loads before any arithmetic.  Input and codes are streamed
+// once, so loads and stores are nontemporal.  Measured at 16384 x 4096 with
+// the Infinity Cache flushed (kernel trace, median): one chunk per thread
+// with plain loads and stores 58.5 us; 1 / 2 / 4 / 8 chunks with
+// nontemporal loads and stores 47.7 / 46.9 / 47.1 / 49.2 us (nontemporal
+// loads alone: 48.5 / 49.0 / 49.2 / 51.0 us).
+constexpr int AQ_U = 2;
+
 template <int GS, bool ROUND>
 __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                         uint8_t* __restrict__ y,
@@ -21,21 +33,37 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restri
                                                         int64_t K) {
   constexpr int LPG = GS / 8;  // lanes per group; groups never straddle waves
   const int64_t cpr = K / 8;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  // K % GS == 0 and 256 % LPG == 0, so a group's lanes are all in or all out
-  if (idx >= M * cpr) return;
-  const int64_t row = idx / cpr;
-  const int64_t c8 = idx - row * cpr;
-  const uint4 v = *reinterpret_cast<const uint4*>(x + row * ldx + c8 * 8);
-  float f[8];
-  unpack8(v, f);
-  float amax = 0.f;
+  const int64_t total = M * cpr;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  const int64_t idx0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+  typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+  u32x4_t v[AQ_U];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[i]));
-  amax = group_max<LPG>(amax);
-  const float sc = scale_from_amax(amax, ROUND);
-  *reinterpret_cast<uint2*>(y + row * K + c8 * 8) = quant8(f, sc);
-  if ((c8 & (LPG - 1)) == 0) s[row * (K / GS) + c8 / LPG] = sc;
+  for (int j = 0; j < AQ_U; ++j) {
+    const int64_t idx = idx0 + j * stride;
+    if (idx < total) {
+      const int64_t row = idx / cpr, c8 = idx - row * cpr;
+      v[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(x + row * ldx + c8 * 8));
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < AQ_U; ++j) {
+    const int64_t idx = idx0 + j * stride;
+    // K % GS == 0 and 256 % LPG == 0, so a group's lanes are all in or all out
+    if (idx >= total) break;
+    const int64_t row = idx / cpr, c8 = idx - row * cpr;
+    float f[8];
+    unpack8(make_uint4(v[j][0], v[j][1], v[j][2], v[j][3]), f);
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[i]));
+    amax = group_max<LPG>(amax);
+    const float sc = scale_from_amax(amax, ROUND);
+    const uint2 q = quant8(f, sc);
+    __builtin_nontemporal_store(u32x2_t{q.x, q.y}, reinterpret_cast<u32x2_t*>(y + row * K + c8 * 8));
+    if ((c8 & (LPG - 1)) == 0) s[row * (K / GS) + c8 / LPG] = sc;
+  }
 }
 
 // --------------------------------------------------------- weight_quant --
@@ -127,7 +155,7 @@ extern "C" int lfs_act_quant(const void* x, int64_t ldx, void* y, float* s, int6
   LFS_REQUIRE(aligned16(x) && ((uintptr_t)y & 7u) == 0 && ((uintptr_t)s & 3u) == 0,
               "act_quant: misaligned buffer");
   const int64_t chunks = M * (K / 8);
-  const dim3 grid((unsigned)((chunks + 255) / 256));
+  const dim3 grid((unsigned)((chunks + 256 * AQ_U - 1) / (256 * AQ_U)));
   hipStream_t st = (hipStream_t)stream;
   const uint16_t* xp = (const uint16_t*)x;
   uint8_t* yp = (uint8_t*)y;
