@@ -214,7 +214,7 @@ def bench_moe(device, reps):
 def bench_decode(name, device, reps, flush_buf):
     from llm_from_scratch_amd import kernels as K
     from llm_from_scratch_amd import workloads as W
-    case = W.paged_case(name, seed=2 if name == "cfg3" else 3)
+    case = W.paged_case(name, seed=3 if name == "cfg4" else 2)
     kc, vc = W.fill_pool(case, seed=2, device=device, only_referenced=(name == "cfg4"))
     g = torch.Generator(device=device).manual_seed(5)
     q = torch.randn(case.batch, case.num_q_heads, case.head_dim, generator=g, device=device,
@@ -321,7 +321,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip decode / act_quant lines")
-    ap.add_argument("--extras", default="act_quant,cfg3,cfg4,prefill,indexer,moe,cfg5",
+    ap.add_argument("--extras", default="act_quant,cfg3,cfg3_4k,cfg4,prefill,indexer,moe,cfg5",
                     help="comma list of extra lines: act_quant, cfg3, cfg4 (paged decode), prefill "
                          "(varlen prefill attention), indexer (DSA fp8_index), moe (MoE layer, grouped "
                          "vs dense dispatch), cfg5 (decode step)")
@@ -383,7 +383,7 @@ def main():
         "gemm_shapes": shapes,
     }
     try:
-        decode = [n for n in ("cfg3", "cfg4") if n in extras]
+        decode = [n for n in ("cfg3", "cfg3_4k", "cfg4") if n in extras]
         if decode or "act_quant" in extras:
             flush_buf = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev).zero_()
         if "act_quant" in extras:

@@ -184,10 +184,15 @@ int lfs_store_kvcache(const void* key, int64_t k_stride_t, const void* value, in
  * [B, bt_stride], entries t/BS < ceil(L_b/BS) valid, the rest ignored (-1
  * padding); out: bf16 [B, Hq, D].  Block ids outside [0, NB) contribute
  * nothing.
- * The context is split into chunks of blocks_per_split blocks processed in
- * parallel and merged by log-sum-exp; the grid depends only on B and
- * max_blocks (not on the lengths), so the call is graph-capturable.
- * workspace: at least lfs_paged_decode_workspace_bytes(...) bytes.
+ * blocks_per_split = n > 0: every context is split into chunks of n blocks
+ * processed in parallel (one wave per sequence, kv head and chunk) and
+ * merged by log-sum-exp.  blocks_per_split = 0 (B <= 8192): balanced split,
+ * a fixed grid of one 4-wave workgroup per CU, each taking an equal share of
+ * the (sequence, kv-head group, tile) work whatever the lengths, then the
+ * same merge.  Either way the grid depends only on the shapes (not on the
+ * lengths), so the call is graph-capturable.
+ * workspace: at least lfs_paged_decode_workspace_bytes(...) bytes (for 0 a
+ * bound from the current device's CU count: size it on that device).
  * Optionally (q_out and q_scale both non-NULL) also the act_quant of each
  * output row, the output projection's FP8 input: q_out e4m3fn [B, Hq*D],
  * q_scale fp32 [B, Hq*D/128], bit-identical to lfs_act_quant(out, 128)

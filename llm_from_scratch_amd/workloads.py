@@ -10,6 +10,8 @@ Shapes and distributions follow the benchmark configs (cfg1..cfg4):
         4096-block pool, scale 1/8
   cfg4  long-context decode, GQA 32/8, D 128, block 256, batch 256, lengths
         log-uniform in [512, 32768], 65536-block pool, scale 1/sqrt(128)
+  cfg3_4k  cfg3's geometry with every context 4096 tokens (batch 64 / 4K
+        context, the decode target's literal reading)
 
 Host-side metadata (lengths, tables, slots) comes from numpy's seeded
 generator; tensor contents from a seeded torch generator on the target
@@ -78,6 +80,8 @@ class PagedCase:
 
 CONFIGS = {
     "cfg3": dict(Hq=16, Hkv=4, D=64, BS=256, B=64, NB=4096, lens=("uniform", 128, 4096), scale=1 / 8),
+    # the north star's decode target read literally: batch 64, every context 4096 tokens
+    "cfg3_4k": dict(Hq=16, Hkv=4, D=64, BS=256, B=64, NB=4096, lens=("fixed", 4096, 4096), scale=1 / 8),
     "cfg4": dict(Hq=32, Hkv=8, D=128, BS=256, B=256, NB=65536, lens=("loguniform", 512, 32768),
                  scale=1 / math.sqrt(128)),
 }
@@ -93,6 +97,8 @@ def paged_case(name: str, seed: int, batch: int | None = None) -> PagedCase:
     kind, lo, hi = c["lens"]
     if kind == "uniform":
         lens = rng.integers(lo, hi + 1, B)
+    elif kind == "fixed":
+        lens = np.full(B, lo, np.int64)
     else:
         lens = np.round(np.exp(rng.uniform(math.log(lo), math.log(hi), B))).astype(np.int64)
     if batch is not None:
