@@ -554,6 +554,10 @@ __global__ __launch_bounds__(128) void paged_decode_merge(
 constexpr int MQ_MAXE = 8192;  // Hq * D per sequence
 constexpr int MQ_MAXH = 128;
 constexpr int MQ_MAXW = 4096;  // (split, head) weights staged in LDS
+// rows of at most MQ_PF_EPT * 256 values whose heads have at most MQ_PF_NS
+// partials: each thread's partial outputs are loaded in the same round trip
+// as the staged (m, l) values, not after the two barriers that follow
+constexpr int MQ_PF_NS = 6, MQ_PF_EPT = 4;
 
 __global__ __launch_bounds__(256) void paged_decode_merge_quant(
     const float* __restrict__ ws_o, const float* __restrict__ ws_ml, const int64_t* __restrict__ ctx_lens,
@@ -586,6 +590,21 @@ __global__ __launch_bounds__(256) void paged_decode_merge_quant(
     // (m, l) of every (split, head) in one parallel step; the per-head max,
     // weights and denominators from LDS (the unfused merge's arithmetic)
     const bool staged = nsmax * Hq <= MQ_MAXW;
+    const bool pf = staged && nsmax <= MQ_PF_NS && E <= 256 * MQ_PF_EPT;
+    float ov[MQ_PF_EPT][MQ_PF_NS];  // thread's elements tid + 256k: partial outputs, or the row value
+    if (pf) {
+#pragma unroll
+      for (int k = 0; k < MQ_PF_EPT; ++k) {
+        const int e = tid + 256 * k;
+        const int h = e < E ? e / D : 0, d = e - h * D;
+        const int ns = e < E ? hNs[h] : 0;
+        const int64_t r0 = hR0[h];
+#pragma unroll
+        for (int sp = 0; sp < MQ_PF_NS; ++sp)
+          ov[k][sp] = sp < ns && ns > 1 ? ws_o[(r0 + sp * rs) * D + d] : 0.f;
+        if (ns == 1) ov[k][0] = bf16_to_f32(orow[e]);  // written by the split kernel
+      }
+    }
     if (staged) {
       for (int x = tid; x < nsmax * Hq; x += 256) {
         const int sp = x / Hq, h = x - sp * Hq;
@@ -611,7 +630,30 @@ __global__ __launch_bounds__(256) void paged_decode_merge_quant(
       hDen[h] = M != -INFINITY ? den : 0.f;
     }
     __syncthreads();
-    for (int e = tid; e < E; e += 256) {
+    if (pf) {
+#pragma unroll
+      for (int k = 0; k < MQ_PF_EPT; ++k) {
+        const int e = tid + 256 * k;
+        if (e >= E) break;
+        const int h = e / D;
+        const int ns = hNs[h];
+        if (ns == 1) {  // written by the split kernel (a bf16 value: exact in fp32)
+          vals[e] = (uint16_t)f32_to_bf16(ov[k][0]);
+          continue;
+        }
+        float num = 0.f, den = 0.f;
+        if (ns > 1) {
+          den = hDen[h];
+#pragma unroll
+          for (int sp = 0; sp < MQ_PF_NS; ++sp)
+            if (sp < ns) num = fmaf(wts[sp * Hq + h], ov[k][sp], num);
+        }
+        const uint16_t v = (uint16_t)f32_to_bf16(den > 0.f ? num / den : 0.f);
+        orow[e] = v;
+        vals[e] = v;
+      }
+    }
+    for (int e = pf ? E : tid; e < E; e += 256) {
       const int h = e / D, d = e - h * D;
       const int ns = hNs[h];
       if (ns == 1) {  // written by the split kernel
