@@ -57,6 +57,7 @@
  *                           model/attention/GQA.py:80-95,
  *                           model/attention/utils.py:34-45
  *   lfs_moe_route           MoE gate, model/architecture/moe.py:45-90
+ *   lfs_add_rmsnorm_route   ffn_norm + MoE gate in one launch (decode step)
  *   lfs_swiglu_quant        silu(w1 x) * w3 x, model/architecture/mlp.py:60-67,
  *                           quantised for the experts' down projection
  * MoE expert dispatch (MoE.moe_infer, model/architecture/moe.py:288-341,
@@ -85,7 +86,7 @@
 extern "C" {
 #endif
 
-#define LFS_ABI_VERSION 8
+#define LFS_ABI_VERSION 9
 
 /* argument errors (negative); launch errors are positive hipError_t values */
 #define LFS_EINVAL (-1)
@@ -306,6 +307,20 @@ int lfs_moe_route(const void* h, const void* gate_weight, const float* expert_bi
                   const float* down_bias, float* dense_weights, float* bias_out, int64_t T,
                   int32_t d, int32_t num_experts, int32_t num_shared, int32_t top_k,
                   int64_t* topk_idx, float* topk_weight, void* stream);
+
+/*
+ * add_rmsnorm_route: lfs_add_rmsnorm (quantised output required) and
+ * lfs_moe_route (dense weights, optional routed bias) of the same rows in one
+ * launch -- the decode step's ffn_norm (model/transformer.py:90-118) followed
+ * by the MoE gate (model/architecture/moe.py:45-90), replacing the pair
+ * add_rmsnorm + moe_route.  Outputs bit-identical to that pair; out (the bf16
+ * normalised rows) may be NULL.  d % 128 == 0, d <= 8192; E + S <= 64.
+ */
+int lfs_add_rmsnorm_route(const void* x, const void* residual, const float* weight, void* out,
+                          void* residual_out, void* q, float* q_scale, int64_t T, int32_t d, float eps,
+                          const void* gate_weight, const float* expert_bias, const float* down_bias,
+                          float* dense_weights, float* bias_out, int32_t num_experts, int32_t num_shared,
+                          int32_t top_k, void* stream);
 
 /*
  * swiglu_quant, for h13: bf16 [T, E, 2, F] (per expert the w1 then the w3

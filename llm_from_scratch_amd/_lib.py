@@ -11,7 +11,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "liblfs_kernels.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _c_i64, _c_i32, _c_p, _c_f = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p, ctypes.c_float
 
@@ -38,6 +38,8 @@ SIGNATURES = {
     "lfs_add_rmsnorm": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_f, _c_p]),
     "lfs_qk_norm_rope_store": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
                                               _c_i64, _c_i32, _c_i32, _c_i32, _c_i64, _c_i64, _c_f, _c_p]),
+    "lfs_add_rmsnorm_route": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_f,
+                                             _c_p, _c_p, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_p]),
     "lfs_moe_route": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_i32,
                                      _c_i32, _c_p, _c_p, _c_p]),
     "lfs_swiglu_quant": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_p]),

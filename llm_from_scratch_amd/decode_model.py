@@ -22,8 +22,9 @@ Interface (nano-vLLM style, as the runner expects):
 
 Kernels per layer: add_rmsnorm (+act_quant) -> qkv FP8 GEMM ->
 qk_norm_rope_store -> paged decode (split + merge with the act_quant of its
-output) -> output FP8 GEMM -> add_rmsnorm (+act_quant) -> moe_route -> gate/up FP8 GEMM ->
-swiglu_quant -> down FP8 GEMM.  Setting ``model.trace = {}`` makes an
+output) -> output FP8 GEMM -> add_rmsnorm_route (the ffn_norm with its act_quant
+and the MoE gate in one launch; add_rmsnorm then moe_route for grouped
+batches) -> gate/up FP8 GEMM -> swiglu_quant -> down FP8 GEMM.  Setting ``model.trace = {}`` makes an
 eager forward record every intermediate (per layer) for parity tests.
 
 MoE in the decode step: every expert runs over the whole batch and is
@@ -236,11 +237,22 @@ class MoE(nn.Module):
                 trace: Optional[dict] = None) -> torch.Tensor:
         """h: the ffn_norm output (bf16, for the gate); hq, hs: the same
         quantised (for the experts)."""
-        T, F = h.size(0), self.d_ff
-        if self.dispatch == "grouped" or (self.dispatch == "auto" and T > self.GROUPED_MIN_TOKENS):
+        T = h.size(0)
+        if not self.dense_dispatch(T):
             return self.forward_grouped(h, hq, hs, trace)
         w, bias = kernels.moe_route(h, self.gate_weight, self.expert_bias, self.w2_bias, self.top_k,
                                     self.n_shared)
+        return self.forward_routed(hq, hs, w, bias, trace)
+
+    def dense_dispatch(self, T: int) -> bool:
+        """Every expert over every token (small batches) rather than grouped."""
+        return not (self.dispatch == "grouped" or (self.dispatch == "auto" and T > self.GROUPED_MIN_TOKENS))
+
+    def forward_routed(self, hq: torch.Tensor, hs: torch.Tensor, w: torch.Tensor, bias: torch.Tensor,
+                       trace: Optional[dict] = None) -> torch.Tensor:
+        """The dense dispatch given the gate's weights and routed bias (from
+        moe_route, or from add_rmsnorm_route together with the ffn_norm)."""
+        T, F = hq.size(0), self.d_ff
         h13 = self.w13.gemm(hq, hs)
         gq, gs = kernels.swiglu_quant(h13.view(T, -1, 2, F), w)
         y = kernels.fp8_gemm(gq, gs, self.w2.weight, self.w2.weight_scale, bias)
@@ -283,6 +295,15 @@ class Block(nn.Module):
             trace.update(x=x, residual=residual)
         h, residual, hq, hs = self.att_norm(x, residual, out=trace is not None, quant=True)
         x = self.att(hq, hs, positions, trace)
+        if self.ffn.dense_dispatch(x.size(0)):
+            # ffn_norm and the MoE gate in one launch (the same results as the pair)
+            ffn = self.ffn
+            h2, residual, hq, hs, w, bias = kernels.add_rmsnorm_route(
+                x, self.ffn_norm.weight, self.ffn_norm.eps, residual, ffn.gate_weight, ffn.expert_bias,
+                ffn.w2_bias, ffn.top_k, ffn.n_shared, out=trace is not None)
+            if trace is not None:
+                trace.update(att_h=h, ffn_h=h2, res_mid=residual)
+            return ffn.forward_routed(hq, hs, w, bias, trace), residual
         h2, residual, hq, hs = self.ffn_norm(x, residual, out=True, quant=True)
         if trace is not None:
             trace.update(att_h=h, ffn_h=h2, res_mid=residual)

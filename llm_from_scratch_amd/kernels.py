@@ -555,6 +555,48 @@ def moe_route(h: torch.Tensor, gate_weight: torch.Tensor, expert_bias: torch.Ten
     return w, bias
 
 
+def add_rmsnorm_route(x: torch.Tensor, weight: torch.Tensor, eps: float, residual: Optional[torch.Tensor],
+                      gate_weight: torch.Tensor, expert_bias: torch.Tensor, down_bias: Optional[torch.Tensor],
+                      top_k: int, num_shared: int, out: bool = False):
+    """The decode step's ffn_norm and MoE gate in one launch: the results of
+    add_rmsnorm(x, weight, eps, residual, out, quant=True) followed by
+    moe_route(normalised rows, gate_weight, expert_bias, down_bias, top_k,
+    num_shared), bit for bit.  Returns (out or None, residual_out, q,
+    q_scale, weights fp32 [T, E + S], bias fp32 [T, d] or None)."""
+    assert x.dim() == 2 and x.is_contiguous(), "x must be contiguous [T, d]"
+    assert gate_weight.is_contiguous()
+    T, d = x.shape
+    E = gate_weight.size(0)
+    _on_gpu(x, weight, gate_weight, expert_bias)
+    _dtype(x, torch.bfloat16, "x")
+    _dtype(weight, torch.float32, "weight")
+    _dtype(gate_weight, torch.bfloat16, "gate_weight")
+    _dtype(expert_bias, torch.float32, "expert_bias")
+    assert weight.is_contiguous() and weight.shape == (d,)
+    assert gate_weight.shape == (E, d) and expert_bias.shape == (E,)
+    res_out = None
+    if residual is not None:
+        _on_gpu(x, residual)
+        _dtype(residual, torch.bfloat16, "residual")
+        assert residual.shape == x.shape and residual.is_contiguous()
+        res_out = torch.empty_like(x)
+    if down_bias is not None:
+        _on_gpu(x, down_bias)
+        _dtype(down_bias, torch.float32, "down_bias")
+        assert down_bias.shape == (E + num_shared, d) and down_bias.is_contiguous()
+    y = torch.empty_like(x) if out else None
+    q = torch.empty(T, d, dtype=FP8, device=x.device)
+    qs = torch.empty(T, d // 128, dtype=torch.float32, device=x.device)
+    w = torch.empty(T, E + num_shared, dtype=torch.float32, device=x.device)
+    bias = torch.empty(T, d, dtype=torch.float32, device=x.device) if down_bias is not None else None
+    rc = _lib.load().lfs_add_rmsnorm_route(_ptr(x), _ptr(residual), _ptr(weight), _ptr(y), _ptr(res_out),
+                                           _ptr(q), _ptr(qs), T, d, float(eps), _ptr(gate_weight),
+                                           _ptr(expert_bias), _ptr(down_bias), _ptr(w), _ptr(bias), E,
+                                           num_shared, top_k, _stream(x))
+    _lib.check(rc, "add_rmsnorm_route")
+    return y, (res_out if residual is not None else x), q, qs, w, bias
+
+
 def swiglu_quant(h13: torch.Tensor, route_weights: torch.Tensor):
     """silu(w1 x) * (w3 x) with bf16 roundings (model/architecture/mlp.py:
     60-67), quantised per 128 group with each group's scale multiplied by the

@@ -138,3 +138,26 @@ def test_swiglu_quant(T, E, F):
     assert same > 0.999, f"codes equal for {same:.5f} of elements"
     want_s = (qs2.view(T, E, F // 128) * route.unsqueeze(-1)).view(T, -1)
     torch.testing.assert_close(qs, want_s, rtol=2e-7, atol=0)
+
+
+@pytest.mark.parametrize("T,d,E,S,top_k,with_res", [(128, 768, 8, 1, 2, True), (37, 1024, 16, 2, 4, False),
+                                                    (9, 2048, 8, 0, 1, True), (5, 4096, 32, 1, 3, True)])
+def test_add_rmsnorm_route_equals_norm_then_gate(T, d, E, S, top_k, with_res):
+    """The fused ffn_norm + MoE gate launch gives the outputs of add_rmsnorm
+    (quantised) followed by moe_route bit for bit: residual, codes, scales,
+    dense routing weights and routed down bias."""
+    g = torch.Generator(device="cuda").manual_seed(T + d + E)
+    x = torch.randn(T, d, generator=g, device="cuda").to(torch.bfloat16)
+    res = torch.randn(T, d, generator=g, device="cuda").to(torch.bfloat16) if with_res else None
+    w = (1 + 0.1 * torch.randn(d, generator=g, device="cuda")).float()
+    gw = (0.05 * torch.randn(E, d, generator=g, device="cuda")).to(torch.bfloat16)
+    eb = (0.1 * torch.randn(E, generator=g, device="cuda")).float()
+    b2 = (0.02 * torch.randn(E + S, d, generator=g, device="cuda")).float()
+    h, r, q, qs = K.add_rmsnorm(x, w, 1e-5, res, out=True, quant=True)
+    rw, rb = K.moe_route(h, gw, eb, b2, top_k, S)
+    h2, r2, q2, qs2, rw2, rb2 = K.add_rmsnorm_route(x, w, 1e-5, res, gw, eb, b2, top_k, S, out=True)
+    torch.cuda.synchronize()
+    assert torch.equal(h2, h) and torch.equal(r2, r)
+    assert torch.equal(q2.view(torch.uint8), q.view(torch.uint8)) and torch.equal(qs2, qs)
+    assert torch.equal(rw2, rw) and torch.equal(rb2, rb)
+    assert int((rw2[:, :E] > 0).sum(1).min()) == top_k and bool((rw2[:, E:] == 1).all())
