@@ -4,16 +4,18 @@
 // bf16, as allocated by engine/model_runner.py:184-190 of the reference; one
 // token's K (or V) row for all kv heads is Hkv*D*2 contiguous bytes.
 //
-// paged decode, phase 1 (paged_decode_split): one wave per (sequence, kv
-//   head, chunk of blocks_per_split KV blocks), four kv heads of one
-//   sequence and chunk per workgroup, grid (sequence, chunk, head group).
-//   The wave walks its chunk in tiles of up to 64 tokens that never cross a
+// paged decode, phase 1: a wave streams a range of one (sequence, kv head)'s
+//   context (decode_chunk) in tiles of up to 64 tokens that never cross a
 //   KV block (one block-table lookup per tile): S = K q^T on MFMA for the G
 //   query heads of its kv head, online softmax in the log2 domain, P through
 //   a wave-private LDS slice, P.V in fp32 registers.  Loads run two tiles
-//   ahead.  The partial (unnormalised o, m, l) of the chunk goes to the
-//   workspace, or, when the chunk is the whole context, the normalised bf16
-//   output is written directly.
+//   ahead.  The partial (unnormalised o, m, l) of the range goes to the
+//   workspace, or, when the range is the whole context, the normalised bf16
+//   output is written directly.  The ranges come from either
+//   paged_decode_balanced (default: one 4-wave workgroup per CU, each an
+//   equal share of the (sequence, kv-head group, tile) work) or
+//   paged_decode_split (one wave per (sequence, kv head, chunk of
+//   blocks_per_split blocks)).
 // phase 2 (paged_decode_merge, one workgroup per (head, sequence)):
 //   log-sum-exp merge of the chunks, normalise, bf16.  Padding rows
 //   (context_len 0) get zeros.  paged_decode_merge_quant (one workgroup per
