@@ -140,7 +140,7 @@ def test_paged_decode_split_independence():
 
 
 @pytest.mark.parametrize("Hq,Hkv,D,BS", [(12, 4, 64, 256), (8, 8, 128, 16), (16, 2, 128, 32),
-                                         (32, 4, 64, 64), (6, 2, 64, 48)])
+                                         (32, 4, 64, 64), (6, 2, 64, 48), (4, 1, 64, 16), (9, 3, 128, 64)])
 def test_paged_decode_shapes(Hq, Hkv, D, BS):
     rng = np.random.default_rng(Hq * 1000 + D + BS)
     B, NB = 7, 128
