@@ -116,6 +116,30 @@ def bench_act_quant(device, reps, flush_buf):
 BF16_PEAK_TFLOPS = 2500.0
 
 
+def bench_gemm_small(device, reps, flush_buf):
+    """cfg2's decode-sized GEMMs (M in {1, 16, 128}): HBM/latency-bound, so
+    reported as algorithmic bytes (A + B + scales read, C written) per second
+    against the 8 TB/s roofline.  The weights (<= 11.5 MB) would sit in the
+    Infinity Cache, so a 512 MB write evicts them before every call.  Default
+    dispatch of kernels.fp8_gemm (skinny kernel, split-K or tiles)."""
+    from llm_from_scratch_amd import kernels as K
+    from llm_from_scratch_amd import workloads as W
+    out = []
+    for M in (1, 16, 128):
+        for Kd, N in W.GEMM_KN:
+            x = W.activation(M, Kd, seed=1 + M + Kd, device=device)
+            w = W.weight(N, Kd, seed=31 + Kd, device=device)
+            xq, xs = K.act_quant(x)
+            wq, ws = K.weight_quant(w)
+            fn = lambda: K.fp8_gemm(xq, xs, wq, ws)  # noqa: E731
+            fn()
+            t = timed_launches([fn], reps, flush=lambda: flush_buf.add_(1))[0]
+            nbytes = M * Kd + N * Kd + 4 * (xs.numel() + ws.numel()) + 2 * M * N
+            out.append({"M": M, "K": Kd, "N": N, "us": t * 1e6, "GB/s": nbytes / t / 1e9,
+                        "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "TFLOP/s": 2.0 * M * N * Kd / t / 1e12})
+    return out
+
+
 def bench_prefill(device, reps):
     """Varlen causal prefill attention at the cfg5 attention geometry (GQA
     12/4, D = 64): 16 whole prompts of 2048 tokens (keys just stored,
@@ -321,7 +345,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip decode / act_quant lines")
-    ap.add_argument("--extras", default="act_quant,cfg3,cfg3_4k,cfg4,prefill,indexer,moe,cfg5",
+    ap.add_argument("--extras", default="act_quant,gemm_small,cfg3,cfg3_4k,cfg4,prefill,indexer,moe,cfg5",
                     help="comma list of extra lines: act_quant, cfg3, cfg4 (paged decode), prefill "
                          "(varlen prefill attention), indexer (DSA fp8_index), moe (MoE layer, grouped "
                          "vs dense dispatch), cfg5 (decode step)")
@@ -384,17 +408,20 @@ def main():
     }
     try:
         decode = [n for n in ("cfg3", "cfg3_4k", "cfg4") if n in extras]
-        if decode or "act_quant" in extras:
+        if decode or "act_quant" in extras or "gemm_small" in extras:
             flush_buf = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev).zero_()
         if "act_quant" in extras:
             log("bench: act_quant")
             out["act_quant"] = bench_act_quant(dev, 20, flush_buf)
+        if "gemm_small" in extras:
+            log("bench: fp8_gemm at M <= 128")
+            out["gemm_small"] = bench_gemm_small(dev, 20, flush_buf)
         if decode:
             out["paged_decode"] = []
             for name in decode:
                 log(f"bench: paged decode {name}")
                 out["paged_decode"].append(bench_decode(name, dev, 20, flush_buf))
-        if decode or "act_quant" in extras:
+        if decode or "act_quant" in extras or "gemm_small" in extras:
             del flush_buf
             torch.cuda.empty_cache()
         if "indexer" in extras:
