@@ -411,14 +411,16 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
 // with no split-K workspace or second kernel.
 constexpr int SK_BN = 32;
 
-template <int MTW, int WGM>
-__global__ __launch_bounds__(256 * WGM) void fp8_gemm_skinny(
+// KW waves of a group split the K blocks (4, or 8 / 16 for one 16-row tile
+// and long K: more K blocks in flight at once, still one launch).
+template <int MTW, int WGM, int KW = 4>
+__global__ __launch_bounds__(64 * KW * WGM) void fp8_gemm_skinny(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ B,
     const float* __restrict__ Bs, const float* __restrict__ bias, int64_t bias_ld, uint16_t* __restrict__ C,
     int M, int N, int K) {
-  __shared__ __attribute__((aligned(16))) v4f red[WGM][4][MTW][2][64];
+  __shared__ __attribute__((aligned(16))) v4f red[WGM][KW][MTW][2][64];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int gm = wave >> 2, kw = wave & 3;
+  const int gm = wave / KW, kw = wave % KW;
   const int r16 = lane & 15, g = lane >> 4;
   const int n0 = blockIdx.x * SK_BN;
   const int KT = K / BK;
@@ -473,27 +475,27 @@ __global__ __launch_bounds__(256 * WGM) void fp8_gemm_skinny(
     }
   };
   if (kw < KT) load_block(bf0, af0, sa0, sb0, kw);
-  for (int kb = kw; kb < KT; kb += 8) {
-    if (kb + 4 < KT) load_block(bf1, af1, sa1, sb1, kb + 4);
+  for (int kb = kw; kb < KT; kb += 2 * KW) {
+    if (kb + KW < KT) load_block(bf1, af1, sa1, sb1, kb + KW);
     compute(bf0, af0, sa0, sb0);
-    if (kb + 4 >= KT) break;
-    if (kb + 8 < KT) load_block(bf0, af0, sa0, sb0, kb + 8);
+    if (kb + KW >= KT) break;
+    if (kb + 2 * KW < KT) load_block(bf0, af0, sa0, sb0, kb + 2 * KW);
     compute(bf1, af1, sa1, sb1);
   }
 
-  // ---- the four partials of the group, summed in wave order
+  // ---- the KW partials of the group, summed in wave order
 #pragma unroll
   for (int mt = 0; mt < MTW; ++mt)
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) red[gm][kw][mt][nt][lane] = acc[mt][nt];
   __syncthreads();
-  for (int mt = kw; mt < MTW; mt += 4) {
+  for (int mt = kw; mt < MTW; mt += KW) {
     const int m = 16 * (gm * MTW + mt) + r16;
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       v4f s = red[gm][0][mt][nt][lane];
 #pragma unroll
-      for (int w = 1; w < 4; ++w) {
+      for (int w = 1; w < KW; ++w) {
         const v4f x = red[gm][w][mt][nt][lane];
 #pragma unroll
         for (int r = 0; r < 4; ++r) s[r] += x[r];
@@ -897,13 +899,17 @@ extern "C" int lfs_fp8_gemm_skinny(const void* a, const float* a_s, const void* 
   const dim3 grid((unsigned)((N + SK_BN - 1) / SK_BN));
   hipStream_t st = (hipStream_t)stream;
   const int mt = (int)((M + 15) / 16);
-#define LFS_SK(MTW, WGM)                                                                                   \
-  hipLaunchKernelGGL((fp8_gemm_skinny<MTW, WGM>), grid, dim3(256 * WGM), 0, st, (const uint8_t*)a, a_s,     \
-                     (const uint8_t*)b, b_s, bias, bias_ld, (uint16_t*)c, (int)M, (int)N, (int)K)
-  if (mt <= 1) LFS_SK(1, 1);
-  else if (mt <= 2) LFS_SK(2, 1);
-  else if (mt <= 4) LFS_SK(4, 1);
-  else LFS_SK(4, 2);
+  const int KT = (int)(K / 128);
+#define LFS_SK(MTW, WGM, KW)                                                                               \
+  hipLaunchKernelGGL((fp8_gemm_skinny<MTW, WGM, KW>), grid, dim3(64 * KW * WGM), 0, st, (const uint8_t*)a,  \
+                     a_s, (const uint8_t*)b, b_s, bias, bias_ld, (uint16_t*)c, (int)M, (int)N, (int)K)
+  // one 16-row tile: the K blocks over 16 / 8 / 4 waves (>= 1.5 blocks per wave)
+  if (mt <= 1 && KT >= 24) LFS_SK(1, 1, 16);
+  else if (mt <= 1 && KT >= 12) LFS_SK(1, 1, 8);
+  else if (mt <= 1) LFS_SK(1, 1, 4);
+  else if (mt <= 2) LFS_SK(2, 1, 4);
+  else if (mt <= 4) LFS_SK(4, 1, 4);
+  else LFS_SK(4, 2, 4);
 #undef LFS_SK
   return check_launch("fp8_gemm_skinny");
 }

@@ -148,7 +148,11 @@ def use_skinny_gemm(M: int, N: int, K: int) -> bool:
     8.0 vs 12.8 us; longer K (the down projection, K 4608: 31.9 vs 16.0 us
     with split-K) and wide N (w13, N 9216: 15.8 vs 13.1; lm_head, N 32000:
     30.6 vs 14.6 -- every workgroup re-reads all of A) stay on the tile
-    kernel."""
+    kernel.  With one 16-row tile (M <= 16) the kernel splits the K blocks
+    over 8 or 16 waves and re-reading A costs little, so any K up to 16384
+    and any N run it (M = 1, K = 4096, N = 1024: split-K tiles 15-16 us)."""
+    if 0 < M <= 16 and K <= 16384:
+        return True
     return 0 < M <= SKINNY_MAX_M and K <= 1024 and N <= 4096
 
 
