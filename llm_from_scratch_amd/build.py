@@ -13,6 +13,8 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
@@ -47,10 +49,7 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the gfx950 kernel library cannot be built")
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every HIP source into LIB_PATH (always recompiles)."""
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{REPO / 'include'}", *[str(CSRC / s) for s in SOURCES], "-o", str(tmp)]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -58,6 +57,22 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stdout}\n{res.stderr}")
     if verbose and res.stderr.strip():
         print(res.stderr, file=sys.stderr)
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile every HIP source into LIB_PATH (always recompiles): one object
+    per source, compiled in parallel, then one shared-library link."""
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    with tempfile.TemporaryDirectory(prefix="lfs_build_") as d:
+        objs = [str(Path(d) / (s.rsplit(".", 1)[0] + ".o")) for s in SOURCES]
+        cmds = [[hipcc(), *flags, f"-I{REPO / 'include'}", "-c", str(CSRC / s), "-o", o]
+                for s, o in zip(SOURCES, objs)]
+        n = jobs or max(1, min(len(cmds), os.cpu_count() or 1, 8))
+        with ThreadPoolExecutor(max_workers=n) as ex:
+            for f in [ex.submit(_run, c, verbose) for c in cmds]:
+                f.result()
+        _run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", str(tmp)], verbose)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

@@ -725,6 +725,224 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_big(
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Persistent 256x256 kernel: the K loop of fp8_gemm_big, one workgroup per CU
+// walking the tile sequence t = slot, slot + nwg, ... so that a tile's
+// prologue and epilogue overlap work instead of idling the CU:
+//   * the last K block of a tile copies the next tile's first block (and its
+//     scale chunk) into the free stage, so the next tile starts on data that
+//     is already in LDS;
+//   * C is written straight from the accumulators: per 16-row m-tile and pair
+//     of 16-column n-tiles a lane holds 2 x 4 adjacent columns of one row;
+//     one v_permlane16_swap per packed bf16 pair moves them so that every
+//     lane holds 8 adjacent columns, stored as one 16-byte write (a store
+//     instruction covers 16 rows x 64 contiguous bytes).  The stores are
+//     bounds-checked buffer stores (rows past M fall outside the buffer's
+//     M*N*2 bytes and are dropped by the hardware), so every wave issues
+//     exactly 16 of them per tile and the next tile's first wait keeps them
+//     in flight with vmcnt(16) (vector memory operations complete in issue
+//     order on gfx9, so that count still covers the older copies).
+// Tile order: round r of the sequence is tiles r*nwg .. r*nwg + nwg - 1 of
+// the grouped order (GROUP_M_BIG row-tiles per group); workgroup w runs on
+// XCD w % 8 and takes position (w % 8) * (nwg / 8) + w / 8 of each round, so
+// the tiles an XCD runs concurrently are consecutive in the grouped order
+// and share A and B panels in that XCD's L2.
+// Requires N % 256 == 0, M * N * 2 < 2^31, 256 * K < 2^31, nwg % 8 == 0;
+// bias: null or an fp32 vector of N (16-byte aligned).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ unsigned cvt_pk_bf16(float lo, float hi) {
+  // v_cvt_pk_bf16_f32: round to nearest even, as f32_to_bf16
+  return __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
+}
+
+template <bool HAS_BIAS>
+__global__ __launch_bounds__(512, 1) void fp8_gemm_persist(
+    const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ B,
+    const float* __restrict__ Bs, const float* __restrict__ bias, uint16_t* __restrict__ C, int M, int N, int K,
+    int tiles_m, int tiles_n) {
+  constexpr int A_BYTES = BIG * BK;
+  constexpr int STAGE = 2 * A_BYTES;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+  __shared__ __attribute__((aligned(1024))) float sas[2][SCKB][BIG];
+  __shared__ __attribute__((aligned(64))) float sbs[2][SCKB][2];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 2, wn = wave & 3;
+  const int KT = K / BK;
+  const int nch = (KT + SCKB - 1) / SCKB;  // scale chunks per tile
+  const int nbs = N / 128;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int ntiles = tiles_m * tiles_n;
+  const int nwg = gridDim.x;
+  auto tile_of = [&](int t, int& m0, int& n0) {
+    const int group = t / (GROUP_M_BIG * tiles_n);
+    const int first_m = group * GROUP_M_BIG;
+    const int gsize = min(tiles_m - first_m, GROUP_M_BIG);
+    m0 = (first_m + (t % gsize)) * BIG;
+    n0 = ((t % (GROUP_M_BIG * tiles_n)) / gsize) * BIG;
+  };
+  int t = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);
+  if (t >= ntiles) return;  // whole workgroup, before any barrier
+  int m0, n0;
+  tile_of(t, m0, n0);
+
+  const unsigned lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
+  const unsigned lsas = __builtin_amdgcn_readfirstlane(lds_addr(&sas[0][0][0]));
+  const unsigned lsbs = __builtin_amdgcn_readfirstlane(lds_addr(&sbs[0][0][0]));
+  // per-lane copy offsets of tile rows 8 (wave + 8u) + lane / 8 from the
+  // tile's first row (rows past `lim` clamped; their results are dropped)
+  auto offs = [&](int base, int lim, unsigned (&o)[4]) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int r = 8 * (wave + 8 * u) + (lane >> 3);
+      const int c = (lane & 7) ^ (((r >> 1) & 7) ^ ((r & 1) << 2));
+      o[u] = (unsigned)(min(base + r, lim - 1) - base) * (unsigned)K + c * 16;
+    }
+  };
+  unsigned offA[4], offB[4];
+  offs(m0, M, offA);
+  offs(n0, N, offB);
+  const uint8_t* tileA = A + (size_t)m0 * K;
+  const uint8_t* tileB = B + (size_t)n0 * K;
+  // scale chunk for K blocks kb0 .. kb0 + SCKB - 1 of tile (mm0, nn0), as in fp8_gemm_big
+  auto issue_scales = [&](int mm0, int nn0, int kb0, int buf) {
+    const int kb = min(kb0 + wave, KT - 1);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float* src = As + (size_t)min(mm0 + 64 * u + lane, M - 1) * KT + kb;
+      dma4(src, lsas + ((buf * SCKB + wave) * BIG + 64 * u) * 4);
+    }
+    if (wave == 0 && lane < 16) {
+      const float* src = Bs + (size_t)min(nn0 / 128 + (lane & 1), nbs - 1) * KT + min(kb0 + (lane >> 1), KT - 1);
+      dma4(src, lsbs + buf * SCKB * 2 * 4);
+    }
+  };
+  const int fsw = ((r16 >> 1) & 7) ^ ((r16 & 1) << 2);
+  const int la0 = (wm * 128 + r16) * BK + ((g ^ fsw) << 4);
+  const int la1 = (wm * 128 + r16) * BK + (((g + 4) ^ fsw) << 4);
+  const int lb0 = A_BYTES + (wn * 64 + r16) * BK + ((g ^ fsw) << 4);
+  const int lb1 = A_BYTES + (wn * 64 + r16) * BK + (((g + 4) ^ fsw) << 4);
+  const __amdgpu_buffer_rsrc_t crs = __builtin_amdgcn_make_buffer_rsrc(C, (short)0, M * N * 2, 0x00020000);
+
+  v4f acc[8][4];
+  issue_scales(m0, n0, 0, 0);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) dma16s(tileA, offA[u], lds0 + (wave + 8 * u) * 1024);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) dma16s(tileB, offB[u], lds0 + A_BYTES + (wave + 8 * u) * 1024);
+
+  int gk = 0;     // K blocks done by this workgroup (stage parity)
+  int cbase = 0;  // scale chunks done (scale buffer parity)
+  bool first = true;
+  for (;;) {
+    const int t_next = t + nwg;
+    const bool has_next = t_next < ntiles;
+    int m0n = m0, n0n = n0;
+    if (has_next) tile_of(t_next, m0n, n0n);
+    for (int kt = 0; kt < KT; ++kt, ++gk) {
+      // this wave's copies of block kt landed (the previous tile's 16 C
+      // stores, issued after them, may still be in flight)
+      if (first || kt > 0) wait_vm<0>();
+      else wait_vm<16>();
+      __syncthreads();  // everyone's copies landed; everyone is done with the other stage
+      const bool last = kt + 1 == KT;
+      const uint8_t* dA = tileA;
+      const uint8_t* dB = tileB;
+      int kn = min(kt + 1, KT - 1);  // the last tile's last block re-copies itself
+      if (!last && (kt + 1) % SCKB == 0) issue_scales(m0, n0, kt + 1, (cbase + (kt + 1) / SCKB) & 1);
+      if (last && has_next) {  // the next tile's first block and scale chunk
+        issue_scales(m0n, n0n, 0, (cbase + nch) & 1);
+        offs(m0n, M, offA);
+        offs(n0n, N, offB);
+        dA = A + (size_t)m0n * K;
+        dB = B + (size_t)n0n * K;
+        kn = 0;
+      }
+      const unsigned nbase = lds0 + ((gk + 1) & 1) * STAGE;
+      const uint8_t* st = smem + (gk & 1) * STAGE;
+      const int sbuf = (cbase + kt / SCKB) & 1, kc = kt % SCKB;
+      const float* sa = &sas[sbuf][kc][wm * 128 + r16];
+      const float bsv = sbs[sbuf][kc][wn >> 1];
+      v8i fb[4], fa[8];
+      float sc[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) fb[j] = frag(st + j * 2048, lb0, lb1);
+      fa[0] = frag(st, la0, la1);
+      sc[0] = sa[0] * bsv;
+      v4f tp[32];
+#pragma unroll
+      for (int k = 0; k < 34; ++k) {
+        if (k < 32) tp[k] = mfma_fp8(fb[k & 3], fa[k >> 2]);
+        if ((k & 1) == 0 && k < 16) {
+          const int u = (k >> 1) & 3;
+          if (k < 8) dma16s(dA + (size_t)kn * BK, offA[u], nbase + (wave + 8 * u) * 1024);
+          else dma16s(dB + (size_t)kn * BK, offB[u], nbase + A_BYTES + (wave + 8 * u) * 1024);
+        }
+        if ((k & 3) == 0 && (k >> 2) + 1 < 8) {
+          const int i1 = (k >> 2) + 1;
+          fa[i1] = frag(st + i1 * 2048, la0, la1);
+          sc[i1] = sa[16 * i1] * bsv;
+        }
+        if (k >= 2) {
+          const int p = k - 2;
+          if (kt == 0) {  // the tile's first K block starts the sums
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[p >> 2][p & 3][r] = tp[p][r] * sc[p >> 2];
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[p >> 2][p & 3][r] = fmaf(tp[p][r], sc[p >> 2], acc[p >> 2][p & 3][r]);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // ---- epilogue: bias, bf16 pairs, permlane16 swap, 16 stores per wave
+    float bv[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (HAS_BIAS) {
+        const float4 b4 = *reinterpret_cast<const float4*>(bias + n0 + wn * 64 + 16 * j + 4 * g);
+        bv[j][0] = b4.x; bv[j][1] = b4.y; bv[j][2] = b4.z; bv[j][3] = b4.w;
+      } else {
+        bv[j][0] = bv[j][1] = bv[j][2] = bv[j][3] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const unsigned row = (unsigned)(m0 + wm * 128 + 16 * i + r16);
+#pragma unroll
+      for (int jp = 0; jp < 2; ++jp) {
+        const v4f& x = acc[i][2 * jp];
+        const v4f& y = acc[i][2 * jp + 1];
+        const float* bx = bv[2 * jp];
+        const float* by = bv[2 * jp + 1];
+        const unsigned a0 = cvt_pk_bf16(x[0] + bx[0], x[1] + bx[1]), a1 = cvt_pk_bf16(x[2] + bx[2], x[3] + bx[3]);
+        const unsigned b0 = cvt_pk_bf16(y[0] + by[0], y[1] + by[1]), b1 = cvt_pk_bf16(y[2] + by[2], y[3] + by[3]);
+        // lanes of row group g: (a of g, a of g+1) for even g, (b of g-1, b of g) for odd g
+        const auto s0 = __builtin_amdgcn_permlane16_swap(a0, b0, false, false);
+        const auto s1 = __builtin_amdgcn_permlane16_swap(a1, b1, false, false);
+        const u32x4 d = {s0[0], s1[0], s0[1], s1[1]};
+        const unsigned col = (unsigned)(n0 + wn * 64 + 32 * jp + (g & 1) * 16 + (g >> 1) * 8);
+        __builtin_amdgcn_raw_buffer_store_b128(d, crs, (row * (unsigned)N + col) * 2u, 0, 0);
+      }
+    }
+    if (!has_next) break;
+    first = false;
+    t = t_next;
+    m0 = m0n;
+    n0 = n0n;
+    tileA = A + (size_t)m0 * K;
+    tileB = B + (size_t)n0 * K;
+    cbase += nch;
+  }
+  wait_vm<0>();  // the final re-copy lands before the workgroup's LDS is released
+}
+
 // out[m, n] = bf16(sum_s ws[s, m, n] + bias), four columns per thread
 __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ ws, int splits,
                                                      const float* __restrict__ bias, int64_t bias_ld,
@@ -787,6 +1005,17 @@ bool use_big_tiles(int64_t M, int64_t N, int64_t K) {
   return t >= cus && t * 100 >= rounds * cus * 85 && K >= 512 && 256 * K < (1ll << 31);
 }
 
+// The persistent 256x256 kernel: N a multiple of 256 (its stores write 16-byte
+// row segments and rely on the buffer range for rows only), a vector bias or
+// none, byte offsets of C and of a 256-row panel within 32 bits, and at
+// least half a round of 256x256 tiles (fewer leave most CUs idle; the
+// 128x128 kernel fills them).
+bool use_persistent(int64_t M, int64_t N, int64_t K, const float* bias, int64_t bias_ld) {
+  const int64_t t = ((M + BIG - 1) / BIG) * (N / BIG);
+  return N % BIG == 0 && bias_ld == 0 && ((uintptr_t)bias & 15u) == 0 && M * N * 2 < (1ll << 31) &&
+         256 * K < (1ll << 31) && K >= 256 && 2 * t >= cu_count();
+}
+
 int fp8_gemm_impl(const void* a, const float* a_s, const void* b, const float* b_s, const float* bias,
                   int64_t bias_ld, void* c, int64_t M, int64_t N, int64_t K, int32_t splits,
                   void* workspace, int64_t workspace_bytes, void* stream) {
@@ -818,6 +1047,17 @@ int fp8_gemm_impl(const void* a, const float* a_s, const void* b, const float* b
     kps = KT;
   }
   hipStream_t st = (hipStream_t)stream;
+  if (ws == nullptr && use_persistent(M, N, K, bias, bias_ld)) {
+    const int64_t bm = (M + BIG - 1) / BIG, bn = N / BIG;
+    const int nwg = (int)std::min<int64_t>(std::max(8, cu_count() / 8 * 8), (bm * bn + 7) / 8 * 8);
+    if (bias != nullptr)
+      hipLaunchKernelGGL(fp8_gemm_persist<true>, dim3((unsigned)nwg), dim3(512), 0, st, (const uint8_t*)a, a_s,
+                         (const uint8_t*)b, b_s, bias, (uint16_t*)c, (int)M, (int)N, (int)K, (int)bm, (int)bn);
+    else
+      hipLaunchKernelGGL(fp8_gemm_persist<false>, dim3((unsigned)nwg), dim3(512), 0, st, (const uint8_t*)a, a_s,
+                         (const uint8_t*)b, b_s, bias, (uint16_t*)c, (int)M, (int)N, (int)K, (int)bm, (int)bn);
+    return check_launch("fp8_gemm");
+  }
   if (ws == nullptr && use_big_tiles(M, N, K)) {
     const int64_t bm = (M + BIG - 1) / BIG, bn = (N + BIG - 1) / BIG;
     hipLaunchKernelGGL(fp8_gemm_big, dim3((unsigned)(bm * bn)), dim3(512), 0, st, (const uint8_t*)a, a_s,

@@ -289,6 +289,41 @@ def test_fp8_gemm_big_tiles_ragged(M, N, Kd):
         assert_close(got, gemm_oracle(a, a_s, b, b_s, bb, rows=rows), f"{M}x{N}x{Kd} {what}")
 
 
+@pytest.mark.parametrize("M,N,Kd", [(8000, 2304, 1152), (4000, 4096, 256), (16384, 1024, 640)])
+def test_fp8_gemm_persistent_tiles(M, N, Kd):
+    """Shapes the persistent 256x256 kernel takes (N a multiple of 256, at
+    least half a round of tiles): more tiles than workgroups, so a workgroup
+    runs several tiles and copies each next tile's first K block during the
+    last one (8000 x 2304: 288 tiles; 16384 x 1024: 256 tiles, one each);
+    ragged M (the last row tile is partial and its stores fall outside the
+    buffer range); 9, 2 and 5 K blocks (partial scale chunks, a single
+    block past the first); vector bias.  Sampled rows include both sides of
+    the tile boundaries near the edges."""
+    rng = np.random.default_rng(M + N + Kd)
+    ac = rng.integers(0, 256, (M, Kd), dtype=np.uint8)
+    bc = rng.integers(0, 256, (N, Kd), dtype=np.uint8)
+    ac[(ac & 0x7F) == 0x7F] = 0
+    bc[(bc & 0x7F) == 0x7F] = 0
+    a = torch.from_numpy(ac).view(torch.float8_e4m3fn).to(DEV)
+    b = torch.from_numpy(bc).view(torch.float8_e4m3fn).to(DEV)
+    a_s = torch.from_numpy(rng.uniform(1e-3, 1e-2, (M, Kd // 128)).astype(np.float32)).to(DEV)
+    b_s = torch.from_numpy(rng.uniform(1e-3, 1e-2, (N // 128, Kd // 128)).astype(np.float32)).to(DEV)
+    bias = torch.from_numpy(rng.standard_normal(N).astype(np.float32)).to(DEV)
+    edge = [0, 1, 255, 256, 511, 512, M - 257, M - 256, M - 2, M - 1]
+    rows = np.unique(np.concatenate([edge, rng.choice(M, 100, replace=False)]))
+    for bb, what in ((None, "nobias"), (bias, "bias")):
+        c = K.fp8_gemm(a, a_s, b, b_s, bb)
+        torch.cuda.synchronize()
+        assert_close(f32(c)[rows], gemm_oracle(a, a_s, b, b_s, bb, rows=rows), f"{M}x{N}x{Kd} {what}")
+        # every element against the 128x128 tile kernel (split-K path, same
+        # per-block products and folds: the same fp32 sums up to the order
+        # of the split partials)
+        ref = f32(K.fp8_gemm(a, a_s, b, b_s, bb, splits=2))
+        assert np.isfinite(f32(c)).all()
+        err = np.abs(f32(c) - ref)
+        assert (err <= ATOL + RTOL * np.abs(ref)).all(), f"{what}: persistent vs split-K max err {err.max()}"
+
+
 @pytest.mark.parametrize("M", [1, 16, 128, 4096])
 @pytest.mark.parametrize("KN", W.GEMM_KN)
 def test_fp8_gemm_cfg2_shapes(M, KN):
@@ -305,13 +340,22 @@ def test_fp8_gemm_cfg2_shapes(M, KN):
     assert_close(got, ref, f"M={M} K={Kd} N={N}")
 
 
-def test_fp8_gemm_m16384_sampled_rows():
-    Kd, N = 2048, 5632
-    x = W.activation(16384, Kd, seed=40).to(DEV)
+@pytest.mark.parametrize("KN", W.GEMM_KN)
+def test_fp8_gemm_m16384_sampled_rows(KN):
+    """The three cfg2 headline shapes at M = 16384 (the bench's launches):
+    sampled rows against the oracle, and the whole output finite and within
+    tolerance of the split-K 128x128 tile kernel on the same codes."""
+    Kd, N = KN
+    x = W.activation(16384, Kd, seed=40 + Kd).to(DEV)
     w = W.weight(N, Kd, seed=41).to(DEV)
     xq, xs = K.act_quant(x)
     wq, ws = K.weight_quant(w)
     c = K.fp8_gemm(xq, xs, wq, ws)
     torch.cuda.synchronize()
-    rows = np.concatenate([[0, 16383], np.random.default_rng(3).choice(16384, 126, replace=False)])
-    assert_close(f32(c)[rows], gemm_oracle(xq, xs, wq, ws, rows=rows), "M=16384")
+    rows = np.concatenate([[0, 255, 256, 16383], np.random.default_rng(3).choice(16384, 124, replace=False)])
+    assert_close(f32(c)[rows], gemm_oracle(xq, xs, wq, ws, rows=rows), f"M=16384 K={Kd} N={N}")
+    ref = f32(K.fp8_gemm(xq, xs, wq, ws, splits=2))
+    got = f32(c)
+    assert np.isfinite(got).all()
+    err = np.abs(got - ref)
+    assert (err <= ATOL + RTOL * np.abs(ref)).all(), f"vs split-K: max err {err.max()}"
