@@ -9,7 +9,9 @@
  *     failure on the calling thread.
  *   - `stream` is a hipStream_t (NULL = the default stream).  Work is only
  *     enqueued: nothing synchronises, allocates or frees.  The caller owns
- *     every buffer, including the paged-decode workspace.
+ *     every buffer, including the paged-decode workspace (except
+ *     lfs_paged_decode_noalloc, whose workspace is a library-owned static
+ *     device array).
  *   - Device pointers must be 16-byte aligned unless stated otherwise.
  *   - bf16 buffers hold uint16 bit patterns; fp8 buffers hold OCP
  *     float8_e4m3fn bytes (torch.float8_e4m3fn).
@@ -38,6 +40,9 @@
  *                           decode call of the same absent layer; math of
  *                           model/attention/GQA.py:118-130, metadata contract
  *                           engine/model_runner.py:253-278 and :288-312
+ *   lfs_paged_decode_noalloc  the same decode with a library-owned static
+ *                           workspace; no reference counterpart (for callers
+ *                           that cannot allocate)
  *   lfs_prefill_attention   varlen causal prefill attention, the
  *                           flash_attn_varlen_func(..., causal=True) call the
  *                           reference names at engine/model_runner.py:291-292
@@ -86,7 +91,7 @@
 extern "C" {
 #endif
 
-#define LFS_ABI_VERSION 9
+#define LFS_ABI_VERSION 10
 
 /* argument errors (negative); launch errors are positive hipError_t values */
 #define LFS_EINVAL (-1)
@@ -210,6 +215,29 @@ int lfs_paged_decode(const void* q, const void* k_cache, const void* v_cache,
                      int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                      int32_t block_size, int64_t num_blocks, int32_t max_blocks, float scale,
                      int32_t blocks_per_split, void* q_out, float* q_scale, void* stream);
+
+/*
+ * lfs_paged_decode without a caller workspace: the split partials live in a
+ * library-owned device array of LFS_DECODE_SCRATCH_BYTES per GPU (allocated
+ * when the library's code object loads on that GPU, held until the process
+ * ends); the call allocates and frees nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops).  Same arguments, result and
+ * kernels as lfs_paged_decode; a shape whose
+ * lfs_paged_decode_workspace_bytes(...) exceeds LFS_DECODE_SCRATCH_BYTES is
+ * rejected with LFS_EINVAL (cfg4's B 256, Hq 32, D 128 needs 42.6 MB on 256
+ * CUs).  Every call on one GPU shares that GPU's array: calls that overlap
+ * on one GPU (two streams, two threads) race and must be serialised by the
+ * caller.
+ */
+#define LFS_DECODE_SCRATCH_BYTES (64ll << 20)
+
+int lfs_paged_decode_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                             const int64_t* context_lens, const int32_t* block_tables, int64_t bt_stride,
+                             void* out, int64_t B, int32_t num_q_heads, int32_t num_kv_heads,
+                             int32_t head_dim, int32_t block_size, int64_t num_blocks, int32_t max_blocks,
+                             float scale, int32_t blocks_per_split, void* q_out, float* q_scale,
+                             void* stream);
 
 /*
  * Varlen causal prefill attention, GQA (G = Hq / Hkv):

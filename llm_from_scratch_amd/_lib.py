@@ -11,7 +11,9 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "liblfs_kernels.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
+# size of the library's static paged-decode workspace (LFS_DECODE_SCRATCH_BYTES)
+DECODE_SCRATCH_BYTES = 64 << 20
 
 _c_i64, _c_i32, _c_p, _c_f = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p, ctypes.c_float
 
@@ -35,6 +37,8 @@ SIGNATURES = {
     "lfs_paged_decode": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64,
                                         _c_i32, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_f, _c_i32,
                                         _c_p, _c_p, _c_p]),
+    "lfs_paged_decode_noalloc": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i32, _c_i32,
+                                                _c_i32, _c_i32, _c_i64, _c_i32, _c_f, _c_i32, _c_p, _c_p, _c_p]),
     "lfs_add_rmsnorm": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_f, _c_p]),
     "lfs_qk_norm_rope_store": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
                                               _c_i64, _c_i32, _c_i32, _c_i32, _c_i64, _c_i64, _c_f, _c_p]),

@@ -23,6 +23,8 @@
 //   of the bf16 output row (the output projection's FP8 input).
 #include "common.h"
 
+#include <mutex>
+
 namespace lfs {
 namespace {
 
@@ -833,13 +835,14 @@ extern "C" int64_t lfs_paged_decode_workspace_bytes(int64_t B, int32_t num_q_hea
   return 4 * B * splits * (int64_t)num_q_heads * ((int64_t)head_dim + 2);
 }
 
-extern "C" int lfs_paged_decode(const void* q, const void* k_cache, const void* v_cache,
-                                const int64_t* context_lens, const int32_t* block_tables,
-                                int64_t bt_stride, void* out, void* workspace,
-                                int64_t workspace_bytes, int64_t B, int32_t num_q_heads,
-                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                                int64_t num_blocks, int32_t max_blocks, float scale,
-                                int32_t blocks_per_split, void* q_out, float* q_scale, void* stream) {
+namespace {
+// Argument checks, then the split (balanced or fixed chunks) and the merge.
+// `noalloc` only changes the wording of the workspace error.
+int paged_decode_impl(const void* q, const void* k_cache, const void* v_cache, const int64_t* context_lens,
+                      const int32_t* block_tables, int64_t bt_stride, void* out, void* workspace,
+                      int64_t workspace_bytes, int64_t B, int32_t num_q_heads, int32_t num_kv_heads,
+                      int32_t head_dim, int32_t block_size, int64_t num_blocks, int32_t max_blocks, float scale,
+                      int32_t blocks_per_split, void* q_out, float* q_scale, void* stream, bool noalloc) {
   const int Hq = num_q_heads, Hkv = num_kv_heads, D = head_dim, BS = block_size;
   LFS_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && BS > 0 && num_blocks >= 0 && max_blocks >= 0,
               "paged_decode: bad shape");
@@ -862,6 +865,10 @@ extern "C" int lfs_paged_decode(const void* q, const void* k_cache, const void* 
   LFS_REQUIRE(q_out == nullptr || (Hq * D % 128 == 0 && Hq * D <= MQ_MAXE && Hq <= MQ_MAXH),
               "paged_decode: the quantised output needs Hq*D %% 128 == 0, Hq*D <= %d", MQ_MAXE);
   const int64_t need = lfs_paged_decode_workspace_bytes(B, Hq, D, max_blocks, blocks_per_split);
+  LFS_REQUIRE(!noalloc || need <= workspace_bytes,
+              "paged_decode_noalloc: this shape needs %lld bytes of workspace, more than the library's "
+              "static scratch of %lld bytes (call lfs_paged_decode with a caller-owned workspace)",
+              (long long)need, (long long)workspace_bytes);
   LFS_REQUIRE(workspace_bytes >= need && (need == 0 || workspace),
               "paged_decode: workspace of %lld bytes < required %lld", (long long)workspace_bytes,
               (long long)need);
@@ -922,6 +929,68 @@ extern "C" int lfs_paged_decode(const void* q, const void* k_cache, const void* 
     if (rc) return rc;
   }
   return paged_decode_merge_launch(ws_o, ws_ml, context_lens, out, q_out, q_scale, B, Hq, D, BS, max_blocks, pm, st);
+}
+
+// Workspace of lfs_paged_decode_noalloc: one array per GPU, allocated when the
+// code object is loaded on that GPU and held until the process ends.  Host
+// code never passes `scratch` itself to a kernel (in host code the name is a
+// stand-in, not a device address); it passes the address hipGetSymbolAddress
+// returns for the current device, looked up once per device.
+constexpr int64_t kDecodeScratchBytes = LFS_DECODE_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kDecodeScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// device address of the current device's scratch array (nullptr + message on failure)
+void* device_scratch() {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("paged_decode_noalloc: no current device (%s)", hipGetErrorString(e));
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("paged_decode_noalloc: hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
+                hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" int lfs_paged_decode(const void* q, const void* k_cache, const void* v_cache,
+                                const int64_t* context_lens, const int32_t* block_tables,
+                                int64_t bt_stride, void* out, void* workspace,
+                                int64_t workspace_bytes, int64_t B, int32_t num_q_heads,
+                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                int64_t num_blocks, int32_t max_blocks, float scale,
+                                int32_t blocks_per_split, void* q_out, float* q_scale, void* stream) {
+  return paged_decode_impl(q, k_cache, v_cache, context_lens, block_tables, bt_stride, out, workspace,
+                           workspace_bytes, B, num_q_heads, num_kv_heads, head_dim, block_size, num_blocks,
+                           max_blocks, scale, blocks_per_split, q_out, q_scale, stream, false);
+}
+
+extern "C" int lfs_paged_decode_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                        const int64_t* context_lens, const int32_t* block_tables,
+                                        int64_t bt_stride, void* out, int64_t B, int32_t num_q_heads,
+                                        int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                        int64_t num_blocks, int32_t max_blocks, float scale,
+                                        int32_t blocks_per_split, void* q_out, float* q_scale, void* stream) {
+  // the kernels fully rewrite the part of the workspace they read (tile scan,
+  // partial rows): nothing in it has to start at zero
+  void* ws = device_scratch();
+  if (ws == nullptr) return LFS_EINVAL;
+  return paged_decode_impl(q, k_cache, v_cache, context_lens, block_tables, bt_stride, out, ws,
+                           kDecodeScratchBytes, B, num_q_heads, num_kv_heads, head_dim, block_size, num_blocks,
+                           max_blocks, scale, blocks_per_split, q_out, q_scale, stream, true);
 }
 
 namespace {

@@ -337,6 +337,45 @@ def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     return (o, oq, os_) if quant else o
 
 
+def paged_attention_decode_noalloc(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                                   context_lens: torch.Tensor, block_tables: torch.Tensor,
+                                   scale: Optional[float] = None, blocks_per_split: Optional[int] = None,
+                                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """paged_attention_decode with the split workspace taken from the
+    library's static device array (lfs_paged_decode_noalloc): the C call
+    allocates nothing, so with a preallocated ``out`` the whole call
+    allocates nothing.  Raises ValueError when the shape needs more than
+    _lib.DECODE_SCRATCH_BYTES of workspace.  Calls that overlap on one GPU
+    share the array and race."""
+    assert q.dim() == 3 and q.is_contiguous(), "q must be contiguous [B, Hq, D]"
+    assert k_cache.is_contiguous() and v_cache.is_contiguous() and k_cache.shape == v_cache.shape
+    assert k_cache.dim() == 4, "caches must be [num_blocks, block_size, Hkv, D]"
+    assert block_tables.dim() == 2 and block_tables.stride(1) == 1, "block_tables must be [B, max_blocks]"
+    assert context_lens.is_contiguous() and context_lens.numel() == q.size(0)
+    _on_gpu(q, k_cache, v_cache, context_lens, block_tables)
+    for t, n in ((q, "q"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _dtype(t, torch.bfloat16, n)
+    _dtype(context_lens, torch.int64, "context_lens")
+    _dtype(block_tables, torch.int32, "block_tables")
+    B, Hq, D = q.shape
+    NB, BS, Hkv, Dk = k_cache.shape
+    assert Dk == D, "head_dim mismatch between q and the caches"
+    assert block_tables.size(0) == B
+    max_blocks = block_tables.size(1)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    bps = default_blocks_per_split(B, Hkv, max_blocks, BS) if blocks_per_split is None else blocks_per_split
+    if out is None:
+        out = torch.empty_like(q)
+    assert out.shape == q.shape and out.dtype == torch.bfloat16 and out.is_contiguous()
+    rc = _lib.load().lfs_paged_decode_noalloc(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(context_lens),
+                                              _ptr(block_tables), block_tables.stride(0), _ptr(out),
+                                              B, Hq, Hkv, D, BS, NB, max_blocks, float(scale), bps,
+                                              None, None, _stream(q))
+    _lib.check(rc, "paged_attention_decode_noalloc")
+    return out
+
+
 def flash_attn_varlen_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                            cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor,
                            max_seqlen_q: int, max_seqlen_k: int, softmax_scale: Optional[float] = None,
