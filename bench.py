@@ -8,17 +8,26 @@ M in {4096, 16384} x (K, N) in {(1024,4096), (4096,1024), (2048,5632)} with
 1x128 activation / 128x128 weight scales, inputs already quantised and
 resident in HBM.  ``roofline`` prices the GEMM against the dense FP8 MFMA
 peak (5.0 PFLOP/s); each launch is bracketed by HIP events on the stream it
-runs on.  ``paged_decode`` (cfg3 and cfg4) and ``act_quant`` report HBM
-GB/s against 8 TB/s, with the 256 MB last-level cache flushed between timed
-decode calls.  ``cpu_baseline`` times the numpy oracle (blockwise fp32 GEMM)
-on the host for the three M=4096 shapes.
+runs on.  ``roofline_decode`` prices the paged decode of cfg3 (the other half
+of the metric) against 8 TB/s.  ``paged_decode`` (cfg3, cfg3_4k, cfg4),
+``act_quant`` (every cfg2 (M, K)), ``store_kvcache`` and the decode-sized
+GEMMs report HBM GB/s against 8 TB/s with the 256 MB last-level cache
+flushed before every timed call.  ``traffic`` and ``kernel_us`` figures come
+from the rocprofv3 summaries under profiles/, used only when the kernel
+source they were measured on is the one built (sha256 recorded there).
+``cpu_baseline`` times the CPU restatements on all host cores (1 warm-up,
+median of 5; 3 for cfg4): the numpy oracle's blockwise fp32 GEMM on the
+three M=4096 shapes (the headline ``value``), plus act_quant, paged decode
+(cfg3, a 16-sequence cfg4 subset) and store_kvcache in torch CPU ops.
 """
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import math
 import os
+import re
 import sys
 import time
 
@@ -28,13 +37,34 @@ import torch
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
 METRIC = "FP8 block-GEMM TFLOP/s & paged-decode HBM GB/s (% of MI355X roofline)"
-# Fabric bytes per fp8_gemm launch, averaged over the six headline shapes,
-# from two rocprofv3 --pmc runs of this script (FETCH_SIZE, then WRITE_SIZE;
-# `--no-cpu --extras act_quant,cfg3 --steps 3 --warmup 1 --copy-calibration`),
-# summarised in profiles/fp8_gemm_cfg2_sweep.md.  FETCH_SIZE is scaled by 2.0
-# and WRITE_SIZE by 1.0: a 256 MiB device copy in the same runs reads back
-# 128 MiB fetched and 256 MiB written.  Re-measure after kernel changes.
-GEMM_TRAFFIC_BYTES = 187.7e6
+REPO = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(REPO, "llm_from_scratch_amd", "csrc")
+PROFILES = os.path.join(REPO, "profiles")
+
+
+def source_sha(name: str) -> str:
+    with open(os.path.join(CSRC, name), "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
+
+
+def profile_figures(md: str, key: str, source: str) -> dict:
+    """Figures a rocprofv3 summary under profiles/ records for `key`, in a
+    line ``<!-- bench key=... source=<file> sha=<16 hex> name=value ... -->``.
+    Returned only if that sha is the current source's, so a kernel change
+    makes them null until the PMC runs are repeated."""
+    path = os.path.join(PROFILES, md)
+    try:
+        text = open(path).read()
+    except OSError:
+        return {"stale": "no profile " + md}
+    for m in re.finditer(r"<!-- bench (.*?) -->", text):
+        kv = dict(item.split("=", 1) for item in m.group(1).split())
+        if kv.get("key") != key:
+            continue
+        if kv.get("sha") != source_sha(source):
+            return {"stale": f"{md}: measured on {source} sha {kv.get('sha')}, built {source_sha(source)}"}
+        return {k: float(v) for k, v in kv.items() if k not in ("key", "source", "sha")}
+    return {"stale": f"{md}: no entry {key}"}
 
 
 def log(*a):
@@ -100,17 +130,74 @@ def bench_gemm(cases, steps, warmup):
 
 
 def bench_act_quant(device, reps, flush_buf):
-    """act_quant over a 16384 x 4096 bf16 input (134 MB: it would fit in the
-    256 MB Infinity Cache, so a 512 MB write evicts it before every call)."""
+    """act_quant over every cfg2 activation shape (M in {1, 16, 128, 4096,
+    16384} x K in {1024, 4096, 2048}), the 512 MB flush before every call
+    (16384 x 4096 is 134 MB and would sit in the Infinity Cache).
+    Algorithmic bytes: 2 read + 1 written per element + 4 per 128-group."""
     from llm_from_scratch_amd import kernels as K
     from llm_from_scratch_amd import workloads as W
-    M, Kd = 16384, 4096
-    x = W.activation(M, Kd, seed=77, device=device)
-    K.act_quant(x)
-    t = timed_launches([lambda: K.act_quant(x)], reps, flush=lambda: flush_buf.add_(1))[0]
-    nbytes = 3 * M * Kd + 4 * M * Kd // 128
-    return {"shape": [M, Kd], "us": t * 1e6, "GB/s": nbytes / t / 1e9,
-            "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "bytes": nbytes}
+    out = []
+    for M in W.GEMM_M:
+        for Kd in sorted({kd for kd, _ in W.GEMM_KN}):
+            x = W.activation(M, Kd, seed=77 + M + Kd, device=device)
+            K.act_quant(x)
+            t = timed_launches([lambda: K.act_quant(x)], reps, flush=lambda: flush_buf.add_(1))[0]
+            nbytes = 3 * M * Kd + 4 * M * Kd // 128
+            out.append({"shape": [M, Kd], "us": t * 1e6, "GB/s": nbytes / t / 1e9,
+                        "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "bytes": nbytes})
+            del x
+    prof = profile_figures("act_quant_16384x4096.md", "act_quant_16384x4096", "quant.hip")
+    for o in out:
+        if o["shape"] == [16384, 4096]:
+            o["kernel_us_rocprof"] = prof.get("kernel_us", prof.get("stale"))
+    return out
+
+
+def bench_cfg1(device, reps):
+    """cfg1 latency: one FP8 linear (act_quant of x [256, 512], fp8_gemm with
+    the 128x128-quantised W [1344, 512]), inputs resident, no flush."""
+    from llm_from_scratch_amd import kernels as K
+    from llm_from_scratch_amd import workloads as W
+    x = W.activation(256, 512, seed=0, outliers=False, device=device)
+    wq, ws = K.weight_quant(W.weight(1344, 512, seed=100, device=device))
+
+    def fn():
+        xq, xs = K.act_quant(x)
+        return K.fp8_gemm(xq, xs, wq, ws)
+
+    fn()
+    t = timed_launches([fn], reps)[0]
+    fl = 2.0 * 256 * 1344 * 512
+    return {"shape": {"M": 256, "K": 512, "N": 1344}, "us": t * 1e6, "TFLOP/s": fl / t / 1e12,
+            "launches": 2}
+
+
+def bench_store_kvcache(device, reps, flush_buf):
+    """store_kvcache of one decode step: cfg3 (64 tokens, 4 kv heads x 64)
+    and cfg4 (256 tokens, 8 x 128) into the full pools at the decode slots.
+    Algorithmic bytes: K and V rows read and written, slots read."""
+    from llm_from_scratch_amd import kernels as K
+    from llm_from_scratch_amd import workloads as W
+    out = []
+    for name, seed in (("cfg3", 2), ("cfg4", 3)):
+        case = W.paged_case(name, seed=seed)
+        shape = (case.num_blocks, case.block_size, case.num_kv_heads, case.head_dim)
+        kc = torch.empty(shape, dtype=torch.bfloat16, device=device)
+        vc = torch.empty(shape, dtype=torch.bfloat16, device=device)
+        g = torch.Generator(device=device).manual_seed(6)
+        T = case.batch
+        k = torch.randn(T, case.num_kv_heads, case.head_dim, generator=g, device=device).to(torch.bfloat16)
+        v = torch.randn(T, case.num_kv_heads, case.head_dim, generator=g, device=device).to(torch.bfloat16)
+        slots = torch.from_numpy(case.slot_mapping).to(device)
+        fn = lambda: K.store_kvcache(k, v, kc, vc, slots)  # noqa: E731
+        fn()
+        t = timed_launches([fn], reps, flush=lambda: flush_buf.add_(1))[0]
+        nbytes = 2 * (T * case.num_kv_heads * case.head_dim * 2) * 2 + 8 * T
+        out.append({"config": name, "tokens": T, "us": t * 1e6, "GB/s": nbytes / t / 1e9,
+                    "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "bytes": nbytes, "bound": "latency"})
+        del kc, vc
+        torch.cuda.empty_cache()
+    return out
 
 
 BF16_PEAK_TFLOPS = 2500.0
@@ -257,6 +344,15 @@ def bench_decode(name, device, reps, flush_buf):
            "head_dim": case.head_dim, "tokens": int(case.context_lens.sum()), "us": t * 1e6,
            "GB/s": nbytes / t / 1e9, "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "bytes": nbytes,
            "blocks_per_split": bps}
+    # split + merge kernel time and fabric bytes of the same call from the
+    # rocprofv3 summary (the event window also holds the launch gap)
+    prof = profile_figures("paged_decode_cfg3_cfg4.md", "paged_decode_" + name, "paged_kv.hip")
+    if "stale" in prof:
+        out["rocprof"] = prof
+    else:
+        out["kernel_us_rocprof"] = prof["kernel_us"]
+        out["kernel_frac"] = nbytes / (prof["kernel_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS
+        out["traffic"] = prof.get("traffic")
     del kc, vc
     torch.cuda.empty_cache()
     return out
@@ -314,28 +410,137 @@ def bench_decode_step(device, reps):
     return out
 
 
-def cpu_baseline():
-    """Numpy oracle (blockwise fp32 GEMM, one matmul per 128-wide K block with
-    the scale product applied to the partial) on the three M=4096 shapes."""
+def _median_time(fn, runs: int, warmup: int = 1) -> float:
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def _cpu_act_quant(x):
+    """act_quant in torch CPU ops, the formula of oracle.fp8.act_quant
+    (model/attention/utils.py:129-139): amax per 128-group, clamp 1e-4,
+    times fp32(1/448), IEEE divide, clamp +-448, RNE cast to e4m3fn."""
+    g = x.float().view(x.shape[0], -1, 128)
+    s = g.abs().amax(-1).clamp_min(1e-4) * torch.tensor(1.0 / 448.0, dtype=torch.float32)
+    y = (g / s[..., None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return y.view(x.shape), s
+
+
+def _cpu_decode(q, kc, vc, lens, bt, scale, BS):
+    """Paged GQA decode in torch CPU fp32: gather each sequence's K/V rows
+    through its block table, softmax(scale q K^T) V per kv head (the math of
+    oracle.paged_kv.paged_decode, model/attention/GQA.py:118-130)."""
+    B, Hq, D = q.shape
+    Hkv = kc.shape[2]
+    G = Hq // Hkv
+    o = torch.zeros(B, Hq, D)
+    for b in range(B):
+        L = int(lens[b])
+        nb = -(-L // BS)
+        blocks = torch.from_numpy(bt[b, :nb].astype(np.int64))
+        Kb = kc[blocks].reshape(-1, Hkv, D)[:L].float().permute(1, 2, 0)  # [Hkv, D, L]
+        Vb = vc[blocks].reshape(-1, Hkv, D)[:L].float().permute(1, 0, 2)  # [Hkv, L, D]
+        qh = q[b].float().view(Hkv, G, D)
+        p = torch.softmax(torch.matmul(qh, Kb) * scale, dim=-1)
+        o[b] = torch.matmul(p, Vb).reshape(Hq, D)
+    return o
+
+
+def _compact_case(name, seed, nseq=None):
+    """cfg3 / cfg4 metadata with the pool compacted to the referenced blocks
+    (tables remapped), K/V ~N(0,1) bf16 on the host."""
+    from llm_from_scratch_amd import workloads as W
+    case = W.paged_case(name, seed=seed)
+    lens = case.context_lens[:nseq] if nseq else case.context_lens
+    bt = case.block_tables[:len(lens)]
+    used = np.unique(bt[bt >= 0])
+    remap = np.full(case.num_blocks, -1, np.int64)
+    remap[used] = np.arange(len(used))
+    bt_c = np.where(bt >= 0, remap[np.maximum(bt, 0)], -1)
+    g = torch.Generator().manual_seed(seed)
+    shape = (len(used), case.block_size, case.num_kv_heads, case.head_dim)
+    kc = torch.randn(shape, generator=g).to(torch.bfloat16)
+    vc = torch.randn(shape, generator=g).to(torch.bfloat16)
+    q = torch.randn(len(lens), case.num_q_heads, case.head_dim, generator=g).to(torch.bfloat16)
+    return case, lens, bt_c, kc, vc, q
+
+
+def cpu_baseline(device):
+    """CPU restatements on all host cores (1 warm-up, median of 5; 3 for
+    cfg4): the headline is the numpy oracle's blockwise fp32 GEMM on the
+    three cfg2 M=4096 shapes; act_quant, paged decode and store_kvcache run
+    the same formulas in torch CPU ops.  The act_quant codes and the decode
+    output are checked against the GPU on the same inputs (bit-exact codes;
+    decode within the 1e-2 / 2e-2 bar)."""
     from threadpoolctl import threadpool_limits
     from oracle import fp8 as F
+    from llm_from_scratch_amd import kernels as K
     from llm_from_scratch_amd import workloads as W
-    threads = min(16, os.cpu_count() or 1)
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    t_start = time.perf_counter()
+    out = {"unit": "TFLOP/s", "cores": cores, "kind": "port"}
     flops, secs = 0.0, 0.0
-    with threadpool_limits(threads):
+    with threadpool_limits(cores):
         for Kd, N in W.GEMM_KN:
             M = 4096
-            x = W.activation(M, Kd, seed=1 + M + Kd).float().numpy()
-            w = W.weight(N, Kd, seed=31 + Kd).float().numpy()
-            a, a_s = F.act_quant(x)
-            b, b_s = F.weight_quant(w)
-            t0 = time.perf_counter()
-            F.fp8_gemm(a, a_s, b, b_s, accum=np.float32)
-            secs += time.perf_counter() - t0
+            a, a_s = F.act_quant(W.activation(M, Kd, seed=1 + M + Kd).float().numpy())
+            b, b_s = F.weight_quant(W.weight(N, Kd, seed=31 + Kd).float().numpy())
+            secs += _median_time(lambda: F.fp8_gemm(a, a_s, b, b_s, accum=np.float32), 5)
             flops += 2.0 * M * N * Kd
-    return {"value": flops / secs / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": "numpy oracle fp8_gemm (blockwise fp32) on cfg2 M=4096 x 3 (K,N) shapes, "
-                      f"{secs:.1f} s"}
+    out["value"] = flops / secs / 1e12
+    out["gemm_s_per_step"] = secs
+
+    # act_quant: 2048 x 4096 rows of the cfg2 activation (1/8 of the GPU line's 16384 rows)
+    x = W.activation(2048, 4096, seed=78)
+    t = _median_time(lambda: _cpu_act_quant(x), 5)
+    nbytes = 3 * x.numel() + 4 * x.numel() // 128
+    yc, sc = _cpu_act_quant(x)
+    yg, sg = K.act_quant(x.to(device))
+    same = bool(torch.equal(yc.view(torch.uint8), yg.view(torch.uint8).cpu()) and torch.equal(sc, sg.cpu()))
+    out["act_quant"] = {"sample": "2048x4096 (GPU line: up to 16384x4096)", "GB/s": nbytes / t / 1e9,
+                        "s": t, "codes_equal_gpu": same}
+
+    # paged decode: cfg3 whole batch; cfg4 its first 16 sequences (compacted pools)
+    out["paged_decode"] = []
+    for name, seed, nseq, runs in (("cfg3", 2, None, 5), ("cfg4", 3, 16, 3)):
+        case, lens, bt, kc, vc, q = _compact_case(name, seed, nseq)
+        t = _median_time(lambda: _cpu_decode(q, kc, vc, lens, bt, case.scale, case.block_size), runs)
+        nbytes = int(lens.sum()) * case.num_kv_heads * case.head_dim * 2 * 2 + \
+            2 * len(lens) * case.num_q_heads * case.head_dim * 2 + 4 * bt.size + 8 * len(lens)
+        ref = _cpu_decode(q, kc, vc, lens, bt, case.scale, case.block_size)
+        dev_bt = torch.from_numpy(bt.astype(np.int32)).to(device)
+        got = K.paged_attention_decode(q.to(device), kc.to(device), vc.to(device),
+                                       torch.from_numpy(lens.astype(np.int64)).to(device), dev_bt, case.scale)
+        err = (got.float().cpu() - ref).abs()
+        ok = bool((err <= 2e-2 + 1e-2 * ref.abs()).all())
+        out["paged_decode"].append({"config": name, "sample": f"{len(lens)} sequences, {int(lens.sum())} tokens",
+                                    "GB/s": nbytes / t / 1e9, "s": t, "runs": runs, "matches_gpu": ok})
+        del kc, vc
+
+    # store_kvcache: cfg3's 64 decode slots into the compacted cfg3 pool (index_copy_)
+    case, lens, bt, kc, vc, q = _compact_case("cfg3", 2)
+    slots = torch.from_numpy((bt[np.arange(len(lens)), (lens - 1) // case.block_size] * case.block_size
+                              + (lens - 1) % case.block_size).astype(np.int64))
+    kf, vf = kc.view(-1, case.num_kv_heads, case.head_dim), vc.view(-1, case.num_kv_heads, case.head_dim)
+    kn, vn = q[:, :case.num_kv_heads].contiguous(), q[:, case.num_kv_heads:2 * case.num_kv_heads].contiguous()
+
+    def store():
+        for _ in range(100):
+            kf.index_copy_(0, slots, kn)
+            vf.index_copy_(0, slots, vn)
+
+    t = _median_time(store, 5) / 100
+    nbytes = 2 * kn.numel() * 2 * 2 + 8 * len(slots)
+    out["store_kvcache"] = {"config": "cfg3", "tokens": len(slots), "us": t * 1e6, "GB/s": nbytes / t / 1e9}
+    out["sample"] = ("GEMM: numpy oracle fp8_gemm (blockwise fp32) on cfg2 M=4096 x 3 (K,N), median of 5; "
+                     f"{time.perf_counter() - t_start:.1f} s of CPU baselines in total")
+    return out
 
 
 def main():
@@ -345,10 +550,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip decode / act_quant lines")
-    ap.add_argument("--extras", default="act_quant,gemm_small,cfg3,cfg3_4k,cfg4,prefill,indexer,moe,cfg5",
-                    help="comma list of extra lines: act_quant, cfg3, cfg4 (paged decode), prefill "
-                         "(varlen prefill attention), indexer (DSA fp8_index), moe (MoE layer, grouped "
-                         "vs dense dispatch), cfg5 (decode step)")
+    ap.add_argument("--extras",
+                    default="cfg1,act_quant,gemm_small,store_kvcache,cfg3,cfg3_4k,cfg4,prefill,indexer,moe,cfg5",
+                    help="comma list of extra lines: cfg1 (FP8 linear latency), act_quant (every cfg2 "
+                         "shape), gemm_small (cfg2 M <= 128), store_kvcache, cfg3, cfg3_4k, cfg4 (paged "
+                         "decode), prefill (varlen prefill attention), indexer (DSA fp8_index), moe (MoE "
+                         "layer, grouped vs dense dispatch), cfg5 (decode step)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 4 plain device copies of 256 MiB (a known-traffic kernel for "
                          "scaling FETCH_SIZE / WRITE_SIZE counters)")
@@ -381,6 +588,9 @@ def main():
                "TFLOP/s": c["flops"] / t / 1e12, "frac": c["flops"] / t / 1e12 / FP8_PEAK_TFLOPS}
               for c, t in zip(cases, per)]
     alg_bytes = sum(c["bytes"] for c in cases) / len(cases)
+    # fabric bytes per launch (average over the six launches) from the PMC
+    # runs summarised in profiles/, if measured on the kernel source built
+    gprof = profile_figures("fp8_gemm_cfg2_sweep.md", "fp8_gemm_cfg2", "fp8_gemm.hip")
     del cases
     torch.cuda.empty_cache()
     out = {
@@ -402,26 +612,46 @@ def main():
                    "launches_per_step": len(per)},
         "roofline": {"bound": "mfma", "kernel": "fp8_gemm", "achieved": achieved,
                      "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": achieved / FP8_PEAK_TFLOPS,
-                     "traffic": GEMM_TRAFFIC_BYTES,
+                     "traffic": gprof.get("traffic"),
                      "algorithmic_bytes": alg_bytes},
         "gemm_shapes": shapes,
     }
+    if "stale" in gprof:
+        out["roofline"]["traffic_note"] = gprof["stale"]
+    else:
+        out["roofline"]["kernel_us_rocprof"] = gprof.get("kernel_us")
     try:
         decode = [n for n in ("cfg3", "cfg3_4k", "cfg4") if n in extras]
-        if decode or "act_quant" in extras or "gemm_small" in extras:
+        flushed = decode or extras & {"act_quant", "gemm_small", "store_kvcache"}
+        if flushed:
             flush_buf = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev).zero_()
+        if "cfg1" in extras:
+            log("bench: cfg1 FP8 linear latency")
+            out["cfg1_linear"] = bench_cfg1(dev, 20)
         if "act_quant" in extras:
             log("bench: act_quant")
             out["act_quant"] = bench_act_quant(dev, 20, flush_buf)
         if "gemm_small" in extras:
             log("bench: fp8_gemm at M <= 128")
             out["gemm_small"] = bench_gemm_small(dev, 20, flush_buf)
+        if "store_kvcache" in extras:
+            log("bench: store_kvcache")
+            out["store_kvcache"] = bench_store_kvcache(dev, 20, flush_buf)
         if decode:
             out["paged_decode"] = []
             for name in decode:
                 log(f"bench: paged decode {name}")
                 out["paged_decode"].append(bench_decode(name, dev, 20, flush_buf))
-        if decode or "act_quant" in extras or "gemm_small" in extras:
+            c3 = [d for d in out["paged_decode"] if d["config"] == "cfg3"]
+            if c3:  # the decode half of the metric: cfg3 against 8 TB/s
+                d = c3[0]
+                out["roofline_decode"] = {"bound": "hbm", "kernel": "paged_decode (split + merge)",
+                                          "workload": "cfg3", "achieved": d["GB/s"], "peak": HBM_PEAK_GBS,
+                                          "unit": "GB/s", "frac": d["frac"], "traffic": d.get("traffic"),
+                                          "algorithmic_bytes": d["bytes"],
+                                          "kernel_us_rocprof": d.get("kernel_us_rocprof"),
+                                          "kernel_frac": d.get("kernel_frac")}
+        if flushed:
             del flush_buf
             torch.cuda.empty_cache()
         if "indexer" in extras:
@@ -440,7 +670,7 @@ def main():
         out["extra_error"] = repr(e)
     if not args.no_cpu:
         log("bench: cpu baseline")
-        out["cpu_baseline"] = cpu_baseline()
+        out["cpu_baseline"] = cpu_baseline(dev)
     print(json.dumps(out), flush=True)
 
 
