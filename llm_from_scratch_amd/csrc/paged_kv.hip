@@ -94,6 +94,28 @@ __device__ __forceinline__ uint4 nt_load16(const uint16_t* p) {
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
+// Reductions over lanes l, l^16 (and l^32) without LDS: v_permlane16_swap
+// (v_permlane32_swap) of a value with itself leaves the value of lane l in
+// one result and that of lane l^16 (l^32) in the other, in both lanes of the
+// pair.  Same operands in the same order as x op __shfl_xor(x, 16 / 32), so
+// the results are bit-identical (IEEE add and max are commutative).
+__device__ __forceinline__ float max_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -135,6 +157,30 @@ __device__ __forceinline__ void decode_chunk(
   float m_run = -INFINITY, l_run = 0.f;
 
   const int ntiles = (int)((t_end - t_begin + tile - 1) / tile);
+  // The chunk's block ids, 256 at a time (window w0 .. w0 + 255 of the
+  // table row): lane l holds ids 4l .. 4l+3 of the window, read back with
+  // readlane, so no tile waits on a scalar load of its block id.  Ids past
+  // the chunk's last block are never read (loaded as 0 to stay in bounds).
+  const int64_t blk_first = t_begin / BS;
+  const int64_t blk_last = (t_end - 1) / BS;
+  int64_t w0 = -1;
+  uint4 ids = make_uint4(0, 0, 0, 0);
+  auto load_window = [&](int64_t w) {
+    w0 = w;
+    const int64_t e = w + 4 * lane;
+    uint32_t v[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) v[c] = e + c <= blk_last ? (uint32_t)btrow[e + c] : 0u;
+    ids = make_uint4(v[0], v[1], v[2], v[3]);
+  };
+  auto block_id = [&](int64_t bi) -> int32_t {
+    if (bi < w0 || bi >= w0 + 256) load_window(bi);  // chunks longer than 256 blocks: next window
+    const int e = (int)(bi - w0);
+    const int src = e >> 2, c = e & 3;
+    const uint32_t x = c == 0 ? ids.x : c == 1 ? ids.y : c == 2 ? ids.z : ids.w;
+    return (int32_t)__builtin_amdgcn_readlane((int)x, src);
+  };
+  load_window(blk_first);
   // tile i of the chunk: valid row count (0 for a skipped block) and the
   // element offset of its first row.  Tiles at or past `last` are
   // look-ahead fillers: n = 0 and row 0 of block 0, so their loads all hit
@@ -148,7 +194,7 @@ __device__ __forceinline__ void decode_chunk(
     }
     const int64_t t0 = t_begin + (int64_t)i * tile;
     n = (int)min((int64_t)tile, t_end - t0);
-    const int32_t blk = btrow[t0 / BS];
+    const int32_t blk = block_id(t0 / BS);
     const bool ok = blk >= 0 && (int64_t)blk < NB;
     if (!ok) n = 0;  // invalid block: contributes nothing
     off = ((int64_t)(ok ? blk : 0) * BS + (t0 % BS)) * row + (int64_t)kh * D;
@@ -215,8 +261,8 @@ __device__ __forceinline__ void decode_chunk(
     __builtin_amdgcn_sched_barrier(0);  // keep the issue order the wait counts assume
     load_k(ka, n2, o2);
     __builtin_amdgcn_sched_barrier(0);
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    tmax = max_xor16(tmax);
+    tmax = max_xor32(tmax);
     const float m_new = fmaxf(m_run, tmax);
     const bool live = m_new != -INFINITY;
     const float alpha = live ? exp2f(m_run - m_new) : 1.f;
@@ -229,8 +275,8 @@ __device__ __forceinline__ void decode_chunk(
         psum += p;
         if (j < G) pw[(g16 * 16 + kq * 4 + r) * GP + j] = p;
       }
-    psum += __shfl_xor(psum, 16, 64);
-    psum += __shfl_xor(psum, 32, 64);
+    psum = sum_xor16(psum);
+    psum = sum_xor32(psum);
     l_run = l_run * alpha + psum;
     m_run = m_new;
     wave_lds_sync();
