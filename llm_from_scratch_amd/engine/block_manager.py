@@ -9,7 +9,11 @@ Behavioural fixes (the reference's bugs are not copied):
   * ``can_append`` asks for a free block when the sequence's newest token
     starts a new block (num_tokens % BS == 1) -- the case in which
     ``append`` allocates -- rather than at num_tokens % BS == 0 (:130-134
-    vs :149-153), which let ``append`` pop an empty free list.
+    vs :149-153), which let ``append`` pop an empty free list;
+  * a prompt's last block is never taken from the prefix cache (:85-114
+    would cache every block of a block-aligned prompt that matches another
+    sequence's, leaving the prefill no query token to sample from): it is
+    recomputed into a fresh block, so num_cached_tokens < num_tokens.
 """
 from __future__ import annotations
 
@@ -82,6 +86,8 @@ class BlockManager:
             block_id = self.hash_to_block_id.get(h, -1)
             if block_id == -1 or self.blocks[block_id].token_ids != token_ids:
                 cache_miss = True
+            if i == seq.num_blocks - 1:
+                cache_miss = True  # the last prompt token is always computed
             if not cache_miss:
                 seq.num_cached_tokens += self.block_size
                 if block_id in self.used_block_ids:

@@ -3,9 +3,14 @@
 Counterpart of engine/model_runner.py of the reference with the same method
 names and data contract (one MI355X, so no process group or shared-memory
 RPC):
-  allocate_kv_cache   one pool [2, L, NB, BS, Hkv, D]; per-layer k_cache /
-                      v_cache views attached to modules that have them
-                      (:162-190)
+  warmup_model        one prefill of max_num_batched_tokens // max_model_length
+                      full-length sequences before the pool exists, so the
+                      peak activation memory is known (:151-159)
+  allocate_kv_cache   one pool [2, L, NB, BS, Hkv, D] of free x
+                      gpu_memory_utilization - (peak - current) bytes after
+                      the warm-up (or num_kv_blocks blocks when given);
+                      per-layer k_cache / v_cache views attached to modules
+                      that have them (:162-190)
   prepare_prefill     input ids / positions of uncached tokens, cu_seqlens,
                       slot_mapping over uncached blocks, block tables when a
                       prefix is cached (:202-249)
@@ -102,11 +107,60 @@ class ModelRunner:
         self.sampler = Sampler()
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
         self.graph_vars: dict[str, torch.Tensor] = {}
+        if "num_kv_blocks" not in config:
+            self.warmup_model()
         self.allocate_kv_cache()
         if not self.enforce_eager:
             self.capture_cudagraph()
 
     # ------------------------------------------------------------ KV pool --
+    def _attach_pool(self, pool: torch.Tensor) -> None:
+        layer = 0
+        for module in self.model.modules():
+            if hasattr(module, "k_cache") and hasattr(module, "v_cache"):
+                module.k_cache = pool[0, layer]
+                module.v_cache = pool[1, layer]
+                layer += 1
+        assert layer == self.config["num_layers"], \
+            f"found {layer} attention layers, expected {self.config['num_layers']}"
+
+    @torch.inference_mode()
+    def warmup_model(self) -> None:
+        """One prefill of max_num_batched_tokens // max_model_length sequences
+        of max_model_length tokens (at least one sequence, at most the token
+        budget long), as engine/model_runner.py:151-159, so that the peak of
+        allocated memory holds the largest prefill's activations when
+        allocate_kv_cache sizes the pool.  This model's attention writes
+        every prompt's K/V into the pool before attending, so the warm-up
+        runs over a temporary pool of exactly the warm-up's blocks, freed
+        afterwards (its bytes count towards the reserved peak)."""
+        cfg = self.config
+        max_len = int(cfg.get("max_model_length", 4096))
+        budget = int(cfg.get("max_num_batched_tokens", cfg.get("max_num_batch_tokens", max_len)))
+        n_seq = max(1, budget // max_len)
+        seq_len = min(max_len, budget)
+        torch.cuda.empty_cache()
+        torch.cuda.reset_peak_memory_stats(self.device)
+        nblk = n_seq * math.ceil(seq_len / self.block_size)
+        pool = torch.empty(2, cfg["num_layers"], nblk, self.block_size, cfg["num_kv_heads"],
+                           cfg.get("head_dim", cfg["hidden_size"] // cfg["num_heads"]),
+                           device=self.device, dtype=cfg.get("kv_dtype", torch.bfloat16))
+        self._attach_pool(pool)
+        seqs = [Sequence([0] * seq_len) for _ in range(n_seq)]
+        per = math.ceil(seq_len / self.block_size)
+        for i, sq in enumerate(seqs):
+            sq.block_table = list(range(i * per, (i + 1) * per))
+        ids, pos = self.prepare_prefill(seqs)
+        self.model(ids, pos)
+        torch.cuda.synchronize(self.device)
+        reset_context()
+        for module in self.model.modules():
+            if hasattr(module, "k_cache") and hasattr(module, "v_cache"):
+                module.k_cache = torch.empty(0)
+                module.v_cache = torch.empty(0)
+        del pool, ids, pos
+        torch.cuda.empty_cache()
+
     def allocate_kv_cache(self) -> None:
         cfg = self.config
         num_layers = cfg["num_layers"]
@@ -117,19 +171,20 @@ class ModelRunner:
         if "num_kv_blocks" in cfg:
             nb = int(cfg["num_kv_blocks"])
         else:
+            # free x utilisation, minus the room the warm-up prefill's
+            # activations needed above what stays allocated
+            # (engine/model_runner.py:162-168)
             free, _ = torch.cuda.mem_get_info(self.device)
-            nb = int(free * cfg.get("gpu_memory_utilization", 0.9) // block_bytes)
+            stats = torch.cuda.memory_stats(self.device)
+            reserve = stats["allocated_bytes.all.peak"] - stats["allocated_bytes.all.current"]
+            available = free * cfg.get("gpu_memory_utilization", 0.9) - reserve
+            nb = int(available // block_bytes)
+            self.kv_reserved_bytes = reserve
         assert nb >= 1, "Not enough memory to hold at least one block of KV cache"
         self.num_available_kv_blocks = nb
         self.kv_cache = torch.empty(2, num_layers, nb, self.block_size, num_kv_heads, head_dim,
                                     device=self.device, dtype=dtype)
-        layer = 0
-        for module in self.model.modules():
-            if hasattr(module, "k_cache") and hasattr(module, "v_cache"):
-                module.k_cache = self.kv_cache[0, layer]
-                module.v_cache = self.kv_cache[1, layer]
-                layer += 1
-        assert layer == num_layers, f"found {layer} attention layers, expected {num_layers}"
+        self._attach_pool(self.kv_cache)
 
     # ----------------------------------------------------------- metadata --
     def _pad_tables(self, seqs: list[Sequence]) -> torch.Tensor:

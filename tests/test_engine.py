@@ -212,3 +212,28 @@ def test_sampler_needs_gpu_tensors():
     s = Sampler()
     with pytest.raises(ValueError):
         s(torch.zeros(2, 8, dtype=torch.bfloat16), torch.ones(2), torch.Generator().manual_seed(0))
+
+
+def test_block_aligned_prompt_fully_matching_keeps_a_query_token():
+    """Two sequences with the same block-aligned prompt: the second one hits
+    the prefix cache on every block but the last, which it recomputes into a
+    block of its own, so its prefill has at least one query token (the
+    reference would cache all blocks and leave none to sample from)."""
+    BS = 16
+    Sequence.block_size = BS
+    bm = BlockManager(16, BS)
+    prompt = list(range(3 * BS))
+    a, b = Sequence(list(prompt)), Sequence(list(prompt))
+    bm.allocate(a)
+    bm.allocate(b)
+    assert a.num_cached_tokens == 0
+    assert b.num_cached_tokens == 2 * BS < b.num_tokens
+    assert b.block_table[:2] == a.block_table[:2] and b.block_table[2] != a.block_table[2]
+    assert bm.blocks[a.block_table[0]].ref_count == 2 and bm.blocks[b.block_table[2]].ref_count == 1
+    m = prefill_metadata([a, b], BS)
+    q = np.diff(m["cu_seqlens_q"])
+    assert q.tolist() == [3 * BS, BS]
+    assert len(m["slot_mapping"]) == 4 * BS  # every uncached block's slots
+    bm.deallocate(b)
+    bm.deallocate(a)
+    assert len(bm.free_block_ids) == 16

@@ -125,6 +125,46 @@ def test_moe_route(T, d, E, S, k):
     torch.testing.assert_close(bias, dense @ b2, rtol=1e-5, atol=1e-5)
 
 
+def test_moe_route_near_ties():
+    """Expert selection on exact and near ties, pinned in the kernel's
+    arithmetic: logits (fp32 dot of bf16 rows) are exact small integers
+    (h = 1, integer gate weights), the biased keys logit + bias are compared
+    in fp32, and exact ties go to the lower expert index.  Token rows:
+    (a) two experts tie exactly (key 10): the lower index wins;
+    (b) keys 10, 10 + 2^-20, 10 + 2^-20 (one fp32 ulp apart; all equal once
+        rounded to bf16, as the reference's bf16 gate would round them): the
+        two larger fp32 keys win;
+    (c) keys 7, 7, 7 + 2^-20: the one-ulp larger key, then the lower index
+        of the exact tie.
+    This fixes the deliberate fp32 choice; the reference rounds logits, the
+    bias add and the renormalised weights to bf16 (model/architecture/moe.py:
+    45-69) and orders ties as torch.topk(sorted=False) does."""
+    d, E, k = 256, 8, 2
+    ulp = 2.0 ** -20
+    rows = [
+        # three-way exact tie at 10: the two lowest indices
+        ([10, 10, 10, 2, 1, 0, 0, 0], [0.0] * 8, [0, 1]),
+        # keys 10, 10 + ulp, 10 + ulp (9 + (1 + 2^-20) is exact in fp32)
+        ([10, 9, 9, 2, 1, 0, 0, 0], [0.0, 1.0 + ulp, 1.0 + ulp, 0, 0, 0, 0, 0], [1, 2]),
+        # keys 7, 7, 7 + ulp: the near-tie first, then the lower of the exact tie
+        ([7, 7, 7, 1, 0, 0, 0, 0], [0.0, 0.0, ulp, 0, 0, 0, 0, 0], [0, 2]),
+    ]
+    T = len(rows)
+    h = torch.ones(T, d, device=DEV, dtype=torch.bfloat16)
+    gw = torch.zeros(T * E, d, device=DEV)
+    outs = []
+    for t, (logit, bias, want) in enumerate(rows):
+        gwt = torch.zeros(E, d, device=DEV)
+        for e, L in enumerate(logit):  # L ones in the row: the dot with h = 1 is exactly L
+            gwt[e, :L] = 1.0
+        w, _ = K.moe_route(h[t:t + 1], gwt.to(torch.bfloat16), torch.tensor(bias, device=DEV),
+                           torch.zeros(E, d, device=DEV), k, 0)
+        chosen = torch.nonzero(w[0] > 0).flatten().tolist()
+        assert sorted(chosen) == sorted(want), f"row {t}: chose {chosen}, expected {want}"
+        sc = torch.sigmoid(torch.tensor(logit, dtype=torch.float32))[want]
+        torch.testing.assert_close(w[0, want].cpu(), sc / (sc.sum() + 1e-10), rtol=1e-6, atol=0)
+
+
 @pytest.mark.parametrize("T,E,F", [(128, 9, 512), (3, 2, 128), (17, 4, 1024)])
 def test_swiglu_quant(T, E, F):
     g = torch.Generator(device=DEV).manual_seed(T + F)

@@ -332,6 +332,51 @@ def _decode(runner, seqs, eager):
 
 
 @torch.inference_mode()
+def test_runner_sizes_pool_after_warmup():
+    """Without num_kv_blocks the runner warms up with a full-length prefill
+    and sizes the pool as free x gpu_memory_utilization - (peak - current)
+    (engine/model_runner.py:151-181); the sized runner then serves a prefill
+    and a decode step with the same logits as a runner given the block count
+    explicitly (same weights, same block tables)."""
+    BS = 16
+    Sequence.block_size = BS
+    model = DecodeModel(SMALL, device="cuda", seed=13)
+    util = 0.02
+    cfg = SMALL.runner_config(block_size=BS, max_num_seqs=4, gpu_memory_utilization=util,
+                              max_num_batched_tokens=2 * SMALL.max_model_length)
+    torch.cuda.empty_cache()
+    runner = ModelRunner(model, cfg)
+    D = SMALL.head_dim
+    block_bytes = BS * 2 * SMALL.num_layers * SMALL.num_kv_heads * D * 2
+    free_after = torch.cuda.mem_get_info()[0]
+    nb = runner.num_available_kv_blocks
+    # the pool took about util x (free before it) minus the warm-up reserve
+    assert runner.kv_reserved_bytes > 0, "the warm-up prefill left no peak above the resident memory"
+    expect = (free_after + nb * block_bytes) * util - runner.kv_reserved_bytes
+    assert abs(nb * block_bytes - expect) <= 0.02 * expect + 4 * block_bytes, (nb, expect / block_bytes)
+    assert nb >= 64
+    assert all(m.k_cache.shape[0] == nb for m in model.modules() if hasattr(m, "k_cache"))
+    prompt = np.random.default_rng(5).integers(0, SMALL.vocab_size, 37).tolist()
+
+    def serve(r):  # prefill, then one graph-replayed decode step
+        s = Sequence(list(prompt))
+        bm = BlockManager(r.num_available_kv_blocks, BS)
+        bm.allocate(s)
+        first = _prefill(r, [s])
+        s.append_token(7)
+        assert bm.can_append(s)
+        bm.append(s)
+        return first, _decode(r, [s], eager=False)
+
+    sized = serve(runner)  # before the second runner re-attaches the model's caches
+    del runner
+    fixed = serve(ModelRunner(model, SMALL.runner_config(block_size=BS, num_kv_blocks=nb, max_num_seqs=4)))
+    assert torch.isfinite(sized[1]).all()
+    assert torch.equal(sized[0], fixed[0]) and torch.equal(sized[1], fixed[1])
+    torch.cuda.empty_cache()
+
+
+@torch.inference_mode()
 def test_decode_steps_match_full_forward_small(block_size):
     """Prefill (with a shared cached prefix), then three decode steps crossing
     block boundaries (BS=16); graph replay == eager, replays repeatable."""
