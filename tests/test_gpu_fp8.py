@@ -51,6 +51,27 @@ def test_act_quant_cfg2_outliers(M, Kd):
     check_act_quant(W.activation(M, Kd, seed=1 + M + Kd).to(DEV))
 
 
+@pytest.mark.parametrize("Kd", [1024, 4096, 2048])
+def test_act_quant_m16384_bitexact(Kd):
+    """cfg2's largest activations (16384 rows, 0.1% outliers at +-40): codes
+    and scales bit-exact against the oracle over every row (the oracle runs
+    on row blocks in parallel threads; numpy releases the GIL)."""
+    from concurrent.futures import ThreadPoolExecutor
+    M = 16384
+    x = W.activation(M, Kd, seed=60 + Kd)
+    y, s = K.act_quant(x.to(DEV))
+    torch.cuda.synchronize()
+    xf = f32(x)
+    blocks = [(r, min(M, r + 512)) for r in range(0, M, 512)]
+    with ThreadPoolExecutor(16) as ex:
+        res = list(ex.map(lambda rr: F.act_quant(xf[rr[0]:rr[1]]), blocks))
+    ry = np.concatenate([r[0] for r in res])
+    rs = np.concatenate([r[1] for r in res])
+    np.testing.assert_array_equal(f32(s), rs)
+    bad = np.argwhere(codes(y) != ry)
+    assert bad.size == 0, f"{len(bad)} code mismatches, first at {bad[:3].tolist()}"
+
+
 def test_act_quant_every_bf16_quotient():
     """Groups whose amax is 448*2^k have s == 2^k exactly (448*fp32(1/448)
     rounds to 1), so x/s runs over every bf16 value in [-448, 448]: an

@@ -456,6 +456,50 @@ def test_decode_step_cfg5_shapes(block_size):
 
 
 @torch.inference_mode()
+def test_decode_step_cfg5_full_batch():
+    """The config-5 decode step at the bench's batch of 128 (contexts uniform
+    in [256, 2048]): the bs=128 graph replay against the eager step on every
+    row (1e-2 relative) and against itself (two replays bit-identical), every
+    op of every layer teacher-forced against its fp32 reference, and 3
+    sampled rows end to end against a full causal forward."""
+    BS, B = 256, 128
+    Sequence.block_size = BS
+    cfg = DecodeModelConfig()
+    rng = np.random.default_rng(14)
+    lens = rng.integers(256, 2049, B)
+    nblk = int((-(-(lens + 1) // BS)).sum())
+    model = DecodeModel(cfg, device="cuda", seed=14)
+    runner = ModelRunner(model, cfg.runner_config(block_size=BS, num_kv_blocks=nblk + 8, max_num_seqs=B))
+    assert B in runner.graphs
+    bm = BlockManager(nblk + 8, BS)
+    seqs = [Sequence(rng.integers(0, cfg.vocab_size, int(n)).tolist()) for n in lens]
+    for s in seqs:
+        bm.allocate(s)
+    for i in range(0, B, 32):  # prefill in four batches of 32 sequences
+        _prefill(runner, seqs[i:i + 32])
+    for s in seqs:
+        s.append_token(int(rng.integers(0, cfg.vocab_size)))
+        assert bm.can_append(s)
+        bm.append(s)
+    g1 = _decode(runner, seqs, eager=False)
+    e = _decode(runner, seqs, eager=True)
+    g2 = _decode(runner, seqs, eager=False)
+    assert torch.equal(g1, g2), "graph replays differ"
+    assert torch.isfinite(g1).all()
+    err = rel_err_rows(g1, e)
+    assert (err <= 1e-2).all(), f"graph vs eager: worst row {int(err.argmax())} rel err {err.max().item():.4f}"
+    worst = check_layers_teacher_forced(model, runner, seqs)
+    rows = (0, int(np.argmax(lens)), 77)
+    errs = [rel_err_rows(g1[i], ref_logits(model, seqs[i].token_ids)[-1]).item() for i in rows]
+    print(f"\ncfg5 B=128: graph vs eager max {err.max().item():.2e}; e2e rel err {['%.4f' % x for x in errs]}; "
+          f"per-stage max " + ", ".join(f"{k} {v:.2e}" for k, v in worst.items()))
+    for i, x in zip(rows, errs):
+        assert x <= e2e_tol(cfg.num_layers), f"seq {i} len {len(seqs[i])} rel err {x:.4f}"
+    del runner, model
+    torch.cuda.empty_cache()
+
+
+@torch.inference_mode()
 def test_engine_generate_runs_to_max_tokens(block_size):
     BS = 16
     Sequence.block_size = BS

@@ -130,6 +130,37 @@ def test_paged_decode_cfg4_subset_full_pool():
     torch.cuda.empty_cache()
 
 
+def test_paged_decode_cfg4_full_batch():
+    """cfg4 at its full batch of 256 (lengths log-uniform to 32768 over the
+    65536-block pool): the balanced split (the default) against 8-block
+    fixed chunks on every (sequence, head), and 8 sampled sequences (the
+    shortest, the longest and 6 random) against the float64 oracle on their
+    own blocks."""
+    case = W.paged_case("cfg4", seed=3)
+    assert case.batch == 256
+    kc, vc = W.fill_pool(case, seed=3, device=DEV, only_referenced=True)
+    q = make_q(case, 11)
+    o = run_decode(case, kc, vc, q, 0)
+    fixed = run_decode(case, kc, vc, q, 8)
+    torch.cuda.synchronize()
+    on, fn = o.float().cpu().numpy(), fixed.float().cpu().numpy()
+    assert np.isfinite(on).all()
+    assert_close(on, fn, "cfg4 balanced vs fixed chunks")
+    lens = case.context_lens
+    pick = np.unique(np.concatenate([[int(lens.argmin()), int(lens.argmax())],
+                                     np.random.default_rng(12).choice(256, 6, replace=False)]))
+    BS = case.block_size
+    for b in pick:
+        nb = -(-int(lens[b]) // BS)
+        ids = torch.from_numpy(case.block_tables[b, :nb].astype(np.int64)).to(DEV)
+        kh, vh = kc[ids].float().cpu().numpy(), vc[ids].float().cpu().numpy()
+        ref = P.paged_decode(q[b:b + 1].float().cpu().numpy(), kh, vh, lens[b:b + 1],
+                             np.arange(nb, dtype=np.int32)[None, :], case.scale)
+        assert_close(on[b:b + 1], ref, f"cfg4 sequence {b} (L={int(lens[b])})")
+    del kc, vc
+    torch.cuda.empty_cache()
+
+
 def test_paged_decode_split_independence():
     case = W.paged_case("cfg3", seed=5, batch=12)
     kc, vc = W.fill_pool(case, seed=5, device=DEV)
