@@ -107,7 +107,7 @@ const char* lfs_last_error(void);
  *   y = e4m3fn(clamp(x / s, -448, 448))   (IEEE fp32 divide, RNE)
  * x: bf16 [M, K] with row stride ldx elements (ldx >= K, ldx % 8 == 0);
  * y: e4m3fn [M, K] contiguous; s: fp32 [M, K / block_size] contiguous.
- * block_size in {32, 64, 128}; K % block_size == 0.
+ * block_size in {32, 64, 128}; K % block_size == 0; M * K < 2^34.
  */
 int lfs_act_quant(const void* x, int64_t ldx, void* y, float* s, int64_t M, int64_t K,
                   int32_t block_size, int32_t round_scale, void* stream);

@@ -95,10 +95,52 @@ __device__ __forceinline__ float qdiv(float x, float s) {
   return q;
 }
 
-__device__ __forceinline__ uint2 quant8(const float* f, float s) {
+__device__ __forceinline__ uint2 quant8_ieee(const float* f, float s) {
   uint2 o;
   o.x = f32x4_to_e4m3(qdiv(f[0], s), qdiv(f[1], s), qdiv(f[2], s), qdiv(f[3], s));
   o.y = f32x4_to_e4m3(qdiv(f[4], s), qdiv(f[5], s), qdiv(f[6], s), qdiv(f[7], s));
+  return o;
+}
+
+// Quotients x / s by a group's scale s = scale_from_amax(amax) for |x| <= amax.
+// This is the compiler's correctly rounded fp32 divide (v_div_scale, rcp,
+// one Newton step on the reciprocal, two residual corrections of the
+// quotient, v_div_fmas, v_div_fixup) with the divisor's half -- y = rcp(s)
+// refined by y += y * (1 - s*y) -- done once per group instead of once per
+// element.  v_div_scale changes neither operand here: s lies in
+// [1e-4/448, 2^120] (normal, 1/s normal), and it only scales a numerator
+// below 2^-104 or 2^96 times smaller than s, whose quotient is below 2^-96
+// and encodes as a signed zero whatever its low bits; with no scaling
+// v_div_fmas is a plain fma and v_div_fixup passes a finite quotient
+// through.  So an element costs a multiply and four FMAs and gets the
+// divide's bits, except that a zero quotient may lose x's sign (callers put
+// it back).  |x / s| <= 448 * (1 + 2^-23), which e4m3's round-to-nearest
+// sends to 448, so the clamp is a no-op.  An infinite s (an infinite input)
+// must take quant8_ieee instead.
+__device__ __forceinline__ float recip_for_div(float s) {
+  const float y = __builtin_amdgcn_rcpf(s);
+  return fmaf(fmaf(-s, y, 1.0f), y, y);
+}
+
+__device__ __forceinline__ float div_by_group(float x, float s, float y) {
+  float q = x * y;
+  float e = fmaf(-s, q, x);
+  q = fmaf(e, y, q);
+  e = fmaf(-s, q, x);
+  return fmaf(e, y, q);
+}
+
+// e4m3 codes of clamp(f[i] / s, -448, 448) (IEEE divide) for a group scale
+// s = scale_from_amax(amax) with every |f[i]| <= amax
+__device__ __forceinline__ uint2 quant8(const float* f, float s) {
+  if (!(s < INFINITY)) return quant8_ieee(f, s);
+  const float y = recip_for_div(s);
+  float q[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q[i] = copysignf(div_by_group(f[i], s, y), f[i]);
+  uint2 o;
+  o.x = f32x4_to_e4m3(q[0], q[1], q[2], q[3]);
+  o.y = f32x4_to_e4m3(q[4], q[5], q[6], q[7]);
   return o;
 }
 

@@ -16,53 +16,71 @@ namespace lfs {
 // ------------------------------------------------------------ act_quant --
 // One lane per 8 consecutive elements (one 16-byte load); a group of GS
 // elements is GS/8 consecutive lanes of one wave, reduced with shuffles.
-// Each thread handles AQ_U chunks a grid-stride apart (the stride is a
-// multiple of 256, so a group's lanes stay together and all in or all out),
-// issuing their loads before any arithmetic.  Input and codes are streamed
-// once, so loads and stores are nontemporal.  Measured at 16384 x 4096 with
-// the Infinity Cache flushed (kernel trace, median): one chunk per thread
-// with plain loads and stores 58.5 us; 1 / 2 / 4 / 8 chunks with
-// nontemporal loads and stores 47.7 / 46.9 / 47.1 / 49.2 us (nontemporal
-// loads alone: 48.5 / 49.0 / 49.2 / 51.0 us).
+// A workgroup takes AQ_U blocks of 256 consecutive chunks and issues all
+// their loads before any arithmetic; input and codes are streamed once, so
+// loads and stores are nontemporal.  A chunk's row is floor(idx * m >> sh)
+// with m = ceil(2^sh / cpr), sh = 31 + ceil(log2 cpr) (Granlund and
+// Montgomery, "Division by invariant integers using multiplication", 1994:
+// exact for every idx below 2^31), not a 64-bit division.
+//
+// The quotients are div_by_group's (the IEEE divide with the divisor's
+// half done once per group); the sign of a zero quotient comes back from
+// the input's bf16 sign bits by one byte permute per four codes.
 constexpr int AQ_U = 2;
+
+// e4m3 codes of 4 quotients, with the sign bits of their inputs (two bf16
+// pairs lo, hi) or-ed in: bytes 1 and 3 of each pair hold the signs at bit 7
+__device__ __forceinline__ uint32_t e4m3_signed(float a, float b, float c, float d, uint32_t lo, uint32_t hi) {
+  const uint32_t sg = __builtin_amdgcn_perm(hi, lo, 0x07050301u) & 0x80808080u;
+  return f32x4_to_e4m3(a, b, c, d) | sg;
+}
 
 template <int GS, bool ROUND>
 __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                         uint8_t* __restrict__ y,
-                                                        float* __restrict__ s, int64_t M,
-                                                        int64_t K) {
+                                                        float* __restrict__ s, uint32_t total,
+                                                        uint32_t cpr, uint64_t magic, uint32_t shift) {
   constexpr int LPG = GS / 8;  // lanes per group; groups never straddle waves
-  const int64_t cpr = K / 8;
-  const int64_t total = M * cpr;
-  const int64_t stride = (int64_t)gridDim.x * 256;
-  const int64_t idx0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
   typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
   typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+  const uint32_t base = blockIdx.x * (256u * AQ_U) + threadIdx.x;
   u32x4_t v[AQ_U];
+  uint32_t rows[AQ_U], cols[AQ_U];
 #pragma unroll
   for (int j = 0; j < AQ_U; ++j) {
-    const int64_t idx = idx0 + j * stride;
-    if (idx < total) {
-      const int64_t row = idx / cpr, c8 = idx - row * cpr;
-      v[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(x + row * ldx + c8 * 8));
-    }
+    const uint32_t idx = base + 256u * j;
+    rows[j] = (uint32_t)(((uint64_t)idx * magic) >> shift);
+    cols[j] = idx - rows[j] * cpr;
+    if (idx < total)
+      v[j] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4_t*>(x + (int64_t)rows[j] * ldx + (int64_t)cols[j] * 8));
   }
 #pragma unroll
   for (int j = 0; j < AQ_U; ++j) {
-    const int64_t idx = idx0 + j * stride;
-    // K % GS == 0 and 256 % LPG == 0, so a group's lanes are all in or all out
-    if (idx >= total) break;
-    const int64_t row = idx / cpr, c8 = idx - row * cpr;
+    // cpr % LPG == 0 and 256 % LPG == 0, so a group's lanes are all in or all out
+    if (base + 256u * j >= total) break;
+    const int64_t row = rows[j], c8 = cols[j];
+    const uint4 w = make_uint4(v[j][0], v[j][1], v[j][2], v[j][3]);
     float f[8];
-    unpack8(make_uint4(v[j][0], v[j][1], v[j][2], v[j][3]), f);
+    unpack8(w, f);
     float amax = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[i]));
     amax = group_max<LPG>(amax);
     const float sc = scale_from_amax(amax, ROUND);
-    const uint2 q = quant8(f, sc);
-    __builtin_nontemporal_store(u32x2_t{q.x, q.y}, reinterpret_cast<u32x2_t*>(y + row * K + c8 * 8));
-    if ((c8 & (LPG - 1)) == 0) s[row * (K / GS) + c8 / LPG] = sc;
+    uint2 o;
+    if (sc < INFINITY) {
+      const float r = recip_for_div(sc);
+      float q[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) q[i] = div_by_group(f[i], sc, r);
+      o.x = e4m3_signed(q[0], q[1], q[2], q[3], w.x, w.y);
+      o.y = e4m3_signed(q[4], q[5], q[6], q[7], w.z, w.w);
+    } else {
+      o = quant8_ieee(f, sc);
+    }
+    __builtin_nontemporal_store(u32x2_t{o.x, o.y}, reinterpret_cast<u32x2_t*>(y + row * (int64_t)cpr * 8 + c8 * 8));
+    if ((c8 & (LPG - 1)) == 0) s[row * ((int64_t)cpr * 8 / GS) + c8 / LPG] = sc;
   }
 }
 
@@ -155,11 +173,20 @@ extern "C" int lfs_act_quant(const void* x, int64_t ldx, void* y, float* s, int6
   LFS_REQUIRE(aligned16(x) && ((uintptr_t)y & 7u) == 0 && ((uintptr_t)s & 3u) == 0,
               "act_quant: misaligned buffer");
   const int64_t chunks = M * (K / 8);
+  LFS_REQUIRE(chunks + 256 * AQ_U < (1ll << 31), "act_quant: M*K=%lld elements is too large", (long long)(M * K));
+  // m * cpr - 2^sh lies in [0, cpr) and cpr <= 2^(sh - 31), so idx * m >> sh
+  // is floor(idx / cpr) for idx < 2^31; m < 2^33 keeps idx * m below 2^64
+  const uint32_t cpr = (uint32_t)(K / 8);
+  uint32_t lg = 0;
+  while ((1ull << lg) < cpr) ++lg;
+  const uint32_t shift = 31 + lg;
+  const uint64_t magic = ((1ull << shift) + cpr - 1) / cpr;
   const dim3 grid((unsigned)((chunks + 256 * AQ_U - 1) / (256 * AQ_U)));
   hipStream_t st = (hipStream_t)stream;
   const uint16_t* xp = (const uint16_t*)x;
   uint8_t* yp = (uint8_t*)y;
-#define LFS_AQ(GS, R) hipLaunchKernelGGL((act_quant_kernel<GS, R>), grid, dim3(256), 0, st, xp, ldx, yp, s, M, K)
+#define LFS_AQ(GS, R) \
+  hipLaunchKernelGGL((act_quant_kernel<GS, R>), grid, dim3(256), 0, st, xp, ldx, yp, s, (uint32_t)chunks, cpr, magic, shift)
   if (round_scale) {
     if (block_size == 32) LFS_AQ(32, true);
     else if (block_size == 64) LFS_AQ(64, true);

@@ -93,6 +93,43 @@ def test_act_quant_every_bf16_quotient():
     assert set(np.unique(sc).tolist()) == {1.0, 2.0 ** -3, 32.0}
 
 
+def _every_scale_quotient_groups():
+    """Groups of 128 = [amax, 127 others] that reach every fp32 quotient
+    x / s act_quant can form with a full-mantissa scale.  s = amax * fp32(1/448)
+    depends on amax's 8-bit mantissa only (up to a power of two), and the
+    fp32 rounding of x / s on x's mantissa and on the binade only where e4m3
+    is subnormal; so one amax per bf16 mantissa (128, spread over exponents),
+    each with every bf16 x in [amax * 2^-22, amax] of both signs, covers every
+    (scale, element) mantissa pair in every binade from e4m3 subnormals to
+    448.  One more amax below the 1e-4 floor takes every bf16 x under it."""
+    bits = (np.arange(1 << 16, dtype=np.uint32) << 16).view(np.float32)
+    allv = bits[np.isfinite(bits) & (bits != 0)]
+    rows = []
+    amaxes = [np.float32((1 + m / 128) * 2.0 ** (m % 7 - 3)) for m in range(128)]
+    amaxes.append(np.float32(torch.tensor(6.1e-5).to(torch.bfloat16).item()))
+    for amax in amaxes:
+        lo = amax * np.float32(2.0 ** -22) if amax >= 1e-4 else 0
+        v = allv[(np.abs(allv) <= amax) & (np.abs(allv) >= lo)]
+        n = -(-len(v) // 127)
+        v = np.concatenate([v, np.zeros(n * 127 - len(v), np.float32)]).reshape(n, 127)
+        rows.append(np.concatenate([np.full((n, 1), amax, np.float32), v], axis=1))
+    return np.concatenate(rows)
+
+
+def test_act_quant_every_scale_quotient():
+    """Codes for quotients x / s with full-mantissa scales, which act_quant
+    forms as x times the group's reciprocal with an IEEE-divide fallback near
+    e4m3 rounding midpoints: every (scale mantissa, element mantissa, binade)
+    case, bit-exact against the oracle's correctly rounded divide."""
+    g = _every_scale_quotient_groups()
+    assert len(np.unique(g[:, 0].view(np.uint32) & 0x7F0000)) == 128
+    pad = -len(g) % 4
+    g = np.concatenate([g, np.zeros((pad, 128), np.float32)])
+    x = torch.from_numpy(g.reshape(-1, 512)).to(torch.bfloat16)
+    assert torch.equal(x.float().reshape(-1, 128), torch.from_numpy(g))
+    check_act_quant(x.to(DEV))
+
+
 def test_act_quant_edge_groups():
     x = torch.randn(8, 256).to(torch.bfloat16)
     x[0, :128] = 0.0
