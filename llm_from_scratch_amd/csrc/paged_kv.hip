@@ -904,8 +904,8 @@ int paged_decode_impl(const void* q, const void* k_cache, const void* v_cache, c
   if (B == 0) return 0;
   LFS_REQUIRE(q && k_cache && v_cache && context_lens && out, "paged_decode: null pointer");
   LFS_REQUIRE(max_blocks == 0 || block_tables, "paged_decode: null block table");
-  LFS_REQUIRE(((((uintptr_t)q) | ((uintptr_t)k_cache) | ((uintptr_t)v_cache)) & 15u) == 0,
-              "paged_decode: q and caches must be 16-byte aligned");
+  LFS_REQUIRE(((((uintptr_t)q) | ((uintptr_t)k_cache) | ((uintptr_t)v_cache) | ((uintptr_t)out)) & 15u) == 0,
+              "paged_decode: q, caches and out must be 16-byte aligned");
   LFS_REQUIRE(B < 65536, "paged_decode: batch too large");
   LFS_REQUIRE((q_out == nullptr) == (q_scale == nullptr), "paged_decode: q_out and q_scale go together");
   LFS_REQUIRE(q_out == nullptr || (Hq * D % 128 == 0 && Hq * D <= MQ_MAXE && Hq <= MQ_MAXH),
