@@ -398,8 +398,8 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
 }
 
 // ---------------------------------------------------------------------------
-// Skinny GEMM for decode-sized M (<= 128): one workgroup per 32 output
-// columns and all M rows, in WGM groups of four waves; group gm owns row
+// Skinny GEMM for decode-sized M (<= 128): one workgroup per 16 * NT
+// (NT = 2, or 1 for narrow N) output columns and all M rows, in WGM groups of four waves; group gm owns row
 // tiles gm*MTW .. gm*MTW + MTW - 1, and its wave kw takes K blocks kw,
 // kw+4, ... (each block: MTW x 2 MFMAs, the B fragments as the first operand
 // so a lane ends with one activation row and four weight columns, i.e. one
@@ -409,24 +409,23 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
 // kw, kw + 4, ... of its group (bias, bf16 rounding).  At M = 128 and
 // N = 1280 that is 40 workgroups where the 128 x 128 tile kernel has 10,
 // with no split-K workspace or second kernel.
-constexpr int SK_BN = 32;
 
 // KW waves of a group split the K blocks (4, or 8 / 16 for one 16-row tile
 // and long K: more K blocks in flight at once, still one launch).
-template <int MTW, int WGM, int KW = 4>
+template <int MTW, int WGM, int KW = 4, int NT = 2>
 __global__ __launch_bounds__(64 * KW * WGM) void fp8_gemm_skinny(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ B,
     const float* __restrict__ Bs, const float* __restrict__ bias, int64_t bias_ld, uint16_t* __restrict__ C,
     int M, int N, int K) {
-  __shared__ __attribute__((aligned(16))) v4f red[WGM][KW][MTW][2][64];
+  __shared__ __attribute__((aligned(16))) v4f red[WGM][KW][MTW][NT][64];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int gm = wave / KW, kw = wave % KW;
   const int r16 = lane & 15, g = lane >> 4;
-  const int n0 = blockIdx.x * SK_BN;
+  const int n0 = blockIdx.x * 16 * NT;
   const int KT = K / BK;
-  const uint8_t* brow[2];
+  const uint8_t* brow[NT];
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) brow[nt] = B + (size_t)min(n0 + 16 * nt + r16, N - 1) * K + g * 16;
+  for (int nt = 0; nt < NT; ++nt) brow[nt] = B + (size_t)min(n0 + 16 * nt + r16, N - 1) * K + g * 16;
   // activation rows as 32-bit offsets (M * K < 2^31 is checked on the host)
   uint32_t aoff[MTW], soff[MTW];
 #pragma unroll
@@ -435,13 +434,13 @@ __global__ __launch_bounds__(64 * KW * WGM) void fp8_gemm_skinny(
     aoff[mt] = m * (uint32_t)K + g * 16;
     soff[mt] = m * (uint32_t)KT;
   }
-  const float* bsrow = Bs + (size_t)(n0 / 128) * KT;  // 32 columns share one 128-row scale block
+  const float* bsrow = Bs + (size_t)(n0 / 128) * KT;  // the 16 NT columns share one 128-row scale block
 
-  v4f acc[MTW][2];
+  v4f acc[MTW][NT];
 #pragma unroll
   for (int mt = 0; mt < MTW; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = v4f{0.f, 0.f, 0.f, 0.f};
 
   // operand chunks g and g + 4 of the 128-byte K block (both operands)
   auto ld = [](const uint8_t* p) -> v8i {
@@ -450,11 +449,11 @@ __global__ __launch_bounds__(64 * KW * WGM) void fp8_gemm_skinny(
     return __builtin_bit_cast(v8i, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
   };
   // two register buffers, filled alternately (no copies between them)
-  v8i bf0[2], af0[MTW], bf1[2], af1[MTW];
+  v8i bf0[NT], af0[MTW], bf1[NT], af1[MTW];
   float sa0[MTW], sa1[MTW], sb0 = 0.f, sb1 = 0.f;
-  auto load_block = [&](v8i (&bf)[2], v8i (&af)[MTW], float (&sa)[MTW], float& sb, int kb) {
+  auto load_block = [&](v8i (&bf)[NT], v8i (&af)[MTW], float (&sa)[MTW], float& sb, int kb) {
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) bf[nt] = ld(brow[nt] + (size_t)kb * BK);
+    for (int nt = 0; nt < NT; ++nt) bf[nt] = ld(brow[nt] + (size_t)kb * BK);
 #pragma unroll
     for (int mt = 0; mt < MTW; ++mt) {
       af[mt] = ld(A + aoff[mt] + (uint32_t)kb * BK);
@@ -462,12 +461,12 @@ __global__ __launch_bounds__(64 * KW * WGM) void fp8_gemm_skinny(
     }
     sb = bsrow[kb];
   };
-  auto compute = [&](const v8i (&bf)[2], const v8i (&af)[MTW], const float (&sa)[MTW], float sb) {
+  auto compute = [&](const v8i (&bf)[NT], const v8i (&af)[MTW], const float (&sa)[MTW], float sb) {
 #pragma unroll
     for (int mt = 0; mt < MTW; ++mt) {
       const float sc = sa[mt] * sb;
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
+      for (int nt = 0; nt < NT; ++nt) {
         const v4f t = mfma_fp8(bf[nt], af[mt]);
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[mt][nt][r] = fmaf(t[r], sc, acc[mt][nt][r]);
@@ -487,12 +486,12 @@ __global__ __launch_bounds__(64 * KW * WGM) void fp8_gemm_skinny(
 #pragma unroll
   for (int mt = 0; mt < MTW; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) red[gm][kw][mt][nt][lane] = acc[mt][nt];
+    for (int nt = 0; nt < NT; ++nt) red[gm][kw][mt][nt][lane] = acc[mt][nt];
   __syncthreads();
   for (int mt = kw; mt < MTW; mt += KW) {
     const int m = 16 * (gm * MTW + mt) + r16;
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
+    for (int nt = 0; nt < NT; ++nt) {
       v4f s = red[gm][0][mt][nt][lane];
 #pragma unroll
       for (int w = 1; w < KW; ++w) {
@@ -1136,20 +1135,28 @@ extern "C" int lfs_fp8_gemm_skinny(const void* a, const float* a_s, const void* 
   LFS_REQUIRE(K > 0 && a && a_s && b && b_s && c, "fp8_gemm_skinny: null pointer");
   LFS_REQUIRE((((uintptr_t)a | (uintptr_t)b) & 15u) == 0, "fp8_gemm_skinny: a and b must be 16-byte aligned");
   LFS_REQUIRE(bias_ld == 0 || (bias != nullptr && bias_ld >= N), "fp8_gemm_skinny: bias_ld must be 0 or >= N");
-  const dim3 grid((unsigned)((N + SK_BN - 1) / SK_BN));
   hipStream_t st = (hipStream_t)stream;
   const int mt = (int)((M + 15) / 16);
   const int KT = (int)(K / 128);
-#define LFS_SK(MTW, WGM, KW)                                                                               \
-  hipLaunchKernelGGL((fp8_gemm_skinny<MTW, WGM, KW>), grid, dim3(64 * KW * WGM), 0, st, (const uint8_t*)a,  \
+  // one 16-row tile and N <= 4096 (<= 128 groups of 32 columns): groups of
+  // 16 columns, twice the workgroups (re-reading <= 16 activation rows costs
+  // little).  Measured back to back at M = 16: K 1024 / N 4096 4.8 -> 3.9 us,
+  // K 4096 / N 1024 9.5 -> 7.3 us; at N = 5632 (176 groups of 32) 6.6 -> 7.4 us
+  const bool narrow = mt <= 1 && N <= 4096;
+  const dim3 grid((unsigned)((N + (narrow ? 15 : 31)) / (narrow ? 16 : 32)));
+#define LFS_SK(MTW, WGM, KW, NT)                                                                                \
+  hipLaunchKernelGGL((fp8_gemm_skinny<MTW, WGM, KW, NT>), grid, dim3(64 * KW * WGM), 0, st, (const uint8_t*)a,   \
                      a_s, (const uint8_t*)b, b_s, bias, bias_ld, (uint16_t*)c, (int)M, (int)N, (int)K)
   // one 16-row tile: the K blocks over 16 / 8 / 4 waves (>= 1.5 blocks per wave)
-  if (mt <= 1 && KT >= 24) LFS_SK(1, 1, 16);
-  else if (mt <= 1 && KT >= 12) LFS_SK(1, 1, 8);
-  else if (mt <= 1) LFS_SK(1, 1, 4);
-  else if (mt <= 2) LFS_SK(2, 1, 4);
-  else if (mt <= 4) LFS_SK(4, 1, 4);
-  else LFS_SK(4, 2, 4);
+  if (narrow && KT >= 24) LFS_SK(1, 1, 16, 1);
+  else if (narrow && KT >= 12) LFS_SK(1, 1, 8, 1);
+  else if (narrow) LFS_SK(1, 1, 4, 1);
+  else if (mt <= 1 && KT >= 24) LFS_SK(1, 1, 16, 2);
+  else if (mt <= 1 && KT >= 12) LFS_SK(1, 1, 8, 2);
+  else if (mt <= 1) LFS_SK(1, 1, 4, 2);
+  else if (mt <= 2) LFS_SK(2, 1, 4, 2);
+  else if (mt <= 4) LFS_SK(4, 1, 4, 2);
+  else LFS_SK(4, 2, 4, 2);
 #undef LFS_SK
   return check_launch("fp8_gemm_skinny");
 }

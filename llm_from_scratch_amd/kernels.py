@@ -166,10 +166,12 @@ def fp8_gemm(a: torch.Tensor, a_s: torch.Tensor, b: torch.Tensor, b_s: torch.Ten
     The scale products are applied to each 128-wide K-block partial in an
     fp32 accumulator, the bias is added in fp32, and the result is rounded
     once to bf16 [..., N].  ``splits`` > 1 splits the K blocks over that many
-    workgroups per output tile (fp32 partials, then one reduction); by
-    default decode-sized shapes (M <= 128, K <= 1024, N <= 4096) run the
-    skinny kernel (K split across the waves of a workgroup, 32 columns per
-    workgroup), and other shapes that cannot fill the GPU are split;
+    workgroups per output tile (fp32 partials, then one reduction).  By
+    default the shapes ``use_skinny_gemm`` selects -- M <= 16 with K <= 16384
+    and any N, or M <= 128 with K <= 1024 and N <= 4096 -- run the skinny
+    kernel (the K blocks split across the waves of one workgroup per 32
+    output columns, or per 16 when M <= 16 and N <= 4096), other shapes that
+    cannot fill the GPU are split, and the rest run the tile kernels;
     ``splits=1`` forces the tile kernel.
     """
     assert a.is_contiguous() and b.is_contiguous(), "Input tensors must be contiguous"

@@ -279,14 +279,18 @@ def test_fp8_gemm_split_k(splits):
 @pytest.mark.parametrize("M,N,Kd", [(1, 768, 768), (5, 1282, 128), (17, 250, 384), (33, 96, 1024),
                                     (100, 4096, 768), (128, 1280, 768), (128, 31, 512),
                                     (1, 1024, 4096), (7, 5632, 2048), (16, 96, 1536), (3, 250, 3072),
-                                    (1, 200, 3200)])
+                                    (1, 200, 3200), (16, 96, 16384), (16, 1024, 4608), (9, 4096, 1024),
+                                    (16, 4097, 2048), (2, 24, 256)])
 def test_fp8_gemm_skinny(M, N, Kd):
     """The decode-batch kernel (M <= 128, K blocks split over the waves of a
-    workgroup: four, or 8 / 16 for one 16-row tile and 12 / 24+ K blocks):
+    workgroup: four, or 8 / 16 for one 16-row tile and 12 / 24+ K blocks;
+    16-column groups for one 16-row tile and N <= 4096, 32 otherwise):
     every byte pattern but NaN, distinct scales, ragged M and N (N not a
-    multiple of 32 or of 4), 1 to 32 K blocks (fewer than and not a multiple
-    of the waves), bias vector and per-row bias matrix; against the oracle
-    and the 128 x 128 tile kernel."""
+    multiple of 16, 32 or 4), 1 to 128 K blocks (fewer than and not a
+    multiple of the waves; K = 16384 the longest K the dispatch sends here,
+    (16, 1024, 4608) the cfg5 down projection at 16 sequences), N on both
+    sides of the 4096 column-group switch, bias vector and per-row bias
+    matrix; against the oracle and the 128 x 128 tile kernel."""
     assert K.use_skinny_gemm(M, N, Kd)
     rng = np.random.default_rng(M * 7 + N + Kd)
     ac = rng.integers(0, 256, (M, Kd), dtype=np.uint8)
