@@ -1189,22 +1189,26 @@ extern "C" int lfs_fp8_gemm_skinny(const void* a, const float* a_s, const void* 
   hipStream_t st = (hipStream_t)stream;
   const int mt = (int)((M + 15) / 16);
   const int KT = (int)(K / 128);
-  // one 16-row tile and N <= 4096 (<= 128 groups of 32 columns): groups of
-  // 16 columns, twice the workgroups (re-reading <= 16 activation rows costs
-  // little).  Measured back to back at M = 16: K 1024 / N 4096 4.8 -> 3.9 us,
-  // K 4096 / N 1024 9.5 -> 7.3 us; at N = 5632 (176 groups of 32) 6.6 -> 7.4 us
-  const bool narrow = mt <= 1 && N <= 4096;
+  // N <= 4096 (<= 128 groups of 32 columns): groups of 16 columns, twice
+  // the workgroups, each re-reading all M activation rows.  Measured back to
+  // back: M = 16, K 1024 / N 4096 4.8 -> 3.9 us, K 4096 / N 1024 9.5 -> 7.3
+  // us; M = 128, K 768 / N 1280 7.9 -> 6.7 us, K 1024 / N 4096 10.8 -> 9.6
+  // us; but M = 16, N = 5632 (176 groups of 32) 6.6 -> 7.4 us
+  const bool narrow = N <= 4096;
   const dim3 grid((unsigned)((N + (narrow ? 15 : 31)) / (narrow ? 16 : 32)));
 #define LFS_SK(MTW, WGM, KW, NT)                                                                                \
   hipLaunchKernelGGL((fp8_gemm_skinny<MTW, WGM, KW, NT>), grid, dim3(64 * KW * WGM), 0, st, (const uint8_t*)a,   \
                      a_s, (const uint8_t*)b, b_s, bias, bias_ld, (uint16_t*)c, (int)M, (int)N, (int)K)
   // one 16-row tile: the K blocks over 16 / 8 / 4 waves (>= 1.5 blocks per wave)
-  if (narrow && KT >= 24) LFS_SK(1, 1, 16, 1);
-  else if (narrow && KT >= 12) LFS_SK(1, 1, 8, 1);
-  else if (narrow) LFS_SK(1, 1, 4, 1);
+  if (narrow && mt <= 1 && KT >= 24) LFS_SK(1, 1, 16, 1);
+  else if (narrow && mt <= 1 && KT >= 12) LFS_SK(1, 1, 8, 1);
+  else if (narrow && mt <= 1) LFS_SK(1, 1, 4, 1);
   else if (mt <= 1 && KT >= 24) LFS_SK(1, 1, 16, 2);
   else if (mt <= 1 && KT >= 12) LFS_SK(1, 1, 8, 2);
   else if (mt <= 1) LFS_SK(1, 1, 4, 2);
+  else if (narrow && mt <= 2) LFS_SK(2, 1, 4, 1);
+  else if (narrow && mt <= 4) LFS_SK(4, 1, 4, 1);
+  else if (narrow) LFS_SK(4, 2, 4, 1);
   else if (mt <= 2) LFS_SK(2, 1, 4, 2);
   else if (mt <= 4) LFS_SK(4, 1, 4, 2);
   else LFS_SK(4, 2, 4, 2);

@@ -170,7 +170,7 @@ def fp8_gemm(a: torch.Tensor, a_s: torch.Tensor, b: torch.Tensor, b_s: torch.Ten
     default the shapes ``use_skinny_gemm`` selects -- M <= 16 with K <= 16384
     and any N, or M <= 128 with K <= 1024 and N <= 4096 -- run the skinny
     kernel (the K blocks split across the waves of one workgroup per 32
-    output columns, or per 16 when M <= 16 and N <= 4096), other shapes that
+    output columns, or per 16 when N <= 4096), other shapes that
     cannot fill the GPU are split, and the rest run the tile kernels;
     ``splits=1`` forces the tile kernel.
     """

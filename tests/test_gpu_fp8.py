@@ -284,7 +284,7 @@ def test_fp8_gemm_split_k(splits):
 def test_fp8_gemm_skinny(M, N, Kd):
     """The decode-batch kernel (M <= 128, K blocks split over the waves of a
     workgroup: four, or 8 / 16 for one 16-row tile and 12 / 24+ K blocks;
-    16-column groups for one 16-row tile and N <= 4096, 32 otherwise):
+    16-column groups for N <= 4096, 32 otherwise):
     every byte pattern but NaN, distinct scales, ragged M and N (N not a
     multiple of 16, 32 or 4), 1 to 128 K blocks (fewer than and not a
     multiple of the waves; K = 16384 the longest K the dispatch sends here,
