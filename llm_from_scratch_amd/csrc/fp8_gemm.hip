@@ -273,9 +273,11 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
   // re-copies block KT-1 into the stage just read, which is never read
   // again), so that exactly NST-1 copy groups follow block kt's and the wait
   // below is one constant count.
-  load_scales(0);
+  // the stage copies go out first: the scale table's loads (whose values
+  // must be in registers before they are staged) then share their round trip
 #pragma unroll
   for (int s = 0; s < NST; ++s) issue(min(s, KT - 1), s);
+  load_scales(0);
 
   for (int kt = 0; kt < KT; ++kt) {
     if (kt > 0 && kt % SCK == 0) load_scales(kt);  // old chunk last read before the previous B2
