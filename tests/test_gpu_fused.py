@@ -181,7 +181,8 @@ def test_swiglu_quant(T, E, F):
 
 
 @pytest.mark.parametrize("T,d,E,S,top_k,with_res", [(128, 768, 8, 1, 2, True), (37, 1024, 16, 2, 4, False),
-                                                    (9, 2048, 8, 0, 1, True), (5, 4096, 32, 1, 3, True)])
+                                                    (9, 2048, 8, 0, 1, True), (5, 4096, 32, 1, 3, True),
+                                                    (64, 512, 4, 0, 1, True), (3, 1024, 6, 2, 2, False)])
 def test_add_rmsnorm_route_equals_norm_then_gate(T, d, E, S, top_k, with_res):
     """The fused ffn_norm + MoE gate launch gives the outputs of add_rmsnorm
     (quantised) followed by moe_route bit for bit: residual, codes, scales,
