@@ -30,6 +30,10 @@
  *                           counterpart
  *   lfs_fp8_gemm_splitk     the same GEMM split over K for small M (the
  *                           decode-step linears)
+ *   lfs_fp8_gemm_splitk_partials  its partial sums without the reduction,
+ *                           for a consumer that sums them itself
+ *                           (lfs_add_rmsnorm_partials); no reference
+ *                           counterpart
  *   lfs_fp8_gemm_skinny     the same GEMM for M <= 128 (decode batches):
  *                           K split across the waves of a workgroup
  *   lfs_store_kvcache       the KV slot write of the attention layer that
@@ -58,6 +62,10 @@
  * chain of torch ops of the reference model):
  *   lfs_add_rmsnorm         RMSNorm with fused residual add, model/utils.py:53-67
  *                           (+ act_quant of the output for the next FP8 linear)
+ *   lfs_add_rmsnorm_partials  the same with x the split-K reduction of the
+ *                           previous FP8 linear (the MoE down projection
+ *                           feeding the next layer's fused add & norm,
+ *                           model/transformer.py:90-118)
  *   lfs_qk_norm_rope_store  q_norm/k_norm + RoPE + KV slot write,
  *                           model/attention/GQA.py:80-95,
  *                           model/attention/utils.py:34-45
@@ -91,7 +99,7 @@
 extern "C" {
 #endif
 
-#define LFS_ABI_VERSION 10
+#define LFS_ABI_VERSION 11
 
 /* argument errors (negative); launch errors are positive hipError_t values */
 #define LFS_EINVAL (-1)
@@ -158,6 +166,17 @@ int64_t lfs_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t sp
 int lfs_fp8_gemm_splitk(const void* a, const float* a_s, const void* b, const float* b_s,
                         const float* bias, int64_t bias_ld, void* c, int64_t M, int64_t N, int64_t K,
                         int32_t splits, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * The first kernel of lfs_fp8_gemm_splitk alone: the fp32 partial sums
+ * workspace[s][M][N] for s < n, n = ceil(KT / ceil(KT / splits)), KT = K/128
+ * (no bias, no C).  The split must leave n >= 2 (an argument error
+ * otherwise).  Summing them in order s = 0 .. n-1 from 0.f, adding the bias
+ * and rounding to bf16 gives lfs_fp8_gemm_splitk's C bit for bit.
+ */
+int lfs_fp8_gemm_splitk_partials(const void* a, const float* a_s, const void* b, const float* b_s, int64_t M,
+                                 int64_t N, int64_t K, int32_t splits, void* workspace, int64_t workspace_bytes,
+                                 void* stream);
 
 /*
  * fp8_gemm for decode-sized batches, M <= 128: the same result as
@@ -295,6 +314,17 @@ int lfs_sample_gumbel(const void* logits, int64_t ld, const float* temperatures,
 int lfs_add_rmsnorm(const void* x, const void* residual, const float* weight, void* out,
                     void* residual_out, void* q, float* q_scale, int64_t T, int32_t d, float eps,
                     void* stream);
+
+/*
+ * lfs_add_rmsnorm with x[t] = bf16(sum over s < nparts of parts[s][t] (fp32
+ * [nparts][T][d], summed in order from 0.f) + bias[t]): the output of
+ * lfs_fp8_gemm_splitk_partials followed by the reduction lfs_fp8_gemm_splitk
+ * performs, bit for bit, without its launch.  bias: NULL, fp32 [d]
+ * (bias_ld 0) or rows bias_ld >= d floats apart.  d % 8 == 0, d <= 1024.
+ */
+int lfs_add_rmsnorm_partials(const float* parts, int32_t nparts, const float* bias, int64_t bias_ld,
+                             const void* residual, const float* weight, void* out, void* residual_out, void* q,
+                             float* q_scale, int64_t T, int32_t d, float eps, void* stream);
 
 /*
  * qk_norm_rope_store, per token t of qkv: bf16 [T, ld], row = [q (Hq*D) |

@@ -11,7 +11,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "liblfs_kernels.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 # size of the library's static paged-decode workspace (LFS_DECODE_SCRATCH_BYTES)
 DECODE_SCRATCH_BYTES = 64 << 20
 
@@ -40,6 +40,10 @@ SIGNATURES = {
     "lfs_paged_decode_noalloc": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i32, _c_i32,
                                                 _c_i32, _c_i32, _c_i64, _c_i32, _c_f, _c_i32, _c_p, _c_p, _c_p]),
     "lfs_add_rmsnorm": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_f, _c_p]),
+    "lfs_add_rmsnorm_partials": (ctypes.c_int, [_c_p, _c_i32, _c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
+                                                _c_i64, _c_i32, _c_f, _c_p]),
+    "lfs_fp8_gemm_splitk_partials": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p,
+                                                    _c_i64, _c_p]),
     "lfs_qk_norm_rope_store": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
                                               _c_i64, _c_i32, _c_i32, _c_i32, _c_i64, _c_i64, _c_f, _c_p]),
     "lfs_add_rmsnorm_route": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_f,

@@ -1062,19 +1062,22 @@ bool use_persistent(int64_t M, int64_t N, int64_t K, const float* bias, int64_t 
          256 * K < (1ll << 31) && K >= 256 && 2 * t >= cu_count();
 }
 
+// reduce == false: split-K partials only (ws[s][M][N] fp32, no bias, C not
+// written); at least two K splits must result.
 int fp8_gemm_impl(const void* a, const float* a_s, const void* b, const float* b_s, const float* bias,
                   int64_t bias_ld, void* c, int64_t M, int64_t N, int64_t K, int32_t splits,
-                  void* workspace, int64_t workspace_bytes, void* stream) {
+                  void* workspace, int64_t workspace_bytes, void* stream, bool reduce = true) {
   LFS_REQUIRE(M >= 0 && N >= 0 && K >= 0, "fp8_gemm: negative shape");
   LFS_REQUIRE(K % 128 == 0, "fp8_gemm: K=%lld must be a multiple of 128", (long long)K);
   LFS_REQUIRE(M < (1ll << 31) && N < (1ll << 31) && K < (1ll << 31) && M * K < (1ll << 40),
               "fp8_gemm: shape too large");
   LFS_REQUIRE(splits >= 1, "fp8_gemm: splits must be >= 1");
   if (M == 0 || N == 0) return 0;
-  LFS_REQUIRE(a && a_s && b && b_s && c, "fp8_gemm: null pointer");
+  LFS_REQUIRE(a && a_s && b && b_s && (c || !reduce), "fp8_gemm: null pointer");
   LFS_REQUIRE(K > 0, "fp8_gemm: K must be positive");
   LFS_REQUIRE((((uintptr_t)a | (uintptr_t)b) & 15u) == 0, "fp8_gemm: a and b must be 16-byte aligned");
   LFS_REQUIRE(((uintptr_t)c & 15u) == 0, "fp8_gemm: c must be 16-byte aligned");
+  LFS_REQUIRE(reduce || bias == nullptr, "fp8_gemm_splitk_partials: the bias is added by the consumer");
   LFS_REQUIRE(bias_ld == 0 || (bias != nullptr && bias_ld >= N), "fp8_gemm: bias_ld must be 0 or >= N");
   const int64_t tiles_n = (N + BN - 1) / BN;
   const int64_t tiles_m128 = (M + 127) / 128;
@@ -1092,6 +1095,8 @@ int fp8_gemm_impl(const void* a, const float* a_s, const void* b, const float* b
   } else {
     kps = KT;
   }
+  LFS_REQUIRE(reduce || ws != nullptr, "fp8_gemm_splitk_partials: K=%lld in %d splits gives one split",
+              (long long)K, splits);
   hipStream_t st = (hipStream_t)stream;
   if (ws == nullptr && use_persistent(M, N, K, bias, bias_ld)) {
     const int64_t bm = (M + BIG - 1) / BIG, bn = N / BIG;
@@ -1118,7 +1123,7 @@ int fp8_gemm_impl(const void* a, const float* a_s, const void* b, const float* b
                      (uint16_t*)c, (int)M, (int)N, (int)K, (int)tiles_m128, (int)tiles_n, ws, kps, (int64_t)K,
                      (int)KT, Grouped{});
   int rc = check_launch("fp8_gemm");
-  if (rc != 0 || ws == nullptr) return rc;
+  if (rc != 0 || ws == nullptr || !reduce) return rc;
   if (N % 8 == 0 && ((uintptr_t)c & 15u) == 0 && M * (N / 8) < (1ll << 31) - 256) {
     const int64_t octs = M * (N / 8);
     hipLaunchKernelGGL(splitk_reduce8, dim3((unsigned)((octs + 255) / 256)), dim3(256), 0, st, ws, used, bias,
@@ -1144,6 +1149,13 @@ extern "C" int lfs_fp8_gemm_splitk(const void* a, const float* a_s, const void* 
                                    void* stream) {
   return fp8_gemm_impl(a, a_s, b, b_s, bias, bias_ld, c, M, N, K, splits, workspace, workspace_bytes,
                        stream);
+}
+
+extern "C" int lfs_fp8_gemm_splitk_partials(const void* a, const float* a_s, const void* b, const float* b_s,
+                                            int64_t M, int64_t N, int64_t K, int32_t splits, void* workspace,
+                                            int64_t workspace_bytes, void* stream) {
+  return fp8_gemm_impl(a, a_s, b, b_s, nullptr, 0, nullptr, M, N, K, splits, workspace, workspace_bytes, stream,
+                       false);
 }
 
 extern "C" int lfs_fp8_grouped_gemm(const void* a, const float* a_s, int64_t a_rows, const int32_t* row_index,

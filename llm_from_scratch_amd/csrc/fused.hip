@@ -58,12 +58,53 @@ __device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, 
 // 16 consecutive chunks, which sit in 16 consecutive lanes of one wave.
 // (h_lds: optionally also the bf16 output row, for a consumer in the same
 // workgroup)
-template <int CPT, bool QUANT, int NW = 2>
+// x from split-K partials: the row is bf16(sum of nparts fp32 partial rows
+// in order from 0.f, plus the bias), the value and rounding splitk_reduce8
+// writes for the same partials (parts[s][row][col], s < nparts, rows MN
+// floats apart; bias null, a vector (bias_ld 0) or a per-row matrix).
+struct RowParts {
+  const float* parts;
+  int nparts;
+  int64_t MN;
+  const float* bias;
+  int64_t bias_ld;
+};
+
+__device__ __forceinline__ void parts_chunk(const RowParts& rp, int64_t row, int d, int c, float (&f)[8]) {
+  const float* src = rp.parts + row * d + c * 8;
+  float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < rp.nparts; s0 += 8) {
+    float4 lo[8], hi[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (s0 + j < rp.nparts) {
+        lo[j] = *reinterpret_cast<const float4*>(src + (s0 + j) * rp.MN);
+        hi[j] = *reinterpret_cast<const float4*>(src + (s0 + j) * rp.MN + 4);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (s0 + j < rp.nparts) {
+        v[0] += lo[j].x; v[1] += lo[j].y; v[2] += lo[j].z; v[3] += lo[j].w;
+        v[4] += hi[j].x; v[5] += hi[j].y; v[6] += hi[j].z; v[7] += hi[j].w;
+      }
+    }
+  }
+  if (rp.bias != nullptr) {
+    const float* b = rp.bias + (rp.bias_ld ? row * rp.bias_ld : 0) + c * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] += b[e];
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] = bf16_to_f32(f32_to_bf16(v[e]));
+}
+
+template <int CPT, bool QUANT, int NW = 2, bool PARTS = false>
 __device__ __forceinline__ void add_rmsnorm_row(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ residual,
     const float* __restrict__ w, uint16_t* __restrict__ out, uint16_t* __restrict__ res_out,
     uint8_t* __restrict__ q, float* __restrict__ qs, int d, float eps, int64_t row, float* red,
-    uint16_t* h_lds) {
+    uint16_t* h_lds, const RowParts& rp = RowParts{}) {
   const int cpr = d / 8;
   float f[CPT][8];
   float4 wq[CPT][2];  // weights, loaded before the reduction
@@ -74,7 +115,8 @@ __device__ __forceinline__ void add_rmsnorm_row(
     if (c < cpr && threadIdx.x < 128) {  // chunks on the first 128 threads only
       wq[i][0] = *reinterpret_cast<const float4*>(w + c * 8);
       wq[i][1] = *reinterpret_cast<const float4*>(w + c * 8 + 4);
-      unpack8(*reinterpret_cast<const uint4*>(x + row * d + c * 8), f[i]);
+      if constexpr (PARTS) parts_chunk(rp, row, d, c, f[i]);
+      else unpack8(*reinterpret_cast<const uint4*>(x + row * d + c * 8), f[i]);
       if (residual != nullptr) {
         float r[8];
         unpack8(*reinterpret_cast<const uint4*>(residual + row * d + c * 8), r);
@@ -134,6 +176,17 @@ __global__ __launch_bounds__(128) void add_rmsnorm_kernel(
     uint8_t* __restrict__ q, float* __restrict__ qs, int d, float eps) {
   __shared__ float red[2];
   add_rmsnorm_row<CPT, QUANT>(x, residual, w, out, res_out, q, qs, d, eps, blockIdx.x, red, nullptr);
+}
+
+// add_rmsnorm whose x is the split-K reduction of a GEMM (its partials and
+// bias), so that the reduction needs no launch of its own
+template <bool QUANT>
+__global__ __launch_bounds__(128) void add_rmsnorm_parts_kernel(
+    RowParts rp, const uint16_t* __restrict__ residual, const float* __restrict__ w, uint16_t* __restrict__ out,
+    uint16_t* __restrict__ res_out, uint8_t* __restrict__ q, float* __restrict__ qs, int d, float eps) {
+  __shared__ float red[2];
+  add_rmsnorm_row<1, QUANT, 2, true>(nullptr, residual, w, out, res_out, q, qs, d, eps, blockIdx.x, red, nullptr,
+                                     rp);
 }
 
 // ----------------------------------------------------- qk_norm_rope_store --
@@ -564,6 +617,36 @@ extern "C" int lfs_add_rmsnorm(const void* x, const void* residual, const float*
   if (cpr <= 256) return launch_add_rmsnorm<2>(quant, x, residual, weight, out, residual_out, q, q_scale, T, d, eps, st);
   if (cpr <= 512) return launch_add_rmsnorm<4>(quant, x, residual, weight, out, residual_out, q, q_scale, T, d, eps, st);
   return launch_add_rmsnorm<8>(quant, x, residual, weight, out, residual_out, q, q_scale, T, d, eps, st);
+}
+
+extern "C" int lfs_add_rmsnorm_partials(const float* parts, int32_t nparts, const float* bias, int64_t bias_ld,
+                                        const void* residual, const float* weight, void* out, void* residual_out,
+                                        void* q, float* q_scale, int64_t T, int32_t d, float eps, void* stream) {
+  LFS_REQUIRE(T >= 0 && d > 0 && nparts >= 1, "add_rmsnorm_partials: bad shape");
+  LFS_REQUIRE(d % 8 == 0 && d <= 128 * 8, "add_rmsnorm_partials: d=%d must be a multiple of 8 and <= 1024", d);
+  LFS_REQUIRE((residual == nullptr) == (residual_out == nullptr),
+              "add_rmsnorm_partials: residual and residual_out go together");
+  LFS_REQUIRE((q == nullptr) == (q_scale == nullptr), "add_rmsnorm_partials: q and q_scale go together");
+  LFS_REQUIRE(q == nullptr || d % 128 == 0, "add_rmsnorm_partials: quantised output needs d %% 128 == 0");
+  LFS_REQUIRE(out != nullptr || q != nullptr, "add_rmsnorm_partials: no output");
+  LFS_REQUIRE(bias_ld == 0 || (bias != nullptr && bias_ld >= d), "add_rmsnorm_partials: bias_ld must be 0 or >= d");
+  if (T == 0) return 0;
+  LFS_REQUIRE(parts && weight, "add_rmsnorm_partials: null pointer");
+  LFS_REQUIRE(((uintptr_t)parts | (uintptr_t)residual | (uintptr_t)out | (uintptr_t)residual_out |
+               (uintptr_t)weight | (uintptr_t)q) % 16 == 0,
+              "add_rmsnorm_partials: buffers must be 16-byte aligned");
+  LFS_REQUIRE(T < (1ll << 31), "add_rmsnorm_partials: too many rows");
+  const RowParts rp{parts, nparts, T * d, bias, bias_ld};
+  hipStream_t st = (hipStream_t)stream;
+  if (q != nullptr)
+    hipLaunchKernelGGL((add_rmsnorm_parts_kernel<true>), dim3((unsigned)T), dim3(128), 0, st, rp,
+                       (const uint16_t*)residual, weight, (uint16_t*)out, (uint16_t*)residual_out, (uint8_t*)q,
+                       q_scale, d, eps);
+  else
+    hipLaunchKernelGGL((add_rmsnorm_parts_kernel<false>), dim3((unsigned)T), dim3(128), 0, st, rp,
+                       (const uint16_t*)residual, weight, (uint16_t*)out, (uint16_t*)residual_out, (uint8_t*)q,
+                       q_scale, d, eps);
+  return check_launch("add_rmsnorm_partials");
 }
 
 extern "C" int lfs_qk_norm_rope_store(const void* qkv, int64_t ld, const float* q_weight,

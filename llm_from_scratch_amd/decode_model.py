@@ -40,7 +40,7 @@ from __future__ import annotations
 
 import math
 from dataclasses import dataclass
-from typing import Optional
+from typing import NamedTuple, Optional
 
 import torch
 from torch import nn
@@ -76,6 +76,14 @@ class DecodeModelConfig:
         return d
 
 
+class SplitKOutput(NamedTuple):
+    """An FP8 linear's output left as its split-K partial sums (fp32 [n, T, d])
+    and bias: the next add & norm reduces it (kernels.add_rmsnorm_partials),
+    so the reduction costs no launch of its own."""
+    parts: torch.Tensor
+    bias: Optional[torch.Tensor]
+
+
 class RMSNorm(nn.Module):
     """model/utils.py:44-67: fp32 compute, optional fused residual add; runs
     as one add_rmsnorm launch (optionally also quantising its output)."""
@@ -85,10 +93,14 @@ class RMSNorm(nn.Module):
         self.eps = eps
         self.weight = nn.Parameter(torch.ones(d, dtype=torch.float32, device=device))
 
-    def forward(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None, out: bool = True,
-                quant: bool = False):
+    def forward(self, x, residual: Optional[torch.Tensor] = None, out: bool = True, quant: bool = False):
         """-> (out, residual_out, q, q_scale); residual_out is x without a
-        residual (the reference returns (norm(x), x) in that case)."""
+        residual (the reference returns (norm(x), x) in that case).  x is a
+        bf16 tensor or a SplitKOutput (then a residual is required)."""
+        if isinstance(x, SplitKOutput):
+            assert residual is not None
+            return kernels.add_rmsnorm_partials(x.parts, x.bias, self.weight, self.eps, residual, out=out,
+                                                quant=quant)
         return kernels.add_rmsnorm(x, self.weight, self.eps, residual, out=out, quant=quant)
 
 
@@ -249,12 +261,20 @@ class MoE(nn.Module):
         return not (self.dispatch == "grouped" or (self.dispatch == "auto" and T > self.GROUPED_MIN_TOKENS))
 
     def forward_routed(self, hq: torch.Tensor, hs: torch.Tensor, w: torch.Tensor, bias: torch.Tensor,
-                       trace: Optional[dict] = None) -> torch.Tensor:
+                       trace: Optional[dict] = None, partials: bool = False):
         """The dense dispatch given the gate's weights and routed bias (from
-        moe_route, or from add_rmsnorm_route together with the ffn_norm)."""
+        moe_route, or from add_rmsnorm_route together with the ffn_norm).
+        With ``partials`` (and a down projection the dispatch splits over K)
+        the result is a SplitKOutput for the next add & norm to reduce."""
         T, F = hq.size(0), self.d_ff
         h13 = self.w13.gemm(hq, hs)
         gq, gs = kernels.swiglu_quant(h13.view(T, -1, 2, F), w)
+        N, K = self.w2.weight.shape
+        if partials and trace is None and not kernels.use_skinny_gemm(T, N, K):
+            splits = kernels.default_gemm_splits(T, N, K)
+            if kernels.splitk_used(K, splits) >= 2:
+                parts = kernels.fp8_gemm_splitk_partials(gq, gs, self.w2.weight, self.w2.weight_scale, splits)
+                return SplitKOutput(parts, bias)
         y = kernels.fp8_gemm(gq, gs, self.w2.weight, self.w2.weight_scale, bias)
         if trace is not None:
             trace.update(route_w=w, route_bias=bias, h13=h13, ffn_out=y)
@@ -303,7 +323,7 @@ class Block(nn.Module):
                 ffn.w2_bias, ffn.top_k, ffn.n_shared, out=trace is not None)
             if trace is not None:
                 trace.update(att_h=h, ffn_h=h2, res_mid=residual)
-            return ffn.forward_routed(hq, hs, w, bias, trace), residual
+            return ffn.forward_routed(hq, hs, w, bias, trace, partials=True), residual
         h2, residual, hq, hs = self.ffn_norm(x, residual, out=True, quant=True)
         if trace is not None:
             trace.update(att_h=h, ffn_h=h2, res_mid=residual)

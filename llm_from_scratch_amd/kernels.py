@@ -518,6 +518,72 @@ def add_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
     return y, (res_out if residual is not None else x), q, qs
 
 
+def splitk_used(K: int, splits: int) -> int:
+    """Number of fp32 partials a split-K GEMM over K writes for ``splits``
+    requested splits (consecutive runs of ceil((K/128) / splits) K blocks)."""
+    kt = K // 128
+    kps = -(-kt // max(1, splits))
+    return -(-kt // kps)
+
+
+def fp8_gemm_splitk_partials(a: torch.Tensor, a_s: torch.Tensor, b: torch.Tensor, b_s: torch.Tensor,
+                             splits: int) -> torch.Tensor:
+    """The split-K partial sums of fp8_gemm(a, a_s, b, b_s) without the
+    reduction: fp32 [n, M, N], n = splitk_used(K, splits) >= 2 (no bias).
+    Summing them in order with the bias and rounding to bf16 gives
+    fp8_gemm(..., splits=splits) bit for bit; add_rmsnorm_partials does that
+    as part of the next add & norm."""
+    assert a.is_contiguous() and b.is_contiguous(), "Input tensors must be contiguous"
+    assert a_s.is_contiguous() and b_s.is_contiguous(), "Scaling factor tensors must be contiguous"
+    _on_gpu(a, a_s, b, b_s)
+    _dtype(a, FP8, "a")
+    _dtype(b, FP8, "b")
+    K = a.size(-1)
+    M = a.numel() // K
+    N = b.size(0)
+    n = splitk_used(K, splits)
+    assert n >= 2, "fp8_gemm_splitk_partials needs at least two K splits"
+    parts = torch.empty(n, M, N, dtype=torch.float32, device=a.device)
+    rc = _lib.load().lfs_fp8_gemm_splitk_partials(_ptr(a), _ptr(a_s), _ptr(b), _ptr(b_s), M, N, K, splits,
+                                                  _ptr(parts), parts.numel() * 4, _stream(a))
+    _lib.check(rc, "fp8_gemm_splitk_partials")
+    return parts
+
+
+def add_rmsnorm_partials(parts: torch.Tensor, bias: Optional[torch.Tensor], weight: torch.Tensor, eps: float,
+                         residual: Optional[torch.Tensor] = None, out: bool = True, quant: bool = False):
+    """add_rmsnorm whose x is bf16(sum_s parts[s] + bias), the reduction
+    fp8_gemm's split-K would perform (parts: fp32 [n, T, d] from
+    fp8_gemm_splitk_partials; bias None, fp32 [d] or [T, d]); the same
+    returns as add_rmsnorm, bit-identical to reducing first."""
+    assert parts.dim() == 3 and parts.is_contiguous() and parts.dtype == torch.float32
+    n, T, d = parts.shape
+    _on_gpu(parts, weight)
+    _dtype(weight, torch.float32, "weight")
+    assert weight.is_contiguous() and weight.shape == (d,)
+    bias_ld = 0
+    if bias is not None:
+        _on_gpu(parts, bias)
+        _dtype(bias, torch.float32, "bias")
+        assert bias.stride(-1) == 1 and bias.size(-1) == d
+        bias_ld = 0 if bias.dim() == 1 else bias.stride(0)
+    res_out = None
+    if residual is not None:
+        _dtype(residual, torch.bfloat16, "residual")
+        assert residual.shape == (T, d) and residual.is_contiguous()
+        res_out = torch.empty_like(residual)
+    y = torch.empty(T, d, dtype=torch.bfloat16, device=parts.device) if out else None
+    q = qs = None
+    if quant:
+        q = torch.empty(T, d, dtype=FP8, device=parts.device)
+        qs = torch.empty(T, d // 128, dtype=torch.float32, device=parts.device)
+    rc = _lib.load().lfs_add_rmsnorm_partials(_ptr(parts), n, _ptr(bias), bias_ld, _ptr(residual), _ptr(weight),
+                                              _ptr(y), _ptr(res_out), _ptr(q), _ptr(qs), T, d, float(eps),
+                                              _stream(parts))
+    _lib.check(rc, "add_rmsnorm_partials")
+    return y, res_out, q, qs
+
+
 def qk_norm_rope_store(qkv: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor,
                        cos_sin: torch.Tensor, positions: torch.Tensor, num_q_heads: int,
                        num_kv_heads: int, eps: float, k_cache: Optional[torch.Tensor] = None,

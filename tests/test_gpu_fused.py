@@ -202,3 +202,39 @@ def test_add_rmsnorm_route_equals_norm_then_gate(T, d, E, S, top_k, with_res):
     assert torch.equal(q2.view(torch.uint8), q.view(torch.uint8)) and torch.equal(qs2, qs)
     assert torch.equal(rw2, rw) and torch.equal(rb2, rb)
     assert int((rw2[:, :E] > 0).sum(1).min()) == top_k and bool((rw2[:, E:] == 1).all())
+
+
+@pytest.mark.parametrize("T,d,Kd,splits,bias_kind", [(128, 768, 4608, 6, "matrix"), (37, 512, 2048, 3, "vector"),
+                                                    (5, 1024, 1536, 12, None), (64, 256, 3072, 8, "matrix")])
+def test_add_rmsnorm_partials_equals_reduce_then_norm(T, d, Kd, splits, bias_kind):
+    """add & norm over a split-K GEMM's partials (the cfg5 MoE down
+    projection feeding the next layer's att_norm) equals the split-K GEMM's
+    bf16 output followed by add_rmsnorm, bit for bit: residual, normalised
+    row, codes and scales; the partials summed in order with the bias equal
+    the GEMM's own split-K output."""
+    g = torch.Generator(device=DEV).manual_seed(T + d + Kd)
+    a = torch.randn(T, Kd, generator=g, device=DEV).to(torch.bfloat16)
+    wgt = (0.02 * torch.randn(d, Kd, generator=g, device=DEV)).to(torch.bfloat16)
+    aq, as_ = K.act_quant(a)
+    wq, ws = K.weight_quant(wgt)
+    bias = None
+    if bias_kind == "matrix":
+        bias = torch.randn(T, d, generator=g, device=DEV)
+    elif bias_kind == "vector":
+        bias = torch.randn(d, generator=g, device=DEV)
+    res = torch.randn(T, d, generator=g, device=DEV).to(torch.bfloat16)
+    nw = (1 + 0.1 * torch.randn(d, generator=g, device=DEV)).float()
+    parts = K.fp8_gemm_splitk_partials(aq, as_, wq, ws, splits)
+    assert parts.shape == (K.splitk_used(Kd, splits), T, d)
+    y = K.fp8_gemm(aq, as_, wq, ws, bias, splits=splits)
+    acc = torch.zeros(T, d, device=DEV)  # 0 + p0 + p1 + ... (+ bias), in fp32
+    for s in range(parts.size(0)):
+        acc = acc + parts[s]
+    if bias is not None:
+        acc = acc + bias
+    assert torch.equal(y, acc.to(torch.bfloat16))
+    h, r, q, qs = K.add_rmsnorm(y, nw, 1e-5, res, out=True, quant=True)
+    h2, r2, q2, qs2 = K.add_rmsnorm_partials(parts, bias, nw, 1e-5, res, out=True, quant=True)
+    torch.cuda.synchronize()
+    assert torch.equal(h2, h) and torch.equal(r2, r)
+    assert torch.equal(q2.view(torch.uint8), q.view(torch.uint8)) and torch.equal(qs2, qs)
