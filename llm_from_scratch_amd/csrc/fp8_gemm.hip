@@ -278,6 +278,16 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
 #pragma unroll
   for (int s = 0; s < NST; ++s) issue(min(s, KT - 1), s);
   load_scales(0);
+  // A bias vector is loaded now, inside the first copies' round trip: read
+  // in the epilogue it would cost short-K calls one more round trip there.
+  float bvec[4][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int col = n0 + wn * 64 + j * 16 + 4 * g + r;
+      bvec[j][r] = (bias != nullptr && bias_ld == 0 && ws == nullptr && col < N) ? bias[col] : 0.f;
+    }
 
   for (int kt = 0; kt < KT; ++kt) {
     if (kt > 0 && kt % SCK == 0) load_scales(kt);  // old chunk last read before the previous B2
@@ -354,14 +364,7 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int cl = j * 16 + 4 * g;  // first of this lane's 4 columns in the wave tile
-    float bv[4] = {0.f, 0.f, 0.f, 0.f};
-    if (bias != nullptr && bias_ld == 0) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int col = n0 + wn * 64 + cl + r;
-        bv[r] = col < N ? bias[col] : 0.f;
-      }
-    }
+    float bv[4] = {bvec[j][0], bvec[j][1], bvec[j][2], bvec[j][3]};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int rl = i * 16 + r16;
@@ -476,6 +479,16 @@ __global__ __launch_bounds__(64 * KW * WGM) void fp8_gemm_skinny(
     }
   };
   if (kw < KT) load_block(bf0, af0, sa0, sb0, kw);
+  // a bias vector rides the first round trip (read after the reduction it
+  // would add one at the end)
+  float bvec[NT][4];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int col = n0 + 16 * nt + 4 * g + r;
+      bvec[nt][r] = (bias != nullptr && bias_ld == 0 && kw < MTW && col < N) ? bias[col] : 0.f;
+    }
   for (int kb = kw; kb < KT; kb += 2 * KW) {
     if (kb + KW < KT) load_block(bf1, af1, sa1, sb1, kb + KW);
     compute(bf0, af0, sa0, sb0);
@@ -503,11 +516,11 @@ __global__ __launch_bounds__(64 * KW * WGM) void fp8_gemm_skinny(
       }
       const int col = n0 + 16 * nt + 4 * g;
       if (m >= M) continue;
-      float bv[4] = {0.f, 0.f, 0.f, 0.f};
-      if (bias != nullptr) {
+      float bv[4] = {bvec[nt][0], bvec[nt][1], bvec[nt][2], bvec[nt][3]};
+      if (bias != nullptr && bias_ld != 0) {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (col + r < N) bv[r] = bias_ld == 0 ? bias[col + r] : bias[(int64_t)m * bias_ld + col + r];
+          if (col + r < N) bv[r] = bias[(int64_t)m * bias_ld + col + r];
       }
       uint16_t* dst = C + (size_t)m * N + col;
       if (col + 3 < N && (N & 3) == 0) {
