@@ -35,17 +35,18 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t h16) {
 __device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
-// fp32 -> bf16 bits, round to nearest even (NaN kept quiet)
-// (a select, not a branch: a per-value branch compiles to exec-mask
-// juggling around every conversion)
-__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
-  const uint32_t u = __float_as_uint(f);
-  const uint32_t rne = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-  const uint32_t nan = (u >> 16) | 0x40u;
-  return (u & 0x7FFFFFFFu) > 0x7F800000u ? nan : rne;
-}
+// fp32 -> bf16 bits: round to nearest even, a NaN keeps its sign and upper
+// payload bits with the quiet bit set ((u >> 16) | 0x40).  gfx950's
+// v_cvt_pk_bf16_f32 computes exactly this for every one of the 2^32 fp32
+// inputs (compared exhaustively against the integer formula on the GPU), in
+// one instruction per pair.
+typedef float lfs_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 lfs_bf16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(lfs_f32x2{lo, hi}, lfs_bf16x2));
+}
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
 // eight bf16 (one 16-byte chunk) -> floats
