@@ -144,20 +144,23 @@ struct Grouped {
   int a_rows;
 };
 
-template <int BM, int NST, int SCK, bool GROUPED = false>
-__global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
+template <int BM, int NST, int SCK, bool GROUPED = false, int KS = 1>
+__global__ __launch_bounds__(BM * 2 * KS, KS == 1 ? 256 / BM : 1) void fp8_gemm_tile(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ B,
     const float* __restrict__ Bs, const float* __restrict__ bias, int64_t bias_ld, uint16_t* __restrict__ C, int M,
     int N, int K, int tiles_m, int tiles_n, float* __restrict__ ws, int kps, int64_t ldb, int ldbs, Grouped grp) {
-  constexpr int NW = BM / 32;  // waves
-  constexpr int NT = 64 * NW;  // threads
-  constexpr int SCP = BM + 1;  // padded row of the k-major scale table
+  constexpr int NW = BM / 32;       // waves per K slice
+  constexpr int NT = 64 * NW * KS;  // threads
+  constexpr int SCP = BM + 1;       // padded row of the k-major scale table
   constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK;
-  constexpr int STAGE = A_BYTES + B_BYTES;
+  constexpr int SLOT = A_BYTES + B_BYTES;  // one K block
+  constexpr int STAGE = KS * SLOT;         // one K block per slice
   constexpr int A_PER_WAVE = A_BYTES / 1024 / NW;  // 1 KB (8-row) segments per wave
   constexpr int B_PER_WAVE = B_BYTES / 1024 / NW;
   constexpr int LOADS = A_PER_WAVE + B_PER_WAVE;  // DMA instructions per wave per stage
   static_assert(NW * 8192 <= NST * STAGE, "epilogue staging must fit the stage buffers");
+  static_assert(KS == 1 || (KS - 1) * NW * 16384 <= NST * STAGE, "slice partials must fit the stage buffers");
+  static_assert(SCK % KS == 0, "a scale chunk holds whole iterations");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * STAGE];
   __shared__ __attribute__((aligned(16))) float ssc[SCK * SCP];
 
@@ -193,7 +196,11 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  // KS > 1: KS slices of NW waves; slice ks multiplies K blocks ks, ks + KS,
+  // ... of the range (two waves per SIMD on a workgroup that has its CU to
+  // itself), and the slices' sums are added through LDS at the end
+  const int ks = __builtin_amdgcn_readfirstlane((tid >> 6) / NW);  // wave-uniform (SGPR)
+  const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) % NW);
   const int wm = wave >> 1, wn = wave & 1;
   const int KTA = K / BK;                  // K blocks of a row (scale row stride)
   // split-K: this workgroup sums K blocks kb0 .. kb0+KT-1 (blockIdx.y-th
@@ -223,8 +230,8 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
   const float* bs_row = Bs + (size_t)(n0 / 128) * ldbs + kb0;
   const float* as_base = As + kb0;
 
-  auto issue = [&](int kt, int buf) {
-    const unsigned base = lds0 + buf * STAGE;
+  auto issue = [&](int kt, int buf) {  // K block kt into slot ks of stage buf
+    const unsigned base = lds0 + buf * STAGE + ks * SLOT;
 #pragma unroll
     for (int u = 0; u < A_PER_WAVE; ++u) dma16(srcA[u] + kt * BK, base + (wave + NW * u) * 1024);
 #pragma unroll
@@ -275,8 +282,11 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
   // below is one constant count.
   // the stage copies go out first: the scale table's loads (whose values
   // must be in registers before they are staged) then share their round trip
+  // (KS > 1: iteration it holds blocks it*KS .. it*KS + KS-1, slot ks
+  // holding block it*KS + ks; a slot past the last block re-copies it)
+  const int IT = (KT + KS - 1) / KS;
 #pragma unroll
-  for (int s = 0; s < NST; ++s) issue(min(s, KT - 1), s);
+  for (int s = 0; s < NST; ++s) issue(min(s * KS + ks, KT - 1), s);
   load_scales(0);
   // A bias vector is loaded now, inside the first copies' round trip: read
   // in the epilogue it would cost short-K calls one more round trip there.
@@ -289,11 +299,12 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
       bvec[j][r] = (bias != nullptr && bias_ld == 0 && ws == nullptr && col < N) ? bias[col] : 0.f;
     }
 
-  for (int kt = 0; kt < KT; ++kt) {
-    if (kt > 0 && kt % SCK == 0) load_scales(kt);  // old chunk last read before the previous B2
-    wait_vm<(NST - 1) * LOADS>();  // this wave's copies of block kt landed
-    __syncthreads();  // B1: block kt (and the scale chunk) visible to every wave
-    const uint8_t* st = smem + (kt % NST) * STAGE;
+  for (int it = 0; it < IT; ++it) {
+    const int kt = it * KS + ks;  // this slice's K block (past the range: nothing to multiply)
+    if (it > 0 && (it * KS) % SCK == 0) load_scales(it * KS);  // old chunk last read before the previous B2
+    wait_vm<(NST - 1) * LOADS>();  // this wave's copies of iteration it landed
+    __syncthreads();  // B1: iteration it (and the scale chunk) visible to every wave
+    const uint8_t* st = smem + (it % NST) * STAGE + ks * SLOT;
     const int kc = kt % SCK;
     v8i fa[4], fb[4];
     float sc[4];
@@ -304,12 +315,13 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
       sc[i] = scrow[kc * SCP + i * 16];
     }
     wait_lgkm0();     // this wave's reads of the buffer have completed
-    __syncthreads();  // B2: every wave is done with buffer kt % NST
-    // refill buffer kt % NST with block kt + NST; its copies are spread over
-    // the MFMA sequence (one per two MFMAs) so that no wave waits behind a
-    // full load queue before its MFMAs.
-    const int kn = min(kt + NST, KT - 1);
-    const unsigned rbase = lds0 + (kt % NST) * STAGE;
+    __syncthreads();  // B2: every wave is done with buffer it % NST
+    // refill buffer it % NST with iteration it + NST; its copies are spread
+    // over the MFMA sequence (one per two MFMAs) so that no wave waits
+    // behind a full load queue before its MFMAs.
+    const int kn = min((it + NST) * KS + ks, KT - 1);
+    const unsigned rbase = lds0 + (it % NST) * STAGE + ks * SLOT;
+    const bool live = KS == 1 || kt < KT;
     // MFMA k is issued, then the FMAs fold the product of MFMA k-2, which
     // has retired by then; scheduling fences keep the compiler from pulling
     // a fold up behind its own MFMA (which would idle the matrix core)
@@ -324,14 +336,40 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
       }
       if (k >= 2) {
         const int p = k - 2;
+        const float f = live ? sc[p >> 2] : 0.f;  // a slice past the range adds zeros
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[p >> 2][p & 3][r] = fmaf(t[p][r], sc[p >> 2], acc[p >> 2][p & 3][r]);
+        for (int r = 0; r < 4; ++r) acc[p >> 2][p & 3][r] = fmaf(t[p][r], f, acc[p >> 2][p & 3][r]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
   }
 
   wait_vm<0>();  // the trailing re-copies have landed before the stages are reused or the workgroup ends
+  if constexpr (KS > 1) {
+    // slice sums into slice 0, in slice order, through the idle stage buffers
+    __syncthreads();  // every wave is done with the stage buffers
+    v4f* part = reinterpret_cast<v4f*>(smem);  // [KS-1][NW][16 tiles][64 lanes]
+    if (ks > 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) part[(((ks - 1) * NW + wave) * 16 + i * 4 + j) * 64 + lane] = acc[i][j];
+    }
+    __syncthreads();
+    if (ks == 0) {
+#pragma unroll
+      for (int s2 = 1; s2 < KS; ++s2)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const v4f x = part[(((s2 - 1) * NW + wave) * 16 + i * 4 + j) * 64 + lane];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[i][j][r] += x[r];
+          }
+    }
+    if (ws != nullptr && ks > 0) return;  // (the split-K store below has no barrier)
+  }
   if (ws != nullptr) {
     // split-K partial: fp32, no bias; lane holds rows 16i + r16, columns
     // 16j + 4g .. +3 of its wave's 64x64 tile
@@ -359,7 +397,8 @@ __global__ __launch_bounds__(BM * 2, 256 / BM) void fp8_gemm_tile(
   // ---- epilogue: bias, bf16 (RNE), then each wave's 64x64 tile goes
   // through LDS (the idle stage buffers) so that global stores are whole
   // 128-byte rows: 16-byte chunk c of row r sits at chunk slot c ^ (r & 7)
-  __syncthreads();  // every wave is done with the stage buffers
+  __syncthreads();  // every wave is done with the stage buffers (and with the slice sums)
+  if (KS > 1 && ks > 0) return;
   uint8_t* ot = smem + wave * 8192;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -1131,10 +1170,17 @@ int fp8_gemm_impl(const void* a, const float* a_s, const void* b, const float* b
   }
   // 128x128 tiles, two workgroups per CU.  (256x128 tiles with one
   // 8-wave workgroup per CU measured 10-15% slower on every benchmark shape.)
-  hipLaunchKernelGGL((fp8_gemm_tile<128, 2, 16>), dim3((unsigned)(tiles_m128 * tiles_n), (unsigned)(used > 1 ? used : 1)),
-                     dim3(256), 0, st, (const uint8_t*)a, a_s, (const uint8_t*)b, b_s, bias, bias_ld,
-                     (uint16_t*)c, (int)M, (int)N, (int)K, (int)tiles_m128, (int)tiles_n, ws, kps, (int64_t)K,
-                     (int)KT, Grouped{});
+  // A grid that leaves half the CUs idle gets two K slices per workgroup
+  // instead (each workgroup has its CU to itself either way).
+  const dim3 tgrid((unsigned)(tiles_m128 * tiles_n), (unsigned)(used > 1 ? used : 1));
+  if ((int64_t)tgrid.x * tgrid.y * 2 <= cu_count())
+    hipLaunchKernelGGL((fp8_gemm_tile<128, 2, 16, false, 2>), tgrid, dim3(512), 0, st, (const uint8_t*)a, a_s,
+                       (const uint8_t*)b, b_s, bias, bias_ld, (uint16_t*)c, (int)M, (int)N, (int)K, (int)tiles_m128,
+                       (int)tiles_n, ws, kps, (int64_t)K, (int)KT, Grouped{});
+  else
+    hipLaunchKernelGGL((fp8_gemm_tile<128, 2, 16>), tgrid, dim3(256), 0, st, (const uint8_t*)a, a_s,
+                       (const uint8_t*)b, b_s, bias, bias_ld, (uint16_t*)c, (int)M, (int)N, (int)K, (int)tiles_m128,
+                       (int)tiles_n, ws, kps, (int64_t)K, (int)KT, Grouped{});
   int rc = check_launch("fp8_gemm");
   if (rc != 0 || ws == nullptr || !reduce) return rc;
   if (N % 8 == 0 && ((uintptr_t)c & 15u) == 0 && M * (N / 8) < (1ll << 31) - 256) {
@@ -1195,10 +1241,17 @@ extern "C" int lfs_fp8_grouped_gemm(const void* a, const float* a_s, int64_t a_r
   const int64_t tiles_n = (N + BN - 1) / BN;
   LFS_REQUIRE(num_tiles * tiles_n < (1ll << 31), "fp8_grouped_gemm: too many tiles");
   const Grouped grp{tile_expert, row_index, b_expert_stride, bs_expert_stride, bias_expert_stride, (int)a_rows};
-  hipLaunchKernelGGL((fp8_gemm_tile<128, 2, 16, true>), dim3((unsigned)(num_tiles * tiles_n)), dim3(256), 0,
-                     (hipStream_t)stream, (const uint8_t*)a, a_s, (const uint8_t*)b, b_s, bias, (int64_t)0,
-                     (uint16_t*)c, (int)M, (int)N, (int)K, (int)num_tiles, (int)tiles_n, c_f32, (int)(K / 128),
-                     ldb, (int)ldbs, grp);
+  // the dense kernel's rule: two K slices per workgroup when the grid leaves
+  // half the CUs idle (so a tile's sums match fp8_gemm's on a grid as sparse)
+  const dim3 grid((unsigned)(num_tiles * tiles_n));
+  if ((int64_t)grid.x * 2 <= cu_count())
+    hipLaunchKernelGGL((fp8_gemm_tile<128, 2, 16, true, 2>), grid, dim3(512), 0, (hipStream_t)stream,
+                       (const uint8_t*)a, a_s, (const uint8_t*)b, b_s, bias, (int64_t)0, (uint16_t*)c, (int)M, (int)N,
+                       (int)K, (int)num_tiles, (int)tiles_n, c_f32, (int)(K / 128), ldb, (int)ldbs, grp);
+  else
+    hipLaunchKernelGGL((fp8_gemm_tile<128, 2, 16, true>), grid, dim3(256), 0, (hipStream_t)stream,
+                       (const uint8_t*)a, a_s, (const uint8_t*)b, b_s, bias, (int64_t)0, (uint16_t*)c, (int)M, (int)N,
+                       (int)K, (int)num_tiles, (int)tiles_n, c_f32, (int)(K / 128), ldb, (int)ldbs, grp);
   return check_launch("fp8_grouped_gemm");
 }
 
