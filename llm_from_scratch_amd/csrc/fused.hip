@@ -523,6 +523,11 @@ __global__ __launch_bounds__(256) void moe_route_token_kernel(
 // the gate on all four waves (as moe_route; with two waves it took 14.5 us
 // against 4.8 + 8.2 us for the separate launches).
 constexpr int kNormRouteMaxD = 8192;
+// Gate rows and down biases staged in LDS by the waves the norm leaves idle
+// (threads 128..255), when both fit: their loads then overlap the norm's
+// instead of following it (two dependent round trips fewer).
+constexpr int kRouteStageBytes = 48 * 1024;
+constexpr int kRouteStagePerThread = kRouteStageBytes / 16 / 128;  // 16-byte chunks per staging thread
 
 template <int CPT>
 __global__ __launch_bounds__(256) void add_rmsnorm_route_kernel(
@@ -533,13 +538,39 @@ __global__ __launch_bounds__(256) void add_rmsnorm_route_kernel(
     int top_k) {
   __shared__ float red[4];
   __shared__ __attribute__((aligned(16))) uint16_t h_lds[kNormRouteMaxD];
+  __shared__ __attribute__((aligned(16))) uint4 stage[kRouteStageBytes / 16];
   __shared__ float logits[kMaxExperts];
   __shared__ float wsel[kMaxExperts];
   __shared__ int sel[kMaxExperts];
   const int64_t t = blockIdx.x;
+  // gw: E x d bf16 (16-byte aligned, d % 8 == 0: checked on the host); b2:
+  // (E+S) x d fp32 when given and 16-byte aligned
+  const int gw16 = E * d / 8;
+  const bool b2_ok = b2 != nullptr && ((uintptr_t)b2 & 15u) == 0;
+  const int b216 = b2_ok ? (E + S) * d / 4 : 0;
+  const bool staged = gw16 + b216 <= kRouteStageBytes / 16;
+  if (staged && threadIdx.x >= 128) {
+    const uint4* gsrc = reinterpret_cast<const uint4*>(gw);
+    const uint4* bsrc = reinterpret_cast<const uint4*>(b2);
+    const int tot = gw16 + b216;
+    uint4 v[kRouteStagePerThread];
+#pragma unroll
+    for (int k = 0; k < kRouteStagePerThread; ++k) {
+      const int i = (int)threadIdx.x - 128 + 128 * k;
+      const uint4* src = i < gw16 ? gsrc + i : bsrc + (i - gw16);
+      v[k] = i < tot ? *src : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < kRouteStagePerThread; ++k) {
+      const int i = (int)threadIdx.x - 128 + 128 * k;
+      if (i < tot) stage[i] = v[k];
+    }
+  }
   add_rmsnorm_row<CPT, true, 4>(x, residual, w, out, res_out, q, qs, d, eps, t, red, h_lds);
-  __syncthreads();
-  route_token(h_lds, gw, ebias, b2, dense, bias_out, d, E, S, top_k, nullptr, nullptr, t, logits, wsel, sel);
+  __syncthreads();  // (also: the staged rows are visible)
+  const uint16_t* gws = staged ? reinterpret_cast<const uint16_t*>(stage) : gw;
+  const float* b2s = staged && b2_ok ? reinterpret_cast<const float*>(stage + gw16) : b2;
+  route_token(h_lds, gws, ebias, b2s, dense, bias_out, d, E, S, top_k, nullptr, nullptr, t, logits, wsel, sel);
 }
 
 // ------------------------------------------------------------ swiglu_quant --
