@@ -793,9 +793,19 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_big(
 //     instruction covers 16 rows x 64 contiguous bytes).  The stores are
 //     bounds-checked buffer stores (rows past M fall outside the buffer's
 //     M*N*2 bytes and are dropped by the hardware), so every wave issues
-//     exactly 16 of them per tile and the next tile's first wait keeps them
-//     in flight with vmcnt(16) (vector memory operations complete in issue
-//     order on gfx9, so that count still covers the older copies).
+//     exactly 16 of them per tile; they stay in flight over the next tile's
+//     first 28 MFMAs;
+//   * one barrier per K block, placed after its MFMA 28 instead of before
+//     its first MFMA: by then every wave has consumed its last operand
+//     fragment of block k (so block k's stage is free for the copies of
+//     block k + 2) and has waited for its copies of block k + 1, so the B
+//     fragments, first A fragment and scales of block k + 1 are read while
+//     MFMAs 29-31 of block k run.  (With the barrier at the block start,
+//     every SIMD's two waves waited out the same ~500-cycle LDS round trip
+//     with the MFMA pipe empty; a timeline of s_memtime stamps per wave
+//     showed it on every block.)  The scales of the block are read as two
+//     16-byte loads: the scale table is stored with a lane's eight rows
+//     (16 i + r16) adjacent.
 // Tile order: round r of the sequence is tiles r*nwg .. r*nwg + nwg - 1 of
 // the grouped order (GROUP_M_BIG row-tiles per group); workgroup w runs on
 // XCD w % 8 and takes position (w % 8) * (nwg / 8) + w / 8 of each round, so
@@ -809,6 +819,14 @@ typedef float f32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ unsigned cvt_pk_bf16(float lo, float hi) {
   // v_cvt_pk_bf16_f32: round to nearest even, as f32_to_bf16
   return __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
+}
+
+// x, with the compiler unable to see its value: per-lane addresses derived
+// from it are recomputed where they are used instead of being hoisted out of
+// the K loop and kept live (the K loop has no registers to spare)
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
 }
 
 template <bool HAS_BIAS>
@@ -848,30 +866,37 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_persist(
   const unsigned lsas = __builtin_amdgcn_readfirstlane(lds_addr(&sas[0][0][0]));
   const unsigned lsbs = __builtin_amdgcn_readfirstlane(lds_addr(&sbs[0][0][0]));
   // per-lane copy offsets of tile rows 8 (wave + 8u) + lane / 8 from the
-  // tile's first row (rows past `lim` clamped; their results are dropped)
-  auto offs = [&](int base, int lim, unsigned (&o)[4]) {
+  // tile's first row; rows past M are clamped to M - 1 (their results are
+  // dropped).  The swizzled chunk does not depend on u.
+  auto offs = [&](int lim, unsigned (&o)[4]) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int r = 8 * (wave + 8 * u) + (lane >> 3);
-      const int c = (lane & 7) ^ (((r >> 1) & 7) ^ ((r & 1) << 2));
-      o[u] = (unsigned)(min(base + r, lim - 1) - base) * (unsigned)K + c * 16;
+      const int r = 8 * wave + 64 * u + (lane >> 3);
+      const int c = (lane & 7) ^ ((((8 * wave + (lane >> 3)) >> 1) & 7) ^ ((lane >> 3) & 1) << 2);
+      o[u] = (unsigned)min(r, lim) * (unsigned)K + c * 16;
     }
   };
   unsigned offA[4], offB[4];
-  offs(m0, M, offA);
-  offs(n0, N, offB);
+  offs(M - 1 - m0, offA);
+  offs(255, offB);
   const uint8_t* tileA = A + (size_t)m0 * K;
   const uint8_t* tileB = B + (size_t)n0 * K;
-  // scale chunk for K blocks kb0 .. kb0 + SCKB - 1 of tile (mm0, nn0), as in fp8_gemm_big
+  // scale chunk for K blocks kb0 .. kb0 + SCKB - 1 of tile (mm0, nn0), as in
+  // fp8_gemm_big but with the rows permuted: table position p = 64 u + lane
+  // holds row (p / 128) * 128 + 16 (p % 8) + (p / 8) % 16, so lane l of a
+  // wave finds its rows 16 i + l % 16 (i = 0..7) at 8 (l % 16) .. + 7
   auto issue_scales = [&](int mm0, int nn0, int kb0, int buf) {
     const int kb = min(kb0 + wave, KT - 1);
+    const int ln = opaque(lane);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const float* src = As + (size_t)min(mm0 + 64 * u + lane, M - 1) * KT + kb;
+      const int p = 64 * u + ln;
+      const int r = (p >> 7) * 128 + 16 * (p & 7) + ((p >> 3) & 15);
+      const float* src = As + (size_t)min(mm0 + r, M - 1) * KT + kb;
       dma4(src, lsas + ((buf * SCKB + wave) * BIG + 64 * u) * 4);
     }
-    if (wave == 0 && lane < 16) {
-      const float* src = Bs + (size_t)min(nn0 / 128 + (lane & 1), nbs - 1) * KT + min(kb0 + (lane >> 1), KT - 1);
+    if (wave == 0 && ln < 16) {
+      const float* src = Bs + (size_t)min(nn0 / 128 + (ln & 1), nbs - 1) * KT + min(kb0 + (ln >> 1), KT - 1);
       dma4(src, lsbs + buf * SCKB * 2 * 4);
     }
   };
@@ -889,20 +914,31 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_persist(
 #pragma unroll
   for (int u = 0; u < 4; ++u) dma16s(tileB, offB[u], lds0 + A_BYTES + (wave + 8 * u) * 1024);
 
+  // block 0's operands
+  wait_vm<0>();
+  __syncthreads();
+  v8i fb[4], fa[8];
+  float4 s0, s1;
+  float bsv;
+  {
+    const float4* sa4 = reinterpret_cast<const float4*>(&sas[0][0][wm * 128 + 8 * r16]);
+    s0 = sa4[0];
+    s1 = sa4[1];
+    bsv = sbs[0][0][wn >> 1];
+    fb[0] = frag(smem, lb0, lb1);
+    fa[0] = frag(smem, la0, la1);
+#pragma unroll
+    for (int j = 1; j < 4; ++j) fb[j] = frag(smem + j * 2048, lb0, lb1);
+  }
+
   int gk = 0;     // K blocks done by this workgroup (stage parity)
   int cbase = 0;  // scale chunks done (scale buffer parity)
-  bool first = true;
   for (;;) {
     const int t_next = t + nwg;
     const bool has_next = t_next < ntiles;
     int m0n = m0, n0n = n0;
     if (has_next) tile_of(t_next, m0n, n0n);
     for (int kt = 0; kt < KT; ++kt, ++gk) {
-      // this wave's copies of block kt landed (the previous tile's 16 C
-      // stores, issued after them, may still be in flight)
-      if (first || kt > 0) wait_vm<0>();
-      else wait_vm<16>();
-      __syncthreads();  // everyone's copies landed; everyone is done with the other stage
       const bool last = kt + 1 == KT;
       const uint8_t* dA = tileA;
       const uint8_t* dB = tileB;
@@ -910,27 +946,28 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_persist(
       if (!last && (kt + 1) % SCKB == 0) issue_scales(m0, n0, kt + 1, (cbase + (kt + 1) / SCKB) & 1);
       if (last && has_next) {  // the next tile's first block and scale chunk
         issue_scales(m0n, n0n, 0, (cbase + nch) & 1);
-        offs(m0n, M, offA);
-        offs(n0n, N, offB);
+        offs(M - 1 - m0n, offA);
         dA = A + (size_t)m0n * K;
         dB = B + (size_t)n0n * K;
         kn = 0;
       }
       const unsigned nbase = lds0 + ((gk + 1) & 1) * STAGE;
       const uint8_t* st = smem + (gk & 1) * STAGE;
-      const int sbuf = (cbase + kt / SCKB) & 1, kc = kt % SCKB;
-      const float* sa = &sas[sbuf][kc][wm * 128 + r16];
-      const float bsv = sbs[sbuf][kc][wn >> 1];
-      v8i fb[4], fa[8];
+      const uint8_t* nst = smem + ((gk + 1) & 1) * STAGE;
+      // scale location of block kt + 1 (the next tile's first block after the last)
+      const int sbufn = last ? (cbase + nch) & 1 : (cbase + (kt + 1) / SCKB) & 1;
+      const int kcn = last ? 0 : (kt + 1) % SCKB;
       float sc[8];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) fb[j] = frag(st + j * 2048, lb0, lb1);
-      fa[0] = frag(st, la0, la1);
-      sc[0] = sa[0] * bsv;
+      float4 s0n, s1n;
+      float bsvn;
       v4f tp[32];
 #pragma unroll
       for (int k = 0; k < 34; ++k) {
         if (k < 32) tp[k] = mfma_fp8(fb[k & 3], fa[k >> 2]);
+        if (k == 0) {
+          sc[0] = s0.x * bsv; sc[1] = s0.y * bsv; sc[2] = s0.z * bsv; sc[3] = s0.w * bsv;
+          sc[4] = s1.x * bsv; sc[5] = s1.y * bsv; sc[6] = s1.z * bsv; sc[7] = s1.w * bsv;
+        }
         if ((k & 1) == 0 && k < 16) {
           const int u = (k >> 1) & 3;
           if (k < 8) dma16s(dA + (size_t)kn * BK, offA[u], nbase + (wave + 8 * u) * 1024);
@@ -939,8 +976,22 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_persist(
         if ((k & 3) == 0 && (k >> 2) + 1 < 8) {
           const int i1 = (k >> 2) + 1;
           fa[i1] = frag(st + i1 * 2048, la0, la1);
-          sc[i1] = sa[16 * i1] * bsv;
         }
+        if (k == 28) {
+          // MFMA 28 consumed this wave's last fragment of block kt: once every
+          // wave is here, block kt's stage is free and block kt + 1 (copied
+          // during this block) has landed, so its first operands are read
+          // while MFMAs 29-31 run
+          wait_vm<0>();
+          __syncthreads();
+          const float4* sa4 = reinterpret_cast<const float4*>(&sas[sbufn][kcn][wm * 128 + 8 * r16]);
+          s0n = sa4[0];
+          s1n = sa4[1];
+          bsvn = sbs[sbufn][kcn][wn >> 1];
+          fa[0] = frag(nst, la0, la1);
+          fb[0] = frag(nst, lb0, lb1);
+        }
+        if (k >= 29 && k < 32) fb[k - 28] = frag(nst + (k - 28) * 2048, lb0, lb1);
         if (k >= 2) {
           const int p = k - 2;
           if (kt == 0) {  // the tile's first K block starts the sums
@@ -953,6 +1004,9 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_persist(
         }
         __builtin_amdgcn_sched_barrier(0);
       }
+      s0 = s0n;
+      s1 = s1n;
+      bsv = bsvn;
     }
     // ---- epilogue: bias, bf16 pairs, permlane16 swap, 16 stores per wave
     float bv[4][4];
@@ -985,7 +1039,6 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_persist(
       }
     }
     if (!has_next) break;
-    first = false;
     t = t_next;
     m0 = m0n;
     n0 = n0n;
