@@ -129,6 +129,41 @@ def bench_gemm(cases, steps, warmup):
     return wall, per
 
 
+def bench_vendor_gemm(device, reps):
+    """Context for the headline, not a parity path: the vendor library's
+    FP8 GEMM (torch._scaled_mm -> hipBLASLt) on the same six shapes and the
+    same e4m3fn codes with one scale per tensor -- it has no per-128-block
+    scale fold, the block-scaled GEMM's main extra cost."""
+    from llm_from_scratch_amd import workloads as W
+    rows = []
+    tot_fl = tot_t = 0.0
+    one = torch.ones((), dtype=torch.float32, device=device)
+    for M in (4096, 16384):
+        for Kd, N in W.GEMM_KN:
+            a = torch.randn(M, Kd, device=device).to(torch.float8_e4m3fn)
+            b = torch.randn(N, Kd, device=device).to(torch.float8_e4m3fn)
+            f = lambda: torch._scaled_mm(a, b.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
+            f()
+            torch.cuda.synchronize()
+            ts = []
+            for _ in range(reps):
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+                f()
+                e1.record()
+                torch.cuda.synchronize()
+                ts.append(e0.elapsed_time(e1) / 1e3)
+            t = sorted(ts)[len(ts) // 2]
+            fl = 2.0 * M * N * Kd
+            rows.append({"M": M, "K": Kd, "N": N, "us": t * 1e6, "TFLOP/s": fl / t / 1e12})
+            tot_fl += fl
+            tot_t += t
+            del a, b
+    return {"library": "hipBLASLt via torch._scaled_mm, per-tensor scales (no block scales)",
+            "TFLOP/s": tot_fl / tot_t / 1e12, "frac": tot_fl / tot_t / 1e12 / FP8_PEAK_TFLOPS, "shapes": rows}
+
+
 def bench_act_quant(device, reps, flush_buf):
     """act_quant over every cfg2 activation shape (M in {1, 16, 128, 4096,
     16384} x K in {1024, 4096, 2048}), the 512 MB flush before every call
@@ -585,8 +620,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip decode / act_quant lines")
     ap.add_argument("--extras",
-                    default="cfg1,act_quant,gemm_small,store_kvcache,cfg3,cfg3_4k,cfg4,prefill,indexer,moe,cfg5",
-                    help="comma list of extra lines: cfg1 (FP8 linear latency), act_quant (every cfg2 "
+                    default="vendor,cfg1,act_quant,gemm_small,store_kvcache,cfg3,cfg3_4k,cfg4,prefill,indexer,moe,cfg5",
+                    help="comma list of extra lines: vendor (hipBLASLt per-tensor FP8 GEMM on the headline "
+                         "shapes, for context), cfg1 (FP8 linear latency), act_quant (every cfg2 "
                          "shape), gemm_small (cfg2 M <= 128), store_kvcache, cfg3, cfg3_4k, cfg4 (paged "
                          "decode), prefill (varlen prefill attention), indexer (DSA fp8_index), moe (MoE "
                          "layer, grouped vs dense dispatch), cfg5 (decode step)")
@@ -659,6 +695,12 @@ def main():
         flushed = decode or extras & {"act_quant", "gemm_small", "store_kvcache"}
         if flushed:
             flush_buf = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev).zero_()
+        if "vendor" in extras:
+            log("bench: vendor FP8 GEMM (per-tensor scales)")
+            try:
+                out["vendor_fp8_gemm"] = bench_vendor_gemm(dev, 20)
+            except Exception as e:  # noqa: BLE001 -- a missing vendor kernel is reported, not fatal
+                out["vendor_fp8_gemm"] = {"error": repr(e)[:300]}
         if "cfg1" in extras:
             log("bench: cfg1 FP8 linear latency")
             out["cfg1_linear"] = bench_cfg1(dev, 20)
