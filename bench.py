@@ -106,25 +106,33 @@ def gemm_setup(device):
 
 
 def bench_gemm(cases, steps, warmup):
-    """Warm up, then time exactly `steps` steps between two synchronizes;
-    inside that region every launch is bracketed by events on its stream."""
+    """Warm up, then time exactly `steps` steps between two synchronizes
+    (the whole-job wall time: the launches back to back, nothing between
+    them); then the same `steps` steps again with every launch bracketed by
+    HIP events on its stream (per-launch kernel time for the roofline --
+    an event record is a packet in the queue between two kernels, so that
+    pass is not the one the wall time is taken from)."""
     from llm_from_scratch_amd import kernels as K
     fns = [lambda c=c: K.fp8_gemm(c["a"], c["a_s"], c["b"], c["b_s"]) for c in cases]
     for _ in range(warmup):
         for f in fns:
             f()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for r in range(steps):
+        for f in fns:
+            f()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
     stream = torch.cuda.current_stream()
     evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             for _ in range(steps)] for _ in fns]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
     for r in range(steps):
         for i, f in enumerate(fns):
             evs[i][r][0].record(stream)
             f()
             evs[i][r][1].record(stream)
     torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) / steps
     per = [sum(a.elapsed_time(b) for a, b in e) / steps / 1e3 for e in evs]
     return wall, per
 
