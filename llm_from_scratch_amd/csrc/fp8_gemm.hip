@@ -9,9 +9,12 @@
 // (4 FMAs per tile per K block).  The scales are arbitrary fp32 values, so the
 // hardware's power-of-two (E8M0) operand scaling cannot carry them.
 //
-// Two kernels: fp8_gemm_tile, a 128 x 128 tile (64x64 per wave, two
-// workgroups per CU, optional split-K), and fp8_gemm_big, a 256 x 256 tile
-// (128x64 per wave, one workgroup per CU) for shapes that fill the chip.
+// Kernels: fp8_gemm_persist, 256 x 256 tiles (128x64 per wave, one 8-wave
+// workgroup per CU walking its tiles) for shapes with at least half a round
+// of such tiles; fp8_gemm_big, the same tile with one workgroup per tile,
+// for the other large shapes; fp8_gemm_tile, a 128 x 128 tile (64x64 per
+// wave, two workgroups per CU, optional split-K or two K slices per
+// workgroup; also the grouped MoE GEMM); fp8_gemm_skinny for M <= 128.
 // A and B K-tiles are copied global -> LDS by DMA (no register staging);
 // the activation scales follow in chunks of whole rows.
 //
