@@ -75,6 +75,35 @@ class DecodeModelConfig:
         d.update(kw)
         return d
 
+    def reference_state_keys(self) -> dict[str, tuple]:
+        """Float tensors of the reference's TransformerLM state dict for this
+        config, name -> shape (model/transformer.py:124-160 with GQA from
+        model/attention/GQA.py:34-40, MOE from model/architecture/moe.py:
+        153-194 in every layer, MLP from model/architecture/mlp.py:56-58)."""
+        c = self
+        d, F, kv = c.d_model, c.d_ff, c.num_kv_heads * c.head_dim
+        keys = {"token_embeddings.weight": (c.vocab_size, d), "final_norm.weight": (d,),
+                "lm_head.weight": (c.vocab_size, d), "lm_head.bias": (c.vocab_size,)}
+
+        def lin(name, n_out, n_in):
+            keys[name + ".weight"], keys[name + ".bias"] = (n_out, n_in), (n_out,)
+
+        for i in range(c.num_layers):
+            p = f"layers.{i}."
+            for name, n_out in (("q_proj", d), ("k_proj", kv), ("v_proj", kv), ("output_proj", d)):
+                lin(p + "att." + name, n_out, d)
+            keys[p + "att.q_norm.weight"], keys[p + "att.k_norm.weight"] = (d,), (kv,)
+            keys[p + "att_norm.weight"], keys[p + "ffn_norm.weight"] = (d,), (d,)
+            keys[p + "ffn.gate.weight"] = (c.n_routed_experts, d)
+            keys[p + "ffn.gate.expert_bias"] = (c.n_routed_experts,)
+            mlps = [f"ffn.experts.{e}" for e in range(c.n_routed_experts)]
+            mlps += ["ffn.shared_expert"] if c.n_shared_experts > 0 else []
+            for m in mlps:
+                lin(p + m + ".w1", F, d)
+                lin(p + m + ".w3", F, d)
+                lin(p + m + ".w2", d, F)
+        return keys
+
 
 class SplitKOutput(NamedTuple):
     """An FP8 linear's output left as its split-K partial sums (fp32 [n, T, d])
@@ -367,6 +396,50 @@ class DecodeModel(nn.Module):
                 b = 1.0 / math.sqrt(m.in_features)
                 m.load_weight(uniform((m.out_features, m.in_features), b),
                               uniform((m.out_features,), b) if m.bias is not None else None)
+
+    @torch.no_grad()
+    def load_reference_state_dict(self, sd) -> "DecodeModel":
+        """Load the weights of a reference TransformerLM (attention_type
+        "GQA", use_moe with MoE in every layer, at most one shared expert)
+        from its state dict: q/k/v projections stacked into qkv_proj, each
+        layer's experts and then its shared expert stacked into w13 / w2,
+        every projection quantised to e4m3 with 128x128 block scales, the
+        embedding and gate weights rounded to bf16.  Non-float buffers
+        (the gate's expert_load counts) are ignored; a missing, unexpected
+        or mis-shaped float tensor raises."""
+        want = self.cfg.reference_state_keys()
+        have = {k for k, v in sd.items() if torch.is_tensor(v) and v.is_floating_point()}
+        if have != set(want):
+            raise KeyError(f"reference state dict mismatch: missing {sorted(set(want) - have)}, "
+                           f"unexpected {sorted(have - set(want))}")
+        for k, shape in want.items():
+            if tuple(sd[k].shape) != shape:
+                raise ValueError(f"{k}: shape {tuple(sd[k].shape)}, expected {shape}")
+        dev = self.embed.device
+
+        def t(k):
+            return sd[k].to(device=dev, dtype=torch.float32)
+
+        self.embed.copy_(t("token_embeddings.weight"))
+        self.final_norm.weight.copy_(t("final_norm.weight"))
+        self.lm_head.load_weight(t("lm_head.weight"), t("lm_head.bias"))
+        for i, blk in enumerate(self.layers):
+            p = f"layers.{i}."
+            a = blk.att
+            a.qkv_proj.load_weight(torch.cat([t(p + f"att.{n}.weight") for n in ("q_proj", "k_proj", "v_proj")]),
+                                   torch.cat([t(p + f"att.{n}.bias") for n in ("q_proj", "k_proj", "v_proj")]))
+            a.output_proj.load_weight(t(p + "att.output_proj.weight"), t(p + "att.output_proj.bias"))
+            a.q_norm.weight.copy_(t(p + "att.q_norm.weight"))
+            a.k_norm.weight.copy_(t(p + "att.k_norm.weight"))
+            blk.att_norm.weight.copy_(t(p + "att_norm.weight"))
+            blk.ffn_norm.weight.copy_(t(p + "ffn_norm.weight"))
+            f = blk.ffn
+            f.gate_weight.copy_(t(p + "ffn.gate.weight"))
+            f.expert_bias.copy_(t(p + "ffn.gate.expert_bias"))
+            mlps = [f"ffn.experts.{e}" for e in range(f.n_experts)] + (["ffn.shared_expert"] if f.n_shared else [])
+            f.load_experts([tuple(t(p + m + s) for s in (".w1.weight", ".w1.bias", ".w3.weight", ".w3.bias",
+                                                         ".w2.weight", ".w2.bias")) for m in mlps])
+        return self
 
     def forward(self, input_ids: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
         x = self.embed[input_ids]

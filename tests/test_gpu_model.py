@@ -1,11 +1,15 @@
 """FP8Linear, the paged GQA + MoE decode model and the graph-captured decode
 step, on the GPU.
 
-Decode-step logits are compared with a full causal forward over the same
-tokens written here from the reference's layer math (model/transformer.py:
-162-183, model/attention/GQA.py:65-139, model/utils.py:44-67,
-model/architecture/moe.py:45-90, 288-341) in fp32, with the FP8 linears
-emulated as dequant(act_quant(x)) @ dequant(W)^T + b.
+The checker is oracle/model.py: the reference's decoder forward restated in
+torch (model/transformer.py:90-183, model/attention/GQA.py:65-139,
+model/utils.py:44-67, model/architecture/moe.py:45-90, 272-273, 289-341),
+itself pinned on the CPU to logits the reference's own TransformerLM wrote
+(tests/test_oracle_model.py, tests/golden/model_forward.npz).  Here it runs
+on the product's own weights -- each FP8 projection dequantised, the fused
+q/k/v and stacked expert matrices split back into the reference's state-dict
+layout -- with a linear that emulates the FP8 path:
+dequant(act_quant(x)) @ dequant(W)^T + b, rounded to bf16.
 
 Two tolerances:
   * each op of each layer (FP8 linears, norms, K/V writes, paged attention,
@@ -18,15 +22,17 @@ Two tolerances:
     computations drift apart layer by layer: a bf16 rounding difference in
     one linear's output flips the e4m3 code of some activations in the next
     (one e4m3 step is 2^-3 relative), so a 1e-3 difference entering a MoE
-    leaves it as ~1e-2.  Measured on MI355X: 3.5e-2 after 2 layers, 8.2e-2
-    after 12; every single op stays within 2e-3.
-Planted mistakes, checked on the CPU with the kernels emulated, each fail a
-per-op check by 7e-2 or more: interleaved instead of half-split RoPE, head
-map h % Hkv instead of h // G, a dropped linear bias, the newest token left
-out of attention, a dropped residual add, a softmax gate instead of sigmoid,
-top-k weights not renormalised.
+    leaves it as ~1e-2.  Measured on MI355X: 3.0-4.0e-2 after 2 layers,
+    3.8-7.9e-2 after 12; every single op stays within 4e-3.
+The reference's own logits (the golden fixture, fp32 weights) are also
+compared with the product loaded from the same state dict: that distance is
+the FP8 quantisation of weights and activations itself, bounded separately
+(measured 5.0e-2 after 2 layers).
 """
 import math
+import sys
+import weakref
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -38,10 +44,13 @@ from llm_from_scratch_amd.engine import BlockManager, LLMEngine, ModelRunner, Sa
 from llm_from_scratch_amd.fp8_linear import FP8Linear
 from llm_from_scratch_amd import workloads
 from oracle import fp8 as ofp8
+from oracle import model as om
+
+sys.path.insert(0, str(Path(__file__).with_name("golden")))
+from make_model_golden import GOLDEN_DIMS, GOLDEN_SEED  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
-FP32_EPS = torch.finfo(torch.float32).eps
 INV448 = torch.tensor(1.0 / 448.0, dtype=torch.float32)
 
 
@@ -72,53 +81,21 @@ def lin_w(w: torch.Tensor, bias, x: torch.Tensor) -> torch.Tensor:
     return y.to(torch.bfloat16)
 
 
-def rms(x, w, eps, residual=None):
-    xf = x.float() if residual is None else x.float() + residual.float()
-    out = (w * xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype)
-    return out, xf.to(x.dtype)
+def fp8_linear(wd: dict) -> om.Linear:
+    """The oracle's projection hook: lin_w on the dequantised weights."""
+    return lambda p, x: lin_w(wd[p + ".weight"], wd.get(p + ".bias"), x)
 
 
-def rope(x, pos, theta, D):
-    inv = 1.0 / (theta ** (torch.arange(0, D, 2, device=x.device).float() / D))
-    ang = pos.float()[:, None] * inv[None, :]
-    cos, sin = ang.cos()[:, None, :], ang.sin()[:, None, :]
-    x1, x2 = x.float().chunk(2, -1)
-    return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), -1)
-
-
-def gqa(q, k, v, mask=None):
-    """SDPA with query head h reading kv head h // G (model/attention/GQA.py:
-    118-130), fp32.  q [Tq, Hq, D], k/v [Tk, Hkv, D] -> [Tq, Hq*D]."""
-    Tq, Hq, D = q.shape
-    G = Hq // k.shape[1]
-    kh = k.float().repeat_interleave(G, 1).transpose(0, 1)
-    vh = v.float().repeat_interleave(G, 1).transpose(0, 1)
-    s = torch.matmul(q.float().transpose(0, 1), kh.transpose(1, 2).contiguous()) / math.sqrt(D)
-    if mask is not None:
-        s = s.masked_fill(~mask, float("-inf"))
-    return torch.matmul(torch.softmax(s, -1), vh).transpose(0, 1).reshape(Tq, Hq * D)
+def dims_of(cfg: DecodeModelConfig) -> om.ModelDims:
+    return om.ModelDims(cfg.vocab_size, cfg.d_model, cfg.num_layers, cfg.num_heads, cfg.num_kv_heads, cfg.d_ff,
+                        cfg.n_routed_experts, cfg.num_experts_per_tok, cfg.n_shared_experts, cfg.rope_theta,
+                        cfg.rms_eps)
 
 
 def split_qkv(y, cfg):
-    T, Hq, Hkv, D = y.shape[0], cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
-    q, k, v = y.split([Hq * D, Hkv * D, Hkv * D], dim=-1)
-    return q, k, v.reshape(T, Hkv, D)
-
-
-def norm_rope(a, q, k, pos, cfg):
-    T, Hq, Hkv, D = q.shape[0], cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
-    q = rms(q, a.q_norm.weight, FP32_EPS)[0].view(T, Hq, D)
-    k = rms(k, a.k_norm.weight, FP32_EPS)[0].view(T, Hkv, D)
-    return (rope(q, pos, cfg.rope_theta, D).to(torch.bfloat16),
-            rope(k, pos, cfg.rope_theta, D).to(torch.bfloat16))
-
-
-def ref_qkv(a, h, pos, cfg):
-    """q_proj/k_proj/v_proj (GQA.py:80-82) -- rows of the fused weight --
-    then q_norm over d_model, k_norm over Hkv*D, half-split RoPE."""
-    q, k, v = split_qkv(lin(a.qkv_proj, h), cfg)
-    q, k = norm_rope(a, q, k, pos, cfg)
-    return q, k, v
+    """Rows of the fused q/k/v projection's output -> q, k, v."""
+    Hq, Hkv, D = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
+    return y.split([Hq * D, Hkv * D, Hkv * D], dim=-1)
 
 
 def expert_weights(f, e):
@@ -132,66 +109,53 @@ def expert_weights(f, e):
             w2[:, e * F:(e + 1) * F], f.w2_bias[e])
 
 
-def ref_route(f, h):
-    logits = h.float() @ f.gate_weight.float().t()
-    scores = torch.sigmoid(logits)
-    idx = torch.topk(logits + f.expert_bias, f.top_k, -1).indices
-    w = torch.gather(scores, -1, idx)
-    return idx, w / (w.sum(-1, keepdim=True) + 1e-10)
+def moe_weights(f, p: str) -> dict:
+    """One MoE layer's dequantised weights under the reference's names."""
+    out = {p + "ffn.gate.weight": f.gate_weight.float(), p + "ffn.gate.expert_bias": f.expert_bias}
+    names = [f"ffn.experts.{e}" for e in range(f.n_experts)] + ["ffn.shared_expert"] * f.n_shared
+    for e, m in enumerate(names):
+        for key, t in zip((".w1.weight", ".w1.bias", ".w3.weight", ".w3.bias", ".w2.weight", ".w2.bias"),
+                          expert_weights(f, e)):
+            out[p + m + key] = t
+    return out
 
 
-def ref_combine(f, h, outs, d_model):
-    """sum of the chosen experts' outputs weighted by the renormalised gate
-    scores, plus the shared expert (moe.py:196-260, 288-341), in fp32."""
-    idx, w = ref_route(f, h)
-    y = outs[-1].float().clone()
-    for j in range(f.top_k):
-        for e in range(f.n_experts):
-            sel = idx[:, j] == e
-            y[sel] += w[sel, j:j + 1] * outs[e][sel].float()
-    return y.to(torch.bfloat16)
+_WEIGHTS = weakref.WeakKeyDictionary()
 
 
-def swiglu(a, b):
-    """silu(w1 x) * (w3 x) with the reference's bf16 roundings."""
-    return torch.nn.functional.silu(a.to(torch.bfloat16)) * b.to(torch.bfloat16)
+def product_weights(model: DecodeModel) -> dict:
+    """The model's weights in the reference's state-dict layout, every FP8
+    projection dequantised (computed once per model)."""
+    if model in _WEIGHTS:
+        return _WEIGHTS[model]
+    cfg = model.cfg
+    wd = {"token_embeddings.weight": model.embed, "final_norm.weight": model.final_norm.weight,
+          "lm_head.weight": w_deq(model.lm_head), "lm_head.bias": model.lm_head.bias}
+    for i, blk in enumerate(model.layers):
+        p, a = f"layers.{i}.", blk.att
+        for n, w, b in zip(("q_proj", "k_proj", "v_proj"), split_qkv(w_deq(a.qkv_proj).t(), cfg),
+                           split_qkv(a.qkv_proj.bias, cfg)):
+            wd[p + f"att.{n}.weight"], wd[p + f"att.{n}.bias"] = w.t(), b
+        wd[p + "att.output_proj.weight"] = w_deq(a.output_proj)
+        wd[p + "att.output_proj.bias"] = a.output_proj.bias
+        wd[p + "att.q_norm.weight"], wd[p + "att.k_norm.weight"] = a.q_norm.weight, a.k_norm.weight
+        wd[p + "att_norm.weight"], wd[p + "ffn_norm.weight"] = blk.att_norm.weight, blk.ffn_norm.weight
+        wd.update(moe_weights(blk.ffn, p))
+    _WEIGHTS[model] = wd
+    return wd
 
 
 def ref_moe(f, h, cfg):
-    outs = []
-    for e in range(f.n_experts + f.n_shared):
-        w1, b1, w3, b3, w2, b2 = expert_weights(f, e)
-        outs.append(lin_w(w2, b2, swiglu(lin_w(w1, b1, h), lin_w(w3, b3, h))))
-    return ref_combine(f, h, outs, cfg.d_model)
-
-
-def ref_block(blk, x, residual, pos, cfg, attend):
-    """One decoder block (model/transformer.py:90-118) with fused add & norm;
-    ``attend(q, k, v)`` supplies the attention over the right context."""
-    if residual is None:
-        h, residual = rms(x, blk.att_norm.weight, cfg.rms_eps)[0], x
-    else:
-        h, residual = rms(x, blk.att_norm.weight, cfg.rms_eps, residual)
-    q, k, v = ref_qkv(blk.att, h, pos, cfg)
-    x = lin(blk.att.output_proj, attend(q, k, v).to(torch.bfloat16))
-    h, residual = rms(x, blk.ffn_norm.weight, cfg.rms_eps, residual)
-    return ref_moe(blk.ffn, h, cfg), residual
+    """The oracle's MoE on the FP8-emulated weights of one layer."""
+    wd = moe_weights(f, "")
+    return om.moe(wd, "", h, dims_of(cfg), fp8_linear(wd))
 
 
 def ref_logits(model: DecodeModel, tokens: list[int]) -> torch.Tensor:
-    """Full causal forward over one sequence (model/transformer.py:162-183);
-    fp32 logits [T, vocab]."""
-    cfg = model.cfg
-    dev = model.embed.device
-    T = len(tokens)
-    pos = torch.arange(T, device=dev)
-    x = model.embed[torch.tensor(tokens, device=dev)]
-    causal = torch.tril(torch.ones(T, T, dtype=torch.bool, device=dev))
-    residual = None
-    for blk in model.layers:
-        x, residual = ref_block(blk, x, residual, pos, cfg, lambda q, k, v: gqa(q, k, v, causal))
-    h, _ = rms(x, model.final_norm.weight, cfg.rms_eps, residual)
-    return lin(model.lm_head, h).float()
+    """The oracle's causal forward over one sequence on the model's
+    FP8-emulated weights, bf16 activations; fp32 logits [T, vocab]."""
+    wd = product_weights(model)
+    return om.forward(wd, tokens, dims_of(model.cfg), fp8_linear(wd), embed_dtype=torch.bfloat16)
 
 
 def rel_err_rows(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
@@ -269,6 +233,7 @@ def check_layers_teacher_forced(model, runner, seqs):
     finally:
         model.trace = None
     cfg = model.cfg
+    dims = dims_of(cfg)
     worst: dict[str, float] = {}
 
     def chk(kind, got, want, what):
@@ -286,14 +251,14 @@ def check_layers_teacher_forced(model, runner, seqs):
     for layer, blk in enumerate(model.layers):
         t, p = tr[layer], f"layer {layer}"
         if t["residual"] is None:
-            h, r = rms(t["x"], blk.att_norm.weight, cfg.rms_eps)[0], t["x"]
+            h, r = om.rms_norm(t["x"], blk.att_norm.weight, cfg.rms_eps)[0], t["x"]
         else:
-            h, r = rms(t["x"], blk.att_norm.weight, cfg.rms_eps, t["residual"])
+            h, r = om.rms_norm(t["x"], blk.att_norm.weight, cfg.rms_eps, t["residual"])
         chk("norm", t["att_h"], h, f"{p} att_norm")
         a = blk.att
         chk("linear", t["qkv"], lin(a.qkv_proj, t["att_h"]), f"{p} qkv_proj")
-        q, k, v = split_qkv(t["qkv"], cfg)
-        q, k = norm_rope(a, q, k, pos, cfg)
+        q, k, v = om.qkv_heads(*split_qkv(t["qkv"], cfg), a.q_norm.weight, a.k_norm.weight, pos, dims,
+                               torch.bfloat16)
         chk("q_norm_rope", t["q"], q, p)
         for i, s in enumerate(seqs):
             L = len(s)
@@ -302,13 +267,13 @@ def check_layers_teacher_forced(model, runner, seqs):
             what = f"{p} seq {i} len {L}"
             chk("new_k", Kc[-1:], k[i:i + 1], what)
             chk("new_v", Vc[-1:], v[i:i + 1], what)
-            chk("attention", t["att_o"][i:i + 1], gqa(t["q"][i:i + 1], Kc, Vc), what)
+            chk("attention", t["att_o"][i:i + 1], om.gqa_attention(t["q"][i:i + 1], Kc, Vc), what)
         chk("linear", t["att_out"], lin(a.output_proj, t["att_o"]), f"{p} output_proj")
-        h2, r2 = rms(t["att_out"], blk.ffn_norm.weight, cfg.rms_eps, r)
+        h2, r2 = om.rms_norm(t["att_out"], blk.ffn_norm.weight, cfg.rms_eps, r)
         chk("norm", t["ffn_h"], h2, f"{p} ffn_norm")
         chk("norm", t["res_mid"], r2, f"{p} residual")
         f = blk.ffn
-        idx, w = ref_route(f, t["ffn_h"])
+        idx, w = om.route(t["ffn_h"], f.gate_weight, f.expert_bias, f.top_k)
         dense = torch.zeros(len(seqs), f.n_experts + f.n_shared, device=w.device)
         dense.scatter_(1, idx, w)
         dense[:, f.n_experts:] = 1.0
@@ -319,10 +284,13 @@ def check_layers_teacher_forced(model, runner, seqs):
         for e in range(f.n_experts + f.n_shared):
             _, _, _, _, w2, b2 = expert_weights(f, e)
             r0 = 2 * f.d_ff * e
-            outs.append(lin_w(w2, b2, swiglu(t["h13"][:, r0:r0 + f.d_ff], t["h13"][:, r0 + f.d_ff:r0 + 2 * f.d_ff])))
-        chk("moe_down_combine", t["ffn_out"], ref_combine(f, t["ffn_h"], outs, cfg.d_model), p)
+            h1, h3 = t["h13"][:, r0:r0 + f.d_ff], t["h13"][:, r0 + f.d_ff:r0 + 2 * f.d_ff]
+            outs.append(lin_w(w2, b2, om.swiglu(h1.to(torch.bfloat16), h3.to(torch.bfloat16))))
+        y = om.combine(idx, w, outs[:f.n_experts], outs[f.n_experts] if f.n_shared else None, torch.bfloat16)
+        chk("moe_down_combine", t["ffn_out"], y, p)
     fin = tr["final"]
-    chk("norm", fin["h"], rms(fin["x"], model.final_norm.weight, cfg.rms_eps, fin["residual"])[0], "final_norm")
+    chk("norm", fin["h"], om.rms_norm(fin["x"], model.final_norm.weight, cfg.rms_eps, fin["residual"])[0],
+        "final_norm")
     chk("linear", fin["logits"], lin(model.lm_head, fin["head_in"]), "lm_head")
     return worst
 
@@ -431,6 +399,61 @@ def test_decode_steps_match_full_forward_small(block_size):
             worst[k] = max(worst.get(k, 0.0), v)
     print(f"\nsmall model: e2e rel err max {max(errs):.4f} median {np.median(errs):.4f}; "
           f"per-stage max " + ", ".join(f"{k} {v:.2e}" for k, v in worst.items()))
+
+
+GOLDEN = Path(__file__).with_name("golden") / "model_forward.npz"
+FP8_VS_FP32_TOL = 8e-2  # reference fp32 logits vs the FP8 product, 2 layers
+
+
+@torch.inference_mode()
+def test_reference_state_dict_decode_matches_reference_logits(block_size):
+    """A reference TransformerLM state dict (GQA, MoE with a shared expert;
+    the golden fixture's weights) loaded with load_reference_state_dict and
+    served through the engine: a 13-token prefill, then 11 graph-replayed
+    decode steps fed the fixture's tokens (crossing the 16-token block
+    boundary), three sequences in one batch.  Every step's logits against
+      * the reference TransformerLM's own fp32 logits for that position:
+        relative L2 per row within FP8_VS_FP32_TOL -- the FP8 quantisation of
+        every weight and activation (the oracle's FP8 emulation alone stands
+        4.1-5.2e-2 off these logits);
+      * the oracle's FP8-emulated forward on the loaded (quantised) weights:
+        within e2e_tol(2), as in the other model tests."""
+    g = np.load(GOLDEN)
+    w = om.reference_weights(GOLDEN_DIMS, GOLDEN_SEED)
+    assert om.weights_digest(w) == str(g["weights_sha256"])
+    d = GOLDEN_DIMS
+    cfg = DecodeModelConfig(vocab_size=d.vocab_size, d_model=d.d_model, num_layers=d.num_layers,
+                            num_heads=d.num_heads, num_kv_heads=d.num_kv_heads, d_ff=d.d_ff,
+                            n_routed_experts=d.n_routed_experts, num_experts_per_tok=d.num_experts_per_tok,
+                            n_shared_experts=d.n_shared_experts, max_model_length=64)
+    sd = {k: torch.from_numpy(v) for k, v in w.items()}
+    sd["layers.0.ffn.gate.expert_load"] = torch.zeros(d.n_routed_experts, dtype=torch.long)  # ignored
+    model = DecodeModel(cfg, device="cuda", seed=0).load_reference_state_dict(sd)
+    assert torch.equal(model.embed.float().cpu(), sd["token_embeddings.weight"])
+    BS, P = 16, 13
+    Sequence.block_size = BS
+    runner = ModelRunner(model, cfg.runner_config(block_size=BS, num_kv_blocks=16, max_num_seqs=4))
+    bm = BlockManager(16, BS)
+    tokens, want = g["tokens"], torch.from_numpy(g["logits"]).cuda()
+    seqs = [Sequence(row[:P].tolist()) for row in tokens]
+    for s in seqs:
+        bm.allocate(s)
+    steps = [(P - 1, _prefill(runner, seqs))]
+    for t in range(P, tokens.shape[1]):
+        for s, row in zip(seqs, tokens):
+            s.append_token(int(row[t]))
+            assert bm.can_append(s)
+            bm.append(s)
+        steps.append((t, _decode(runner, seqs, eager=False)))
+    emul = [ref_logits(model, row.tolist()) for row in tokens]
+    e_ref, e_emul = [], []
+    for t, got in steps:
+        e_ref.append(rel_err_rows(got, want[:, t]).max().item())
+        e_emul.append(max(rel_err_rows(got[b], emul[b][t]).item() for b in range(len(seqs))))
+    print(f"\nreference state dict: vs the reference's fp32 logits max {max(e_ref):.4f} "
+          f"median {np.median(e_ref):.4f}; vs the FP8-emulated oracle max {max(e_emul):.4f}")
+    assert max(e_ref) <= FP8_VS_FP32_TOL, f"vs reference logits {['%.4f' % e for e in e_ref]}"
+    assert max(e_emul) <= e2e_tol(cfg.num_layers), f"vs FP8-emulated oracle {['%.4f' % e for e in e_emul]}"
 
 
 @torch.inference_mode()
