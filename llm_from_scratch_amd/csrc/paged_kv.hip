@@ -8,7 +8,7 @@
 //   context (decode_chunk) in tiles of up to 64 tokens that never cross a
 //   KV block (one block-table lookup per tile): S = K q^T on MFMA for the G
 //   query heads of its kv head, online softmax in the log2 domain, P through
-//   a wave-private LDS slice, P.V in fp32 registers.  Loads run two tiles
+//   a wave-private LDS slice, P.V in fp32 registers.  Loads run one tile
 //   ahead.  The partial (unnormalised o, m, l) of the range goes to the
 //   workspace, or, when the range is the whole context, the normalised bf16
 //   output is written directly.  The ranges come from either
@@ -58,12 +58,12 @@ __global__ __launch_bounds__(128) void store_kvcache_kernel(
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-// One wave per (sequence, kv head, chunk of the context).  Per tile of T
+// One wave per (sequence, kv head, range of the context).  Per tile of T
 // tokens (one KV block never straddled):
 //   K  : MFMA A operand straight from HBM -- lane l loads token (l % 16) of a
 //        16-token group, dims c*32 + (l / 16)*8 .. +7 (16 B);
 //   q^T: MFMA B operand, column j = l % 16 is query head kh*G + j (zero for
-//        j >= G), preloaded once;
+//        j >= G);
 //   S  = K q^T with v_mfma_f32_16x16x32_bf16: lane l ends with the scores of
 //        head (l % 16) for tokens 4*(l / 16) .. +3 of each group, so the
 //        online-softmax max/sum per head is a 2-step xor over lanes 16, 32;
@@ -71,12 +71,16 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 //   V  : lane l owns token (l / (D/8)) + (64/(D/8))*i and dims
 //        (l % (D/8))*8 .. +7 (coalesced 16-byte loads), fp32 FMAs into
 //        acc[G][8], rescaled by exp2(m_old - m_new) read from lane g.
-// Loads are software-pipelined two tiles ahead (two K and two V buffers,
-// each refilled as soon as its tile is consumed) with nontemporal 16-byte
-// loads, since every KV row is read exactly once.  There is no workgroup
-// barrier: waves exit independently.  A chunk that covers
-// the whole context writes the normalised bf16 output directly; otherwise
-// the unnormalised partial (o, m, l) goes to the workspace for the merge.
+// Loads are software-pipelined one tile ahead (two K and two V buffers: a
+// step issues the next tile's loads, then computes on the tile loaded by
+// the step before) with nontemporal 16-byte loads, since every KV row is
+// read exactly once.  One tile in flight per wave is 16 KiB, 16 MiB over
+// the chip: enough to keep HBM busy, and a new request does not queue
+// behind twice that (two tiles ahead measured 4 % slower on every decode
+// shape).  There is no workgroup barrier: waves exit independently.  A
+// range that covers the whole context writes the normalised bf16 output
+// directly; otherwise the unnormalised partial (o, m, l) goes to the
+// workspace for the merge.
 template <int D>
 struct DecodeGeom {
   static constexpr int LPR = D / 8;               // lanes per token row in the P.V mapping
@@ -122,6 +126,180 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// The per-wave pieces of a decode range.  A tile is (n, off): n valid rows
+// (0 for a skipped block or a look-ahead filler) starting at element offset
+// off of the cache.
+template <int D, int G>
+struct DecodeWave {
+  using Geo = DecodeGeom<D>;
+  static constexpr int GP = G <= 4 ? 4 : 8;  // padded heads per token in the P slice
+  typedef uint4 KBuf[Geo::NG][Geo::NDC];
+  typedef uint4 VBuf[Geo::UV];
+  typedef uint4 QBuf[Geo::NDC];
+
+  int lane, j, kq, ts, dc;
+  int64_t row;  // elements per token row of the cache (Hkv * D)
+  float acc[G][8];
+  float m_run, l_run;
+
+  __device__ __forceinline__ DecodeWave(int lane_, int Hkv) : lane(lane_) {
+    j = lane & 15;
+    kq = lane >> 4;
+    ts = lane / Geo::LPR;
+    dc = lane % Geo::LPR;
+    row = (int64_t)Hkv * D;
+    reset();
+  }
+  __device__ __forceinline__ void reset() {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+    m_run = -INFINITY;
+    l_run = 0.f;
+  }
+  // q^T columns of kv head kh of sequence b (lanes j >= G load nothing)
+  __device__ __forceinline__ void load_q(QBuf& qa, const uint16_t* __restrict__ q, int64_t b, int kh, int Hq) const {
+#pragma unroll
+    for (int c = 0; c < Geo::NDC; ++c) {
+      uint4 w = make_uint4(0, 0, 0, 0);
+      if (j < G) w = *reinterpret_cast<const uint4*>(q + ((int64_t)b * Hq + kh * G + j) * D + c * 32 + kq * 8);
+      qa[c] = w;
+    }
+  }
+  // Every load is issued unconditionally: rows past the valid count n read
+  // row n-1 (row 0 of block 0 for a skipped block), whose scores are masked
+  // and whose P is 0 (a skipped block's P.V is not run).  Offsets inside a
+  // tile are 32-bit from a wave-uniform base.
+  __device__ __forceinline__ void load_k(KBuf& ka, const uint16_t* __restrict__ kc, int n, int64_t off) const {
+    const uint16_t* kb = kc + off;
+    const int nn = max(n, 1);
+#pragma unroll
+    for (int g16 = 0; g16 < Geo::NG; ++g16) {
+      const int tr = min(g16 * 16 + j, nn - 1);
+#pragma unroll
+      for (int c = 0; c < Geo::NDC; ++c)
+        ka[g16][c] = nt_load16(kb + (uint32_t)(tr * (int)row + c * 32 + kq * 8));
+    }
+  }
+  __device__ __forceinline__ void load_v(VBuf& va, const uint16_t* __restrict__ vc, int n, int64_t off) const {
+    const uint16_t* vb = vc + off;
+    const int nn = max(n, 1);
+#pragma unroll
+    for (int i = 0; i < Geo::UV; ++i)
+      va[i] = nt_load16(vb + (uint32_t)(min(ts + Geo::TPI * i, nn - 1) * (int)row + dc * 8));
+  }
+
+  // One tile of n valid rows: scores (log2 domain), online-softmax update
+  // for head j, P through the LDS slice pw, P.V into acc.
+  __device__ __forceinline__ void tile(const KBuf& ka, const VBuf& va, const QBuf& qa, int n, float scale_log2,
+                                       float* __restrict__ pw) {
+    float s[Geo::NG][4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int g16 = 0; g16 < Geo::NG; ++g16) {
+      v4f sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < Geo::NDC; ++c)
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, ka[g16][c]),
+                                                     __builtin_bit_cast(v8bf, qa[c]), sc, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tok = g16 * 16 + kq * 4 + r;
+        s[g16][r] = tok < n ? sc[r] * scale_log2 : -INFINITY;
+        tmax = fmaxf(tmax, s[g16][r]);
+      }
+    }
+    tmax = max_xor16(tmax);
+    tmax = max_xor32(tmax);
+    const float m_new = fmaxf(m_run, tmax);
+    const bool live = m_new != -INFINITY;
+    const float alpha = live ? exp2f(m_run - m_new) : 1.f;
+    float psum = 0.f;
+#pragma unroll
+    for (int g16 = 0; g16 < Geo::NG; ++g16)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = live ? exp2f(s[g16][r] - m_new) : 0.f;
+        psum += p;
+        if (j < G) pw[(g16 * 16 + kq * 4 + r) * GP + j] = p;
+      }
+    psum = sum_xor16(psum);
+    psum = sum_xor32(psum);
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+    wave_lds_sync();
+
+    // P.V (rows past n have P = 0; a skipped block adds nothing)
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), g));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] *= a;
+    }
+    if (n > 0) {
+#pragma unroll
+      for (int iv = 0; iv < Geo::UV; ++iv) {
+        const int tok = ts + Geo::TPI * iv;
+        float pg[GP];
+#pragma unroll
+        for (int g4 = 0; g4 < GP; g4 += 4) {
+          const float4 p4 = *reinterpret_cast<const float4*>(&pw[tok * GP + g4]);
+          pg[g4] = p4.x; pg[g4 + 1] = p4.y; pg[g4 + 2] = p4.z; pg[g4 + 3] = p4.w;
+        }
+        float vf[8];
+        unpack8(va[iv], vf);
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pg[g], vf[e], acc[g][e]);
+      }
+    }
+    wave_lds_sync();
+  }
+
+  // End of a range: sum the token subgroups (lanes with the same dc), then
+  // the normalised bf16 output of query heads kh*G + g (whole context) or
+  // the unnormalised partial to workspace rows prow + g.
+  __device__ __forceinline__ void finish(bool whole, uint16_t* __restrict__ out, float* __restrict__ ws_o,
+                                         float* __restrict__ ws_ml, int64_t b, int kh, int Hq, int64_t prow) {
+#pragma unroll
+    for (int o = Geo::LPR; o < 64; o <<= 1)
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] += __shfl_xor(acc[g][e], o, 64);
+    if (whole) {
+      if (ts == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float lg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l_run), g));
+          const float inv = lg > 0.f ? 1.f / lg : 0.f;
+          uint4 o;
+          o.x = pack_bf16x2(acc[g][0] * inv, acc[g][1] * inv);
+          o.y = pack_bf16x2(acc[g][2] * inv, acc[g][3] * inv);
+          o.z = pack_bf16x2(acc[g][4] * inv, acc[g][5] * inv);
+          o.w = pack_bf16x2(acc[g][6] * inv, acc[g][7] * inv);
+          *reinterpret_cast<uint4*>(out + (b * Hq + kh * G + g) * D + dc * 8) = o;
+        }
+      }
+    } else {
+      if (ts == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          float* dst = ws_o + (prow + g) * D + dc * 8;
+          *reinterpret_cast<float4*>(dst) = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+          *reinterpret_cast<float4*>(dst + 4) = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
+        }
+      }
+      if (lane < G) {
+        ws_ml[(prow + lane) * 2 + 0] = m_run;
+        ws_ml[(prow + lane) * 2 + 1] = l_run;
+      }
+    }
+  }
+};
+
 // One wave: kv head kh of sequence b over context rows [t_begin, t_end)
 // (t_begin a multiple of `tile`, t_end <= Lc).  A range that is the whole
 // context (t_begin == 0, t_end >= Lc) writes the normalised bf16 output;
@@ -135,26 +313,11 @@ __device__ __forceinline__ void decode_chunk(
     float* __restrict__ ws_ml, uint16_t* __restrict__ out, int Hkv, int BS, int64_t NB, int tile,
     float scale_log2, int b, int kh, int64_t t_begin, int64_t t_end, int64_t Lc, int64_t prow,
     float* __restrict__ pw, int lane) {
-  using Geo = DecodeGeom<D>;
-  constexpr int GP = G <= 4 ? 4 : 8;  // padded heads per token in the P slice
+  using W = DecodeWave<D, G>;
+  W w(lane, Hkv);
   const int Hq = Hkv * G;
-  const int64_t row = (int64_t)Hkv * D;
-
-  const int j = lane & 15, kq = lane >> 4;
-  v8bf qb[Geo::NDC];
-#pragma unroll
-  for (int c = 0; c < Geo::NDC; ++c) {
-    uint4 w = make_uint4(0, 0, 0, 0);
-    if (j < G) w = *reinterpret_cast<const uint4*>(q + ((int64_t)b * Hq + kh * G + j) * D + c * 32 + kq * 8);
-    qb[c] = __builtin_bit_cast(v8bf, w);
-  }
-  const int ts = lane / Geo::LPR, dc = lane % Geo::LPR;
-  float acc[G][8];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
+  typename W::QBuf qa;
+  w.load_q(qa, q, b, kh, Hq);
 
   const int ntiles = (int)((t_end - t_begin + tile - 1) / tile);
   // The chunk's block ids, 256 at a time (window w0 .. w0 + 255 of the
@@ -165,9 +328,9 @@ __device__ __forceinline__ void decode_chunk(
   const int64_t blk_last = (t_end - 1) / BS;
   int64_t w0 = -1;
   uint4 ids = make_uint4(0, 0, 0, 0);
-  auto load_window = [&](int64_t w) {
-    w0 = w;
-    const int64_t e = w + 4 * lane;
+  auto load_window = [&](int64_t wb) {
+    w0 = wb;
+    const int64_t e = wb + 4 * lane;
     uint32_t v[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) v[c] = e + c <= blk_last ? (uint32_t)btrow[e + c] : 0u;
@@ -197,179 +360,49 @@ __device__ __forceinline__ void decode_chunk(
     const int32_t blk = block_id(t0 / BS);
     const bool ok = blk >= 0 && (int64_t)blk < NB;
     if (!ok) n = 0;  // invalid block: contributes nothing
-    off = ((int64_t)(ok ? blk : 0) * BS + (t0 % BS)) * row + (int64_t)kh * D;
-  };
-  // Every load is issued unconditionally: rows past the valid count n read
-  // row n-1 (row 0 of block 0 for a skipped block), whose scores are masked
-  // and whose P is 0 (a skipped block's P.V is not run).  Offsets inside a
-  // tile are 32-bit from a wave-uniform base.
-  auto load_k = [&](uint4 (&ka)[Geo::NG][Geo::NDC], int n, int64_t off) {
-    const uint16_t* kb = kc + off;
-    const int nn = max(n, 1);
-#pragma unroll
-    for (int g16 = 0; g16 < Geo::NG; ++g16) {
-      const int tr = min(g16 * 16 + j, nn - 1);
-#pragma unroll
-      for (int c = 0; c < Geo::NDC; ++c)
-        ka[g16][c] = nt_load16(kb + (uint32_t)(tr * (int)row + c * 32 + kq * 8));
-    }
-  };
-  auto load_v = [&](uint4 (&va)[Geo::UV], int n, int64_t off) {
-    const uint16_t* vb = vc + off;
-    const int nn = max(n, 1);
-#pragma unroll
-    for (int i = 0; i < Geo::UV; ++i)
-      va[i] = nt_load16(vb + (uint32_t)(min(ts + Geo::TPI * i, nn - 1) * (int)row + dc * 8));
+    off = ((int64_t)(ok ? blk : 0) * BS + (t0 % BS)) * w.row + (int64_t)kh * D;
   };
 
-  // Software pipeline two tiles deep, two K and two V buffers.  Issue order:
-  //   prologue K0 V0 K1 V1;  tile i: [QK_i] K_{i+2} [softmax, P.V_i] V_{i+2}
-  // Each buffer is refilled with tile i+2 as soon as tile i has consumed it,
-  // so up to two tiles of K and V are in flight while a tile is computed.
-  // The tiles of a chunk are processed in straight-line code (MAXT steps
+  // Pipeline one tile deep over two K and two V buffers: step i issues the
+  // loads of tile i+1 into the other buffers, then computes tile i.  The
+  // tiles of a chunk are processed in straight-line code (MAXT steps
   // unrolled, with early exits), every step issuing the same loads, so the
-  // compiler's in-order wait counts are exact: QK_i waits only for K_i and
-  // P.V_i only for V_i.  (In a loop, its conservative merge at the loop
-  // header drains every load in flight once per iteration.)  Chunks longer
-  // than MAXT tiles are walked MAXT tiles at a time.
+  // compiler's in-order wait counts are exact: tile i waits only for its own
+  // loads.  Chunks longer than MAXT tiles are walked MAXT tiles at a time.
   constexpr int MAXT = 8;
-  uint4 ka0[Geo::NG][Geo::NDC], ka1[Geo::NG][Geo::NDC];
-  uint4 va0[Geo::UV], va1[Geo::UV];
+  typename W::KBuf ka0, ka1;
+  typename W::VBuf va0, va1;
   int nb0 = 0, nb1 = 0;
-  auto step = [&](int i, uint4 (&ka)[Geo::NG][Geo::NDC], uint4 (&va)[Geo::UV], int& nb) {
-    const int n = nb;
-    int n2;
-    int64_t o2;
-    tile_at(i + 2, n2, o2);
-
-    // ---- scores (log2 domain) and online-softmax update for head j
-    float s[Geo::NG][4];
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int g16 = 0; g16 < Geo::NG; ++g16) {
-      v4f sc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int c = 0; c < Geo::NDC; ++c)
-        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, ka[g16][c]), qb[c], sc, 0, 0, 0);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int tok = g16 * 16 + kq * 4 + r;
-        s[g16][r] = tok < n ? sc[r] * scale_log2 : -INFINITY;
-        tmax = fmaxf(tmax, s[g16][r]);
-      }
-    }
+  auto step = [&](int i, typename W::KBuf& ka, typename W::VBuf& va, int nb, typename W::KBuf& kx,
+                  typename W::VBuf& vx, int& nbx) {
+    int n1;
+    int64_t o1;
+    tile_at(i + 1, n1, o1);
     __builtin_amdgcn_sched_barrier(0);  // keep the issue order the wait counts assume
-    load_k(ka, n2, o2);
+    w.load_k(kx, kc, n1, o1);
+    w.load_v(vx, vc, n1, o1);
     __builtin_amdgcn_sched_barrier(0);
-    tmax = max_xor16(tmax);
-    tmax = max_xor32(tmax);
-    const float m_new = fmaxf(m_run, tmax);
-    const bool live = m_new != -INFINITY;
-    const float alpha = live ? exp2f(m_run - m_new) : 1.f;
-    float psum = 0.f;
-#pragma unroll
-    for (int g16 = 0; g16 < Geo::NG; ++g16)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float p = live ? exp2f(s[g16][r] - m_new) : 0.f;
-        psum += p;
-        if (j < G) pw[(g16 * 16 + kq * 4 + r) * GP + j] = p;
-      }
-    psum = sum_xor16(psum);
-    psum = sum_xor32(psum);
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-    wave_lds_sync();
-
-    // ---- P.V (rows past n have P = 0; a skipped block adds nothing)
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), g));
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[g][e] *= a;
-    }
-    if (n > 0) {
-#pragma unroll
-      for (int iv = 0; iv < Geo::UV; ++iv) {
-        const int tok = ts + Geo::TPI * iv;
-        float pg[GP];
-#pragma unroll
-        for (int g4 = 0; g4 < GP; g4 += 4) {
-          const float4 p4 = *reinterpret_cast<const float4*>(&pw[tok * GP + g4]);
-          pg[g4] = p4.x; pg[g4 + 1] = p4.y; pg[g4 + 2] = p4.z; pg[g4 + 3] = p4.w;
-        }
-        float vf[8];
-        unpack8(va[iv], vf);
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pg[g], vf[e], acc[g][e]);
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    load_v(va, n2, o2);
-    __builtin_amdgcn_sched_barrier(0);
-    wave_lds_sync();
-    nb = n2;
+    nbx = n1;
+    w.tile(ka, va, qa, nb, scale_log2, pw);
   };
   for (int base = 0; base < ntiles; base += MAXT) {
     last = min(ntiles, base + MAXT);
     {
-      int64_t o0, o1;
+      int64_t o0;
       tile_at(base, nb0, o0);
-      tile_at(base + 1, nb1, o1);
-      load_k(ka0, nb0, o0);
-      load_v(va0, nb0, o0);
-      load_k(ka1, nb1, o1);
-      load_v(va1, nb1, o1);
+      w.load_k(ka0, kc, nb0, o0);
+      w.load_v(va0, vc, nb0, o0);
     }
 #pragma unroll
     for (int u = 0; u < MAXT; u += 2) {
       if (base + u >= last) break;
-      step(base + u, ka0, va0, nb0);
+      step(base + u, ka0, va0, nb0, ka1, va1, nb1);
       if (base + u + 1 >= last) break;
-      step(base + u + 1, ka1, va1, nb1);
+      step(base + u + 1, ka1, va1, nb1, ka0, va0, nb0);
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // drain the look-ahead loads
   }
-
-  // ---- reduce the token subgroups (lanes with the same dc)
-#pragma unroll
-  for (int o = Geo::LPR; o < 64; o <<= 1)
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[g][e] += __shfl_xor(acc[g][e], o, 64);
-
-  if (t_begin == 0 && t_end >= Lc) {
-    // the whole context is in this chunk: normalise and write bf16
-    if (ts == 0) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float lg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l_run), g));
-        const float inv = lg > 0.f ? 1.f / lg : 0.f;
-        uint4 o;
-        o.x = pack_bf16x2(acc[g][0] * inv, acc[g][1] * inv);
-        o.y = pack_bf16x2(acc[g][2] * inv, acc[g][3] * inv);
-        o.z = pack_bf16x2(acc[g][4] * inv, acc[g][5] * inv);
-        o.w = pack_bf16x2(acc[g][6] * inv, acc[g][7] * inv);
-        *reinterpret_cast<uint4*>(out + ((int64_t)b * Hq + kh * G + g) * D + dc * 8) = o;
-      }
-    }
-  } else {
-    if (ts == 0) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float* dst = ws_o + (prow + g) * D + dc * 8;
-        *reinterpret_cast<float4*>(dst) = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
-        *reinterpret_cast<float4*>(dst + 4) = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
-      }
-    }
-    if (lane < G) {
-      ws_ml[(prow + lane) * 2 + 0] = m_run;
-      ws_ml[(prow + lane) * 2 + 1] = l_run;
-    }
-  }
+  w.finish(t_begin == 0 && t_end >= Lc, out, ws_o, ws_ml, b, kh, Hq, prow);
 }
 
 // Fixed chunks: one wave per (sequence, kv head, chunk of bps blocks), four
