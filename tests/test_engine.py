@@ -237,3 +237,19 @@ def test_block_aligned_prompt_fully_matching_keeps_a_query_token():
     bm.deallocate(b)
     bm.deallocate(a)
     assert len(bm.free_block_ids) == 16
+
+
+def test_block_hash_is_chained_xxh64():
+    """Prefix-cache block hashes: xxh64 (the reference's engine/block_manager.py:45-57 calls
+    the same library) over the previous block's hash as 8 little-endian bytes, then the
+    block's token ids as int32.  The library is pinned by xxHash's published known answers
+    (empty input and "abc", seed 0); the chaining by hashes that must differ and agree."""
+    import xxhash
+    assert xxhash.xxh64(b"").intdigest() == 0xEF46DB3751D8E999
+    assert xxhash.xxh64(b"abc").intdigest() == 0x44BC2CF5AD770999
+    h0 = BlockManager.compute_hash([1, 2, 3])
+    assert h0 == xxhash.xxh64(b"\x01\x00\x00\x00\x02\x00\x00\x00\x03\x00\x00\x00").intdigest()
+    h1 = BlockManager.compute_hash([4, 5, 6], h0)
+    assert h1 == xxhash.xxh64(h0.to_bytes(8, "little") + bytes([4, 0, 0, 0, 5, 0, 0, 0, 6, 0, 0, 0])).intdigest()
+    assert h1 != BlockManager.compute_hash([4, 5, 6])  # the prefix changes the hash
+    assert BlockManager.compute_hash([-1]) == xxhash.xxh64(b"\xff\xff\xff\xff").intdigest()
