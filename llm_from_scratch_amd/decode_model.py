@@ -80,24 +80,23 @@ class DecodeModelConfig:
         config, name -> shape (model/transformer.py:124-160 with GQA from
         model/attention/GQA.py:34-40, MOE from model/architecture/moe.py:
         153-194 in every layer, MLP from model/architecture/mlp.py:56-58)."""
-        c = self
-        d, F, kv = c.d_model, c.d_ff, c.num_kv_heads * c.head_dim
-        keys = {"token_embeddings.weight": (c.vocab_size, d), "final_norm.weight": (d,),
-                "lm_head.weight": (c.vocab_size, d), "lm_head.bias": (c.vocab_size,)}
+        d, F, kv = self.d_model, self.d_ff, self.num_kv_heads * self.head_dim
+        keys = {"token_embeddings.weight": (self.vocab_size, d), "final_norm.weight": (d,),
+                "lm_head.weight": (self.vocab_size, d), "lm_head.bias": (self.vocab_size,)}
 
         def lin(name, n_out, n_in):
             keys[name + ".weight"], keys[name + ".bias"] = (n_out, n_in), (n_out,)
 
-        for i in range(c.num_layers):
+        for i in range(self.num_layers):
             p = f"layers.{i}."
             for name, n_out in (("q_proj", d), ("k_proj", kv), ("v_proj", kv), ("output_proj", d)):
                 lin(p + "att." + name, n_out, d)
             keys[p + "att.q_norm.weight"], keys[p + "att.k_norm.weight"] = (d,), (kv,)
             keys[p + "att_norm.weight"], keys[p + "ffn_norm.weight"] = (d,), (d,)
-            keys[p + "ffn.gate.weight"] = (c.n_routed_experts, d)
-            keys[p + "ffn.gate.expert_bias"] = (c.n_routed_experts,)
-            mlps = [f"ffn.experts.{e}" for e in range(c.n_routed_experts)]
-            mlps += ["ffn.shared_expert"] if c.n_shared_experts > 0 else []
+            keys[p + "ffn.gate.weight"] = (self.n_routed_experts, d)
+            keys[p + "ffn.gate.expert_bias"] = (self.n_routed_experts,)
+            mlps = [f"ffn.experts.{e}" for e in range(self.n_routed_experts)]
+            mlps += ["ffn.shared_expert"] if self.n_shared_experts > 0 else []
             for m in mlps:
                 lin(p + m + ".w1", F, d)
                 lin(p + m + ".w3", F, d)
