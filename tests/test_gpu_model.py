@@ -457,6 +457,35 @@ def test_reference_state_dict_decode_matches_reference_logits(block_size):
 
 
 @torch.inference_mode()
+def test_reference_state_dict_rejects_mismatches():
+    """A missing, an unexpected or a mis-shaped float tensor raises before any
+    weight is loaded; integer buffers (the gate's expert_load) are ignored."""
+    d = GOLDEN_DIMS
+    cfg = DecodeModelConfig(vocab_size=d.vocab_size, d_model=d.d_model, num_layers=d.num_layers,
+                            num_heads=d.num_heads, num_kv_heads=d.num_kv_heads, d_ff=d.d_ff,
+                            n_routed_experts=d.n_routed_experts, num_experts_per_tok=d.num_experts_per_tok,
+                            n_shared_experts=d.n_shared_experts, max_model_length=64)
+    model = DecodeModel(cfg, device="cuda", seed=0)
+    before = model.lm_head.weight.clone()
+    good = {k: torch.from_numpy(v) for k, v in om.reference_weights(d, GOLDEN_SEED).items()}
+    missing = dict(good)
+    del missing["layers.1.ffn.shared_expert.w2.bias"]
+    with pytest.raises(KeyError, match="shared_expert.w2.bias"):
+        model.load_reference_state_dict(missing)
+    extra = dict(good, **{"layers.0.att.head_gates_logits": torch.zeros(d.num_heads)})
+    with pytest.raises(KeyError, match="head_gates_logits"):
+        model.load_reference_state_dict(extra)
+    bad = dict(good)
+    bad["layers.0.att.k_proj.weight"] = torch.zeros(d.d_model, d.d_model)
+    with pytest.raises(ValueError, match="k_proj.weight"):
+        model.load_reference_state_dict(bad)
+    assert torch.equal(model.lm_head.weight, before), "a rejected state dict changed the weights"
+    ok = dict(good, **{"layers.0.ffn.gate.expert_load": torch.zeros(d.n_routed_experts, dtype=torch.long)})
+    model.load_reference_state_dict(ok)
+    assert not torch.equal(model.lm_head.weight, before)
+
+
+@torch.inference_mode()
 def test_decode_step_cfg5_shapes(block_size):
     """The config-5 model (12 layers, d=768, GQA 12/4, 8 experts top-2 + 1
     shared, vocab 32000) on 16 sequences with contexts in [256, 2048]."""
