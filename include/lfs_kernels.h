@@ -221,8 +221,8 @@ int lfs_store_kvcache(const void* key, int64_t k_stride_t, const void* value, in
  * Optionally (q_out and q_scale both non-NULL) also the act_quant of each
  * output row, the output projection's FP8 input: q_out e4m3fn [B, Hq*D],
  * q_scale fp32 [B, Hq*D/128], bit-identical to lfs_act_quant(out, 128)
- * (needs Hq*D % 128 == 0, Hq*D <= 8192); the merge then runs one workgroup
- * per sequence instead of one per (head, sequence).
+ * (needs Hq*D % 128 == 0); the merge then runs one workgroup per
+ * (128-value group, sequence) instead of one per (head, sequence).
  * D in {64, 128}; Hq % Hkv == 0, Hq/Hkv <= 8; block_size a multiple of 16.
  */
 int64_t lfs_paged_decode_workspace_bytes(int64_t B, int32_t num_q_heads, int32_t head_dim,

@@ -18,9 +18,10 @@
 //   blocks_per_split blocks)).
 // phase 2 (paged_decode_merge, one workgroup per (head, sequence)):
 //   log-sum-exp merge of the chunks, normalise, bf16.  Padding rows
-//   (context_len 0) get zeros.  paged_decode_merge_quant (one workgroup per
-//   sequence) does the same and also writes the act_quant codes and scales
-//   of the bf16 output row (the output projection's FP8 input).
+//   (context_len 0) get zeros.  paged_decode_merge_quant_group (one
+//   workgroup per 128-value group of an output row) does the same and also
+//   writes the group's act_quant codes and scale (the output projection's
+//   FP8 input).
 #include "common.h"
 
 #include <mutex>
@@ -572,22 +573,15 @@ __device__ __forceinline__ int part_span(const PartMap& pm, int b, int h, int Hq
   return (int)(wl - wf + 1);
 }
 
-// One workgroup per (head, sequence), one lane per head dim.  Up to MERGE_NS
-// partials are loaded together (one memory round trip), more in a loop.
+// Log-sum-exp merge of one output element: partials s = 0 .. ns-1 of a
+// (sequence, head) at workspace rows r0 + s*rs, element d.  Up to MERGE_NS
+// partials are loaded together (one memory round trip), more in a loop with
+// the same arithmetic in the same order.  ns == 0 (no context) gives 0.
 constexpr int MERGE_NS = 16;
-__global__ __launch_bounds__(128) void paged_decode_merge(
-    const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
-    const int64_t* __restrict__ ctx_lens, uint16_t* __restrict__ out, int Hq, int D, int BS,
-    int max_blocks, PartMap pm) {
-  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-  const int64_t Lc = min(ctx_lens[b], (int64_t)max_blocks * BS);
-  int64_t r0, rs;
-  const int ns = part_span(pm, b, h, Hq, Lc, BS, r0, rs);
-  if (ns == 1 || d >= D) return;
+__device__ __forceinline__ float merge_element(const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
+                                               int64_t r0, int64_t rs, int ns, int D, int d) {
   float res = 0.f;
   if (ns > 1 && ns <= MERGE_NS) {
-    // every partial's (m, l, o) loaded in one round trip, then the same
-    // arithmetic in the same order as the loop below (bit-identical)
     float mv[MERGE_NS], lv[MERGE_NS], ov[MERGE_NS];
 #pragma unroll
     for (int s = 0; s < MERGE_NS; ++s) {
@@ -625,163 +619,61 @@ __global__ __launch_bounds__(128) void paged_decode_merge(
     }
     res = den > 0.f ? num / den : 0.f;
   }
-  out[((int64_t)b * Hq + h) * D + d] = (uint16_t)f32_to_bf16(res);
+  return res;
 }
 
-// Phase 2 fused with the output projection's act_quant: one workgroup per
-// sequence merges every head (or re-reads the rows the split kernel wrote
-// for a head whose context one chunk covered; zeros for context 0), writes
-// the bf16 output, and quantises the row per 128-value group with
-// act_quant's formula and rounding (the codes equal act_quant of the bf16
-// output bit for bit).
-constexpr int MQ_MAXE = 8192;  // Hq * D per sequence
-constexpr int MQ_MAXH = 128;
-constexpr int MQ_MAXW = 4096;  // (split, head) weights staged in LDS
-// rows of at most MQ_PF_EPT * 256 values whose heads have at most MQ_PF_NS
-// partials: each thread's partial outputs are loaded in the same round trip
-// as the staged (m, l) values, not after the two barriers that follow
-constexpr int MQ_PF_NS = 6, MQ_PF_EPT = 4;
+// One workgroup per (head, sequence), one lane per head dim.
+__global__ __launch_bounds__(128) void paged_decode_merge(
+    const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
+    const int64_t* __restrict__ ctx_lens, uint16_t* __restrict__ out, int Hq, int D, int BS,
+    int max_blocks, PartMap pm) {
+  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  const int64_t Lc = min(ctx_lens[b], (int64_t)max_blocks * BS);
+  int64_t r0, rs;
+  const int ns = part_span(pm, b, h, Hq, Lc, BS, r0, rs);
+  if (ns == 1 || d >= D) return;
+  out[((int64_t)b * Hq + h) * D + d] = (uint16_t)f32_to_bf16(merge_element(ws_o, ws_ml, r0, rs, ns, D, d));
+}
 
-__global__ __launch_bounds__(256) void paged_decode_merge_quant(
+// The merge fused with the act_quant of its output row (the output
+// projection's FP8 input): one 128-thread workgroup per (128-value act_quant
+// group, sequence), every group independent.  Each thread merges one element
+// of the group (the arithmetic of paged_decode_merge; ns == 1: the split
+// kernel wrote the value), then 16 lanes quantise the group's 128 bf16
+// values 8 each, as act_quant does: codes and scale bit-identical to
+// act_quant(out row, 128).  Needs Hq * D % 128 == 0.
+__global__ __launch_bounds__(128) void paged_decode_merge_quant_group(
     const float* __restrict__ ws_o, const float* __restrict__ ws_ml, const int64_t* __restrict__ ctx_lens,
     uint16_t* __restrict__ out, uint8_t* __restrict__ qo, float* __restrict__ qs, int Hq, int D, int BS,
     int max_blocks, PartMap pm) {
-  __shared__ float hDen[MQ_MAXH];
-  __shared__ int hNs[MQ_MAXH];
-  __shared__ int64_t hR0[MQ_MAXH];
-  __shared__ int s_nsmax;
-  __shared__ float wts[MQ_MAXW];  // [split][head]: m, then exp2(m - M_head)
-  __shared__ __attribute__((aligned(16))) uint16_t vals[MQ_MAXE];
-  const int b = blockIdx.x, tid = threadIdx.x;
-  const int64_t Lc = min(ctx_lens[b], (int64_t)max_blocks * BS);
+  __shared__ __attribute__((aligned(16))) uint16_t vals[128];
+  const int g = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
   const int E = Hq * D;
+  const int e = g * 128 + t;
+  const int h = e / D, d = e - h * D;
+  const int64_t Lc = min(ctx_lens[b], (int64_t)max_blocks * BS);
+  int64_t r0, rs;
+  const int ns = part_span(pm, b, h, Hq, Lc, BS, r0, rs);
   uint16_t* orow = out + (int64_t)b * E;
-  if (tid == 0) s_nsmax = 0;
-  __syncthreads();
-  int64_t rs = 0;
-  for (int h = tid; h < Hq; h += 256) {
-    int64_t r0;
-    const int ns = part_span(pm, b, h, Hq, Lc, BS, r0, rs);
-    hNs[h] = ns;
-    hR0[h] = r0;
-    atomicMax(&s_nsmax, ns);
-  }
-  rs = pm.bps > 0 ? (int64_t)Hq : (int64_t)pm.wpg * pm.G;
-  __syncthreads();
-  const int nsmax = s_nsmax;
-  if (nsmax > 1) {
-    // (m, l) of every (split, head) in one parallel step; the per-head max,
-    // weights and denominators from LDS (the unfused merge's arithmetic)
-    const bool staged = nsmax * Hq <= MQ_MAXW;
-    const bool pf = staged && nsmax <= MQ_PF_NS && E <= 256 * MQ_PF_EPT;
-    float ov[MQ_PF_EPT][MQ_PF_NS];  // thread's elements tid + 256k: partial outputs, or the row value
-    if (pf) {
-#pragma unroll
-      for (int k = 0; k < MQ_PF_EPT; ++k) {
-        const int e = tid + 256 * k;
-        const int h = e < E ? e / D : 0, d = e - h * D;
-        const int ns = e < E ? hNs[h] : 0;
-        const int64_t r0 = hR0[h];
-#pragma unroll
-        for (int sp = 0; sp < MQ_PF_NS; ++sp)
-          ov[k][sp] = sp < ns && ns > 1 ? ws_o[(r0 + sp * rs) * D + d] : 0.f;
-        if (ns == 1) ov[k][0] = bf16_to_f32(orow[e]);  // written by the split kernel
-      }
-    }
-    if (staged) {
-      for (int x = tid; x < nsmax * Hq; x += 256) {
-        const int sp = x / Hq, h = x - sp * Hq;
-        wts[x] = sp < hNs[h] ? ws_ml[(hR0[h] + sp * rs) * 2] : -INFINITY;
-      }
-      __syncthreads();
-    }
-    auto mval = [&](int sp, int h) -> float { return staged ? wts[sp * Hq + h] : ws_ml[(hR0[h] + sp * rs) * 2]; };
-    for (int h = tid; h < Hq; h += 256) {
-      const int ns = hNs[h];
-      if (ns <= 1) continue;
-      float M = -INFINITY;
-      for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, mval(sp, h));
-      float den = 0.f;
-      if (M != -INFINITY)
-        for (int sp = 0; sp < ns; ++sp) {
-          const float w = exp2f(mval(sp, h) - M);
-          den = fmaf(w, ws_ml[(hR0[h] + sp * rs) * 2 + 1], den);
-          if (staged) wts[sp * Hq + h] = w;  // this thread alone reads / writes head h's entries
-        }
-      else if (staged)
-        for (int sp = 0; sp < ns; ++sp) wts[sp * Hq + h] = 0.f;
-      hDen[h] = M != -INFINITY ? den : 0.f;
-    }
-    __syncthreads();
-    if (pf) {
-#pragma unroll
-      for (int k = 0; k < MQ_PF_EPT; ++k) {
-        const int e = tid + 256 * k;
-        if (e >= E) break;
-        const int h = e / D;
-        const int ns = hNs[h];
-        if (ns == 1) {  // written by the split kernel (a bf16 value: exact in fp32)
-          vals[e] = (uint16_t)f32_to_bf16(ov[k][0]);
-          continue;
-        }
-        float num = 0.f, den = 0.f;
-        if (ns > 1) {
-          den = hDen[h];
-#pragma unroll
-          for (int sp = 0; sp < MQ_PF_NS; ++sp)
-            if (sp < ns) num = fmaf(wts[sp * Hq + h], ov[k][sp], num);
-        }
-        const uint16_t v = (uint16_t)f32_to_bf16(den > 0.f ? num / den : 0.f);
-        orow[e] = v;
-        vals[e] = v;
-      }
-    }
-    for (int e = pf ? E : tid; e < E; e += 256) {
-      const int h = e / D, d = e - h * D;
-      const int ns = hNs[h];
-      if (ns == 1) {  // written by the split kernel
-        vals[e] = orow[e];
-        continue;
-      }
-      float num = 0.f, den = 0.f;
-      if (ns > 1) {
-        den = hDen[h];
-        const int64_t r0 = hR0[h];
-        if (staged) {
-          for (int sp = 0; sp < ns; ++sp) num = fmaf(wts[sp * Hq + h], ws_o[(r0 + sp * rs) * D + d], num);
-        } else {
-          float M = -INFINITY;
-          for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, mval(sp, h));
-          if (M != -INFINITY)
-            for (int sp = 0; sp < ns; ++sp)
-              num = fmaf(exp2f(mval(sp, h) - M), ws_o[(r0 + sp * rs) * D + d], num);
-        }
-      }
-      const uint16_t v = (uint16_t)f32_to_bf16(den > 0.f ? num / den : 0.f);
-      orow[e] = v;
-      vals[e] = v;
-    }
-  } else if (nsmax == 1) {
-    for (int e = tid; e < E; e += 256) vals[e] = orow[e];  // written by the split kernel
+  uint16_t v;
+  if (ns == 1) {
+    v = orow[e];  // written by the split kernel
   } else {
-    for (int e = tid; e < E; e += 256) {
-      orow[e] = 0;
-      vals[e] = 0;
-    }
+    v = (uint16_t)f32_to_bf16(merge_element(ws_o, ws_ml, r0, rs, ns, D, d));
+    orow[e] = v;
   }
+  vals[t] = v;
   __syncthreads();
-  // act_quant of the row: 16 lanes per 128-value group, 8 values per lane
-  // (E / 8 is a multiple of 16, so a group's lanes are all in or all out)
-  for (int c8 = tid; c8 < E / 8; c8 += 256) {
+  if (t < 16) {
     float f[8];
-    unpack8(*reinterpret_cast<const uint4*>(&vals[c8 * 8]), f);
+    unpack8(*reinterpret_cast<const uint4*>(&vals[t * 8]), f);
     float amax = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[i]));
     amax = group_max<16>(amax);
     const float sc = scale_from_amax(amax, false);
-    *reinterpret_cast<uint2*>(qo + (int64_t)b * E + c8 * 8) = quant8(f, sc);
-    if ((c8 & 15) == 0) qs[(int64_t)b * (E / 128) + c8 / 16] = sc;
+    *reinterpret_cast<uint2*>(qo + (int64_t)b * E + g * 128 + t * 8) = quant8(f, sc);
+    if (t == 0) qs[(int64_t)b * (E / 128) + g] = sc;
   }
 }
 
@@ -941,8 +833,7 @@ int paged_decode_impl(const void* q, const void* k_cache, const void* v_cache, c
               "paged_decode: q, caches and out must be 16-byte aligned");
   LFS_REQUIRE(B < 65536, "paged_decode: batch too large");
   LFS_REQUIRE((q_out == nullptr) == (q_scale == nullptr), "paged_decode: q_out and q_scale go together");
-  LFS_REQUIRE(q_out == nullptr || (Hq * D % 128 == 0 && Hq * D <= MQ_MAXE && Hq <= MQ_MAXH),
-              "paged_decode: the quantised output needs Hq*D %% 128 == 0, Hq*D <= %d", MQ_MAXE);
+  LFS_REQUIRE(q_out == nullptr || Hq * D % 128 == 0, "paged_decode: the quantised output needs Hq*D %% 128 == 0");
   const int64_t need = lfs_paged_decode_workspace_bytes(B, Hq, D, max_blocks, blocks_per_split);
   LFS_REQUIRE(!noalloc || need <= workspace_bytes,
               "paged_decode_noalloc: this shape needs %lld bytes of workspace, more than the library's "
@@ -1077,8 +968,8 @@ int paged_decode_merge_launch(float* ws_o, float* ws_ml, const int64_t* context_
                               float* q_scale, int64_t B, int Hq, int D, int BS, int max_blocks, const PartMap& pm,
                               hipStream_t st) {
   if (q_out != nullptr) {
-    hipLaunchKernelGGL(paged_decode_merge_quant, dim3((unsigned)B), dim3(256), 0, st, ws_o, ws_ml, context_lens,
-                       (uint16_t*)out, (uint8_t*)q_out, q_scale, Hq, D, BS, max_blocks, pm);
+    hipLaunchKernelGGL(paged_decode_merge_quant_group, dim3((unsigned)(Hq * D / 128), (unsigned)B), dim3(128), 0, st,
+                       ws_o, ws_ml, context_lens, (uint16_t*)out, (uint8_t*)q_out, q_scale, Hq, D, BS, max_blocks, pm);
     return check_launch("paged_decode(merge + quant)");
   }
   hipLaunchKernelGGL(paged_decode_merge, dim3((unsigned)Hq, (unsigned)B), dim3((unsigned)D), 0, st,
