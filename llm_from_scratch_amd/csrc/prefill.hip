@@ -9,8 +9,8 @@
 // block_table[i][t / BS] * BS + t % BS of the KV pool (paged mode, a
 // prefix-cache hit: the cached blocks and the just-stored new tokens).
 //
-// One workgroup per (sequence, tile of 16 or 32 query tokens, kv head), one wave
-// per query head of the kv head's group (G waves).  Per tile of 32 keys:
+// One workgroup per (sequence, tile of 16, 32 or 64 query tokens, kv head), one
+// wave per (query head of the kv head's group, 16-query sub-tile).  Per tile of 32 keys:
 //   S^T = K Q^T   v_mfma_f32_16x16x32_bf16, K as the A operand loaded from
 //                 HBM in operand layout (lane l: key l % 16, dims
 //                 32c + 8(l / 16) .. +7), Q^T as the B operand (preloaded);
@@ -343,10 +343,13 @@ extern "C" int lfs_prefill_attention(const void* q, const void* k, const void* v
     LFS_REQUIRE(block_size > 0 && block_size % 16 == 0 && num_slots >= block_size && bt_stride > 0,
                 "prefill_attention: bad paged KV geometry (block_size must be a multiple of 16)");
   }
-  // Two 16-query sub-tiles per workgroup (each K / V tile feeds twice the
-  // queries) when that grid still fills every CU several times over;
-  // otherwise one, for finer load balance (measured: 16 x 2048-token
-  // prompts 301 vs 322 us, 16 x 512 queries over 2048 paged keys 220 vs 194 us).
+  // Four (G <= 4) or two 16-query sub-tiles per workgroup (each K / V tile
+  // feeds four or two times the queries) when that grid still fills every
+  // CU several times over; otherwise one, for finer load balance.  Measured
+  // on 16 x 2048-token prompts: four 254 us against two 266 us (10 launches
+  // back to back); two 301 us against one 322 us (one launch).  16 x 512
+  // queries over 2048 paged keys: two 220 us, one 194 us (one launch).
+  // Results are bit-identical: a sub-tile's extra key tiles are all masked.
   const int G = Hq / Hkv;
   const int64_t qtiles2 = ((int64_t)max_seqlen_q + 2 * QT - 1) / (2 * QT);
   static int cu_cache[64] = {0};  // compute units per device, read once
@@ -359,7 +362,8 @@ extern "C" int lfs_prefill_attention(const void* q, const void* k, const void* v
     }
     cus = cu_cache[dev];
   }
-  const int QWs = B * qtiles2 * Hkv >= 8ll * cus ? 2 : 1;
+  const int64_t qtiles4 = ((int64_t)max_seqlen_q + 4 * QT - 1) / (4 * QT);
+  const int QWs = (G <= 4 && B * qtiles4 * Hkv >= 8ll * cus) ? 4 : (B * qtiles2 * Hkv >= 8ll * cus ? 2 : 1);
   const int64_t qtiles = ((int64_t)max_seqlen_q + QT * QWs - 1) / (QT * QWs);
   LFS_REQUIRE(B * qtiles < (1ll << 31) && Hkv < 65536, "prefill_attention: grid too large");
   const dim3 grid((unsigned)(B * qtiles), (unsigned)Hkv);
@@ -375,11 +379,11 @@ extern "C" int lfs_prefill_attention(const void* q, const void* k, const void* v
   launch_prefill<DD, PG, QQ>(G, grid, st, qq, kk, vv, cu_seqlens_q, cu_seqlens_k, bt, bts, BS, num_slots, oo, Hkv, qt, sl2)
   bool ok;
   if (bt != nullptr)
-    ok = D == 64 ? (QWs == 2 ? LFS_PF(64, true, 2) : LFS_PF(64, true, 1))
-                 : (QWs == 2 ? LFS_PF(128, true, 2) : LFS_PF(128, true, 1));
+    ok = D == 64 ? (QWs == 4 ? LFS_PF(64, true, 4) : QWs == 2 ? LFS_PF(64, true, 2) : LFS_PF(64, true, 1))
+                 : (QWs == 4 ? LFS_PF(128, true, 4) : QWs == 2 ? LFS_PF(128, true, 2) : LFS_PF(128, true, 1));
   else
-    ok = D == 64 ? (QWs == 2 ? LFS_PF(64, false, 2) : LFS_PF(64, false, 1))
-                 : (QWs == 2 ? LFS_PF(128, false, 2) : LFS_PF(128, false, 1));
+    ok = D == 64 ? (QWs == 4 ? LFS_PF(64, false, 4) : QWs == 2 ? LFS_PF(64, false, 2) : LFS_PF(64, false, 1))
+                 : (QWs == 4 ? LFS_PF(128, false, 4) : QWs == 2 ? LFS_PF(128, false, 2) : LFS_PF(128, false, 1));
 #undef LFS_PF
   LFS_REQUIRE(ok, "prefill_attention: unsupported group size %d", G);
   return check_launch("prefill_attention");

@@ -130,13 +130,14 @@ def test_prefill_long_prompt_and_graph_grid():
     assert_close(f64(o), ref, "long prompt")
 
 
-def test_prefill_large_grid_two_subtiles_vs_torch_fp32():
-    """A grid large enough for two 16-query sub-tiles per workgroup (G * 2
-    waves sharing each K / V tile): against causal attention computed per
-    sequence in float32 with torch on the GPU (the float64 oracle is too
-    slow at this size)."""
+@pytest.mark.parametrize("B,L,Hq,Hkv,D", [(8, 1024, 16, 8, 64), (16, 2048, 12, 4, 64)])
+def test_prefill_large_grid_subtiles_vs_torch_fp32(B, L, Hq, Hkv, D):
+    """Grids large enough for two (8 x 1024 tokens, G = 2) or four (16 x 2048
+    tokens, G = 3: the bench shape) 16-query sub-tiles per workgroup (G * 2
+    or G * 4 waves sharing each K / V tile): against causal attention
+    computed per sequence in float32 with torch on the GPU (the float64
+    oracle is too slow at this size)."""
     g = torch.Generator(device=DEV).manual_seed(13)
-    B, L, Hq, Hkv, D = 8, 1024, 16, 8, 64
     q = torch.randn(B * L, Hq, D, generator=g, device=DEV).to(torch.bfloat16)
     k = torch.randn(B * L, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
     v = torch.randn(B * L, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
