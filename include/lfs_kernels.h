@@ -58,6 +58,8 @@
  *   lfs_sample_gumbel       temperature + Gumbel-max sampling,
  *                           utils/sampler.py:35-53 (Sampler.forward), with
  *                           its Exp(1) noise from Philox4x32-10
+ *   lfs_sample_gumbel_split  the same sampler with each row cut into slices
+ *                           (a caller workspace; same picks)
  * Fused row kernels of the decode step around those calls (each replaces a
  * chain of torch ops of the reference model):
  *   lfs_add_rmsnorm         RMSNorm with fused residual add, model/utils.py:53-67
@@ -99,7 +101,7 @@
 extern "C" {
 #endif
 
-#define LFS_ABI_VERSION 11
+#define LFS_ABI_VERSION 12
 
 /* argument errors (negative); launch errors are positive hipError_t values */
 #define LFS_EINVAL (-1)
@@ -300,6 +302,20 @@ int lfs_fp8_index(const void* q, const float* q_s, const void* k, const float* k
  */
 int lfs_sample_gumbel(const void* logits, int64_t ld, const float* temperatures, int64_t B, int32_t vocab,
                       uint64_t seed, uint64_t offset, int64_t* out, float* noise_out, void* stream);
+
+/*
+ * The same sampling with each row cut into slices of consecutive elements,
+ * one workgroup per (row, slice), then a per-row pick of the best slice:
+ * the same picks (and noise) as lfs_sample_gumbel, with more workgroups
+ * when the batch alone would leave compute units idle.  workspace: at least
+ * lfs_sample_gumbel_workspace_bytes(B, vocab) bytes, 8-byte aligned (0
+ * bytes: the call is one pass and needs none; size it on the device that
+ * runs the call).
+ */
+int64_t lfs_sample_gumbel_workspace_bytes(int64_t B, int32_t vocab);
+int lfs_sample_gumbel_split(const void* logits, int64_t ld, const float* temperatures, int64_t B,
+                            int32_t vocab, uint64_t seed, uint64_t offset, int64_t* out, float* noise_out,
+                            void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * add_rmsnorm, per row t of x: bf16 [T, d]:

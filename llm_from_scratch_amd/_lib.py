@@ -11,7 +11,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "liblfs_kernels.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 # size of the library's static paged-decode workspace (LFS_DECODE_SCRATCH_BYTES)
 DECODE_SCRATCH_BYTES = 64 << 20
 
@@ -55,6 +55,9 @@ SIGNATURES = {
                                      _c_i64, _c_p]),
     "lfs_sample_gumbel": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_i32, ctypes.c_uint64, ctypes.c_uint64,
                                          _c_p, _c_p, _c_p]),
+    "lfs_sample_gumbel_workspace_bytes": (ctypes.c_int64, [_c_i64, _c_i32]),
+    "lfs_sample_gumbel_split": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_i32, ctypes.c_uint64, ctypes.c_uint64,
+                                               _c_p, _c_p, _c_p, _c_i64, _c_p]),
     "lfs_prefill_attention": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i64, _c_p,
                                              _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_f, _c_p]),
     "lfs_moe_align_tiles": (ctypes.c_int64, [_c_i64, _c_i32, _c_i32, _c_i32]),

@@ -11,7 +11,14 @@
 // the elements as softmax(x / T)_i / max(e_i, 1e-10) does (the softmax's
 // normaliser is common to the row); ties go to the lowest index.  Four
 // consecutive elements per lane per step (one 8-byte load, one Philox call).
+// With a workspace (lfs_sample_gumbel_split) each row is cut into S slices
+// of consecutive elements, one workgroup per (row, slice) writing its
+// slice's best (score, index), and a second launch picks each row's best
+// slice by the same rule -- the same picks, with S times the workgroups
+// when the batch alone would leave CUs idle.
 #include "common.h"
+
+#include <algorithm>
 
 namespace lfs {
 namespace {
@@ -55,17 +62,23 @@ __device__ __forceinline__ void load4(const uint16_t* row, int64_t i, int V, flo
   }
 }
 
+// One workgroup per (row b, slice blockIdx.y of gridDim.y): the element
+// groups of the slice; the slice's best goes to part[b * S + slice] (score
+// bits, index) when part is given, else (one slice) straight to out[b].
 __global__ __launch_bounds__(1024) void sample_gumbel_kernel(const uint16_t* __restrict__ logits, int64_t ld,
                                                             const float* __restrict__ temps, int V, uint64_t seed,
                                                             uint64_t offset, int64_t* __restrict__ out,
-                                                            float* __restrict__ noise_out) {
+                                                            float* __restrict__ noise_out, uint2* __restrict__ part) {
   __shared__ float red_v[SNT / 64];
   __shared__ int red_i[SNT / 64];
   const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int S = gridDim.y, slice = blockIdx.y;
   const uint16_t* row = logits + (int64_t)b * ld;
   const float T = temps[b];
   const bool vec = ((ld & 3) == 0) && ((((uintptr_t)logits) & 7u) == 0);
   const int n4 = (V + 3) / 4;
+  const int chunk = (n4 + S - 1) / S;
+  const int g_end = min(n4, (slice + 1) * chunk);
 
   // ---- one pass: softmax(x / T)_i / e_i = exp(x_i / T - log e_i) / Z, so
   // its argmax is the argmax of x_i / T - log(max(e_i, 1e-10)) (ties: lowest
@@ -74,7 +87,7 @@ __global__ __launch_bounds__(1024) void sample_gumbel_kernel(const uint16_t* __r
   const float invT = 1.0f / T;
   float best = -INFINITY;
   int besti = 0x7FFFFFFF;
-  for (int g = tid; g < n4; g += SNT) {
+  for (int g = slice * chunk + tid; g < g_end; g += SNT) {
     float x[4];
     load4(row, 4ll * g, V, x, vec);
     const uint64_t lo = (uint64_t)(uint32_t)offset + (uint64_t)g;
@@ -106,8 +119,46 @@ __global__ __launch_bounds__(1024) void sample_gumbel_kernel(const uint16_t* __r
   if (tid == 0) {
     for (int w = 1; w < SNT / 64; ++w)
       if (red_v[w] > best || (red_v[w] == best && red_i[w] < besti)) { best = red_v[w]; besti = red_i[w]; }
-    out[b] = besti == 0x7FFFFFFF ? 0 : besti;
+    if (part != nullptr) part[(int64_t)b * S + slice] = make_uint2(__float_as_uint(best), (uint32_t)besti);
+    else out[b] = besti == 0x7FFFFFFF ? 0 : besti;
   }
+}
+
+// Each row's best over its S slices (slices in index order, so the rule
+// "larger score, or equal score and smaller index" picks what one pass
+// over the row picks).
+__global__ __launch_bounds__(256) void sample_gumbel_reduce_kernel(const uint2* __restrict__ part, int64_t B, int S,
+                                                                   int64_t* __restrict__ out) {
+  const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (b >= B) return;
+  float best = -INFINITY;
+  int besti = 0x7FFFFFFF;
+  for (int s = 0; s < S; ++s) {
+    const uint2 p = part[b * S + s];
+    const float v = __uint_as_float(p.x);
+    const int i = (int)p.y;
+    if (v > best || (v == best && i < besti)) { best = v; besti = i; }
+  }
+  out[b] = besti == 0x7FFFFFFF ? 0 : besti;
+}
+
+// Slices per row: enough workgroups for two per CU, each slice at least
+// one element group per thread.
+int sampler_slices(int64_t B, int V) {
+  static int cu_cache[64] = {0};
+  int cus = 256, dev = 0;
+  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
+    if (cu_cache[dev] == 0) {
+      int n = 0;
+      cu_cache[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0
+                          ? n : 256;
+    }
+    cus = cu_cache[dev];
+  }
+  if (B <= 0) return 1;
+  const int64_t by_cus = (2 * (int64_t)cus + B - 1) / B;
+  const int64_t by_len = std::max<int64_t>(1, ((int64_t)V + 4 * SNT - 1) / (4 * SNT));
+  return (int)std::max<int64_t>(1, std::min<int64_t>({by_cus, by_len, 16}));
 }
 
 }  // namespace
@@ -123,7 +174,37 @@ extern "C" int lfs_sample_gumbel(const void* logits, int64_t ld, const float* te
   if (B == 0) return 0;
   LFS_REQUIRE(logits && temperatures && out, "sample_gumbel: null pointer");
   LFS_REQUIRE(B < (1ll << 31), "sample_gumbel: too many rows");
-  hipLaunchKernelGGL(sample_gumbel_kernel, dim3((unsigned)B), dim3(SNT), 0, (hipStream_t)stream,
-                     (const uint16_t*)logits, ld, temperatures, vocab, seed, offset, out, noise_out);
+  hipLaunchKernelGGL(sample_gumbel_kernel, dim3((unsigned)B, 1), dim3(SNT), 0, (hipStream_t)stream,
+                     (const uint16_t*)logits, ld, temperatures, vocab, seed, offset, out, noise_out, nullptr);
   return check_launch("sample_gumbel");
+}
+
+extern "C" int64_t lfs_sample_gumbel_workspace_bytes(int64_t B, int32_t vocab) {
+  if (B < 0 || vocab <= 0) return -1;
+  const int S = sampler_slices(B, vocab);
+  return S > 1 ? 8 * B * S : 0;
+}
+
+extern "C" int lfs_sample_gumbel_split(const void* logits, int64_t ld, const float* temperatures, int64_t B,
+                                       int32_t vocab, uint64_t seed, uint64_t offset, int64_t* out,
+                                       float* noise_out, void* workspace, int64_t workspace_bytes, void* stream) {
+  LFS_REQUIRE(B >= 0 && vocab > 0 && ld >= vocab, "sample_gumbel: bad shape B=%lld V=%d ld=%lld", (long long)B,
+              vocab, (long long)ld);
+  if (B == 0) return 0;
+  LFS_REQUIRE(logits && temperatures && out, "sample_gumbel: null pointer");
+  LFS_REQUIRE(B < (1ll << 31), "sample_gumbel: too many rows");
+  const int S = sampler_slices(B, vocab);
+  if (S == 1)
+    return lfs_sample_gumbel(logits, ld, temperatures, B, vocab, seed, offset, out, noise_out, stream);
+  LFS_REQUIRE(workspace != nullptr && workspace_bytes >= 8 * B * S && ((uintptr_t)workspace & 7u) == 0,
+              "sample_gumbel: workspace of %lld bytes < required %lld (8-byte aligned)", (long long)workspace_bytes,
+              (long long)(8 * B * S));
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(sample_gumbel_kernel, dim3((unsigned)B, (unsigned)S), dim3(SNT), 0, st, (const uint16_t*)logits,
+                     ld, temperatures, vocab, seed, offset, out, noise_out, (uint2*)workspace);
+  const int rc = check_launch("sample_gumbel(slices)");
+  if (rc) return rc;
+  hipLaunchKernelGGL(sample_gumbel_reduce_kernel, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, st,
+                     (const uint2*)workspace, B, S, out);
+  return check_launch("sample_gumbel(reduce)");
 }

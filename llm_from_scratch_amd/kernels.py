@@ -459,7 +459,7 @@ def fp8_index(q: torch.Tensor, q_s: torch.Tensor, k: torch.Tensor, k_s: torch.Te
 
 def sample_gumbel(logits: torch.Tensor, temperatures: torch.Tensor, seed: int, offset: int,
                   return_noise: bool = False):
-    """Temperature + Gumbel-max sampling in one launch (utils/sampler.py:35-53:
+    """Temperature + Gumbel-max sampling (utils/sampler.py:35-53:
     argmax(softmax(logits / T) / Exp(1) noise), noise clamped at 1e-10).
 
     logits: bf16 [B, V] (unit column stride); temperatures: fp32 [B].  The
@@ -478,9 +478,13 @@ def sample_gumbel(logits: torch.Tensor, temperatures: torch.Tensor, seed: int, o
     assert temperatures.shape == (B,)
     out = torch.empty(B, dtype=torch.int64, device=logits.device)
     noise = torch.empty(B, V, dtype=torch.float32, device=logits.device) if return_noise else None
-    rc = _lib.load().lfs_sample_gumbel(_ptr(logits), logits.stride(0), _ptr(temperatures), B, V,
-                                       int(seed) & ((1 << 64) - 1), int(offset) & ((1 << 64) - 1), _ptr(out),
-                                       _ptr(noise) if noise is not None else None, _stream(logits))
+    L = _lib.load()
+    # rows cut into slices when the batch alone leaves CUs idle (same picks)
+    need = int(L.lfs_sample_gumbel_workspace_bytes(B, V)) if B > 0 else 0
+    ws = torch.empty(max(need, 8), dtype=torch.uint8, device=logits.device)
+    rc = L.lfs_sample_gumbel_split(_ptr(logits), logits.stride(0), _ptr(temperatures), B, V,
+                                   int(seed) & ((1 << 64) - 1), int(offset) & ((1 << 64) - 1), _ptr(out),
+                                   _ptr(noise) if noise is not None else None, _ptr(ws), ws.numel(), _stream(logits))
     _lib.check(rc, "sample_gumbel")
     return (out, noise) if return_noise else out
 

@@ -61,3 +61,40 @@ def test_engine_sampler_advances():
     b = s(logits, temps, g)
     assert a.dtype == torch.int64 and a.shape == (64,)
     assert not torch.equal(a, b)  # uniform logits: fresh noise picks other tokens
+
+
+@pytest.mark.parametrize("B,V", [(128, 32000), (4, 32000), (16, 50000), (1, 7), (2048, 4096), (5, 4100)])
+def test_sample_gumbel_slices_pick_what_one_pass_picks(B, V):
+    """lfs_sample_gumbel_split (rows cut into slices, a per-row reduce)
+    returns exactly the tokens of the one-pass lfs_sample_gumbel, with the
+    same noise, on random logits and on rows whose equal maxima start in a
+    later slice (ties go to the lowest index in both)."""
+    from llm_from_scratch_amd import _lib
+    L = _lib.load()
+    g = torch.Generator(device=DEV).manual_seed(7 * B + V)
+    for case in ("random", "ties"):
+        if case == "random":
+            logits = (torch.randn(B, V, generator=g, device=DEV) * 4).to(torch.bfloat16)
+        else:  # equal maxima from mid-row on; T = 1e-30 makes x / T swamp the noise: exact score ties
+            logits = torch.zeros(B, V, device=DEV).to(torch.bfloat16)
+            logits[:, V // 2::97] = 30.0
+        temps = torch.full((B,), 0.7 if case == "random" else 1e-30, device=DEV)
+        one = torch.empty(B, dtype=torch.int64, device=DEV)
+        rc = L.lfs_sample_gumbel(logits.data_ptr(), V, temps.data_ptr(), B, V, 1234, 99, one.data_ptr(), None,
+                                 torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+        need = int(L.lfs_sample_gumbel_workspace_bytes(B, V))
+        ws = torch.empty(max(need, 8), dtype=torch.uint8, device=DEV)
+        sl = torch.empty(B, dtype=torch.int64, device=DEV)
+        rc = L.lfs_sample_gumbel_split(logits.data_ptr(), V, temps.data_ptr(), B, V, 1234, 99, sl.data_ptr(), None,
+                                       ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+        torch.cuda.synchronize()
+        assert torch.equal(one, sl), f"{case}: {int((one != sl).sum())} rows differ"
+        if case == "ties":
+            assert bool((sl == V // 2).all()), "ties must go to the lowest index"
+        assert torch.equal(K.sample_gumbel(logits, temps, 1234, 99), one)
+    if need:  # too small a workspace is refused, nothing launched
+        rc = L.lfs_sample_gumbel_split(logits.data_ptr(), V, temps.data_ptr(), B, V, 1, 0, sl.data_ptr(), None,
+                                       ws.data_ptr(), need - 8, torch.cuda.current_stream().cuda_stream)
+        assert rc != 0
