@@ -124,17 +124,29 @@ def weight_dequant(x: torch.Tensor, s: torch.Tensor, block_size: int = 128) -> t
 
 def default_gemm_splits(M: int, N: int, K: int) -> int:
     """K splits for fp8_gemm: 1 when the 128x128 output tiles alone give
-    >= 192 workgroups or K has fewer than 12 blocks of 128; otherwise up to
-    ~256 workgroups, keeping >= 6 K blocks per split (a split's fixed
-    latency outweighs a shorter K loop below that, and the fp32 partials it
-    adds must be reduced) and the partials <= 8 MB.  Measured on MI355X at
-    M = 128: K = 768 is fastest unsplit (11 us vs 15.5 us at 3 splits),
-    K = 4608, N = 768 at 6 splits (15.7 us vs 19.8 us at 18)."""
+    >= 192 workgroups or K has fewer than 12 blocks of 128.  Below that grid
+    each workgroup already runs two K slices, and a call takes about 6.5 us
+    plus 1.1 us per K block of a slice (measured back to back on MI355X at
+    M = 128-512, K 2048 / 4096, N 1536-8192), so splitting pays where it
+    shortens long slices by more than the fp32 partials and their reduction
+    cost: with >= 24 K blocks, max(4, K blocks / 6) splits (K = 4096: 16-22 %
+    faster than unsplit at 12-64 tiles; K = 4608, N = 768 at 6 splits 14.7
+    us); with 12-23 K blocks only for <= 16 tiles (4 splits, 15.4 -> 14.0
+    us at M = 128, K = 2048, N = 1536), since from 24 tiles up the unsplit
+    call is the fastest (N = 5632: 15.9 us against 18.2 at 2 splits).  At
+    most ~256 workgroups and 32 MB of partials (M = 128, K = 4096, N = 8192:
+    4 splits 22.0 us, unsplit 25.9)."""
     tiles = -(-M // 128) * -(-N // 128)
     kt = K // 128
     if tiles >= 192 or kt < 12:
         return 1
-    splits = min(kt // 6, max(1, 256 // tiles), max(1, (8 << 20) // max(1, 4 * M * N)))
+    if kt >= 24:
+        splits = max(4, kt // 6)
+    elif tiles <= 16:
+        splits = min(4, kt // 4)
+    else:
+        return 1
+    splits = min(splits, max(1, 256 // tiles), max(1, (32 << 20) // max(1, 4 * M * N)))
     return max(1, splits)
 
 
