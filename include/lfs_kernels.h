@@ -101,7 +101,7 @@
 extern "C" {
 #endif
 
-#define LFS_ABI_VERSION 12
+#define LFS_ABI_VERSION 13
 
 /* argument errors (negative); launch errors are positive hipError_t values */
 #define LFS_EINVAL (-1)
@@ -216,15 +216,20 @@ int lfs_store_kvcache(const void* key, int64_t k_stride_t, const void* value, in
  * merged by log-sum-exp.  blocks_per_split = 0 (B <= 8192): balanced split,
  * a fixed grid of one 4-wave workgroup per CU, each taking an equal share of
  * the (sequence, kv-head group, tile) work whatever the lengths, then the
- * same merge.  Either way the grid depends only on the shapes (not on the
- * lengths), so the call is graph-capturable.
+ * same merge.  blocks_per_split = -1: single launch, one 8-wave workgroup
+ * per (sequence, pair of kv heads) (one kv head when Hkv is odd) whose waves
+ * walk interleaved tiles and merge through LDS; no workspace, no second
+ * launch.  Whatever the mode, the grid depends only on the shapes (not on
+ * the lengths), so the call is graph-capturable.
  * workspace: at least lfs_paged_decode_workspace_bytes(...) bytes (for 0 a
- * bound from the current device's CU count: size it on that device).
+ * bound from the current device's CU count: size it on that device; for -1
+ * zero, and workspace may be NULL).
  * Optionally (q_out and q_scale both non-NULL) also the act_quant of each
  * output row, the output projection's FP8 input: q_out e4m3fn [B, Hq*D],
  * q_scale fp32 [B, Hq*D/128], bit-identical to lfs_act_quant(out, 128)
- * (needs Hq*D % 128 == 0); the merge then runs one workgroup per
- * (128-value group, sequence) instead of one per (head, sequence).
+ * (needs Hq*D % 128 == 0, and for -1 also an even Hkv or G*D % 128 == 0);
+ * the merge then runs one workgroup per (128-value group, sequence) instead
+ * of one per (head, sequence).
  * D in {64, 128}; Hq % Hkv == 0, Hq/Hkv <= 8; block_size a multiple of 16.
  */
 int64_t lfs_paged_decode_workspace_bytes(int64_t B, int32_t num_q_heads, int32_t head_dim,

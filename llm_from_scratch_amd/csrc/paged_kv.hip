@@ -262,14 +262,19 @@ struct DecodeWave {
   // End of a range: sum the token subgroups (lanes with the same dc), then
   // the normalised bf16 output of query heads kh*G + g (whole context) or
   // the unnormalised partial to workspace rows prow + g.
-  __device__ __forceinline__ void finish(bool whole, uint16_t* __restrict__ out, float* __restrict__ ws_o,
-                                         float* __restrict__ ws_ml, int64_t b, int kh, int Hq, int64_t prow) {
+  // Sum acc over the token subgroups: afterwards lanes with ts == 0 hold the
+  // wave's totals for dims dc*8 .. +7 of every head.
+  __device__ __forceinline__ void reduce_lanes() {
 #pragma unroll
     for (int o = Geo::LPR; o < 64; o <<= 1)
 #pragma unroll
       for (int g = 0; g < G; ++g)
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[g][e] += __shfl_xor(acc[g][e], o, 64);
+  }
+  __device__ __forceinline__ void finish(bool whole, uint16_t* __restrict__ out, float* __restrict__ ws_o,
+                                         float* __restrict__ ws_ml, int64_t b, int kh, int Hq, int64_t prow) {
+    reduce_lanes();
     if (whole) {
       if (ts == 0) {
 #pragma unroll
@@ -301,32 +306,28 @@ struct DecodeWave {
   }
 };
 
-// One wave: kv head kh of sequence b over context rows [t_begin, t_end)
-// (t_begin a multiple of `tile`, t_end <= Lc).  A range that is the whole
-// context (t_begin == 0, t_end >= Lc) writes the normalised bf16 output;
-// otherwise the unnormalised partial of query head kh*G + g goes to row
-// prow + g of the workspace (o: ws_o[row*D ..], (m, l): ws_ml[row*2 ..]).
-// pw: the wave's private LDS slice (T * GP floats).
+// One wave streams tiles of kv head kh of one sequence into w: tile i of the
+// walk covers context rows [t_begin + i*tstride*tile, +tile) clipped to
+// t_end (t_begin a multiple of `tile`, t_end <= the context length), so a
+// range of consecutive tiles is tstride 1 and every S-th tile from s*tile
+// is t_begin = s*tile, tstride S.  btrow: the sequence's block-table row;
+// block ids at or past id_end are never loaded.  pw: the wave's private
+// LDS slice (T * GP floats).
 template <int D, int G>
-__device__ __forceinline__ void decode_chunk(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
-    const uint16_t* __restrict__ vc, const int32_t* __restrict__ btrow, float* __restrict__ ws_o,
-    float* __restrict__ ws_ml, uint16_t* __restrict__ out, int Hkv, int BS, int64_t NB, int tile,
-    float scale_log2, int b, int kh, int64_t t_begin, int64_t t_end, int64_t Lc, int64_t prow,
-    float* __restrict__ pw, int lane) {
+__device__ __forceinline__ void decode_walk(
+    DecodeWave<D, G>& w, const typename DecodeWave<D, G>::QBuf& qa, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, const int32_t* __restrict__ btrow, int BS, int64_t NB, int tile,
+    float scale_log2, int kh, int64_t t_begin, int64_t t_end, int tstride, int64_t id_end,
+    float* __restrict__ pw) {
   using W = DecodeWave<D, G>;
-  W w(lane, Hkv);
-  const int Hq = Hkv * G;
-  typename W::QBuf qa;
-  w.load_q(qa, q, b, kh, Hq);
-
-  const int ntiles = (int)((t_end - t_begin + tile - 1) / tile);
-  // The chunk's block ids, 256 at a time (window w0 .. w0 + 255 of the
-  // table row): lane l holds ids 4l .. 4l+3 of the window, read back with
-  // readlane, so no tile waits on a scalar load of its block id.  Ids past
-  // the chunk's last block are never read (loaded as 0 to stay in bounds).
+  const int lane = w.lane;
+  const int64_t step_rows = (int64_t)tile * tstride;
+  const int ntiles = (int)((t_end - t_begin + step_rows - 1) / step_rows);
+  // The walk's block ids, 256 at a time (window w0 .. w0 + 255 of the table
+  // row): lane l holds ids 4l .. 4l+3 of the window, read back with
+  // readlane, so no tile waits on a scalar load of its block id.  Ids at or
+  // past id_end are never read (loaded as 0 to stay in bounds).
   const int64_t blk_first = t_begin / BS;
-  const int64_t blk_last = (t_end - 1) / BS;
   int64_t w0 = -1;
   uint4 ids = make_uint4(0, 0, 0, 0);
   auto load_window = [&](int64_t wb) {
@@ -334,18 +335,18 @@ __device__ __forceinline__ void decode_chunk(
     const int64_t e = wb + 4 * lane;
     uint32_t v[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) v[c] = e + c <= blk_last ? (uint32_t)btrow[e + c] : 0u;
+    for (int c = 0; c < 4; ++c) v[c] = e + c < id_end ? (uint32_t)btrow[e + c] : 0u;
     ids = make_uint4(v[0], v[1], v[2], v[3]);
   };
   auto block_id = [&](int64_t bi) -> int32_t {
-    if (bi < w0 || bi >= w0 + 256) load_window(bi);  // chunks longer than 256 blocks: next window
+    if (bi < w0 || bi >= w0 + 256) load_window(bi);  // walks longer than 256 blocks: next window
     const int e = (int)(bi - w0);
     const int src = e >> 2, c = e & 3;
     const uint32_t x = c == 0 ? ids.x : c == 1 ? ids.y : c == 2 ? ids.z : ids.w;
     return (int32_t)__builtin_amdgcn_readlane((int)x, src);
   };
   load_window(blk_first);
-  // tile i of the chunk: valid row count (0 for a skipped block) and the
+  // tile i of the walk: valid row count (0 for a skipped block) and the
   // element offset of its first row.  Tiles at or past `last` are
   // look-ahead fillers: n = 0 and row 0 of block 0, so their loads all hit
   // one line (they only keep the per-step load count constant).
@@ -356,7 +357,7 @@ __device__ __forceinline__ void decode_chunk(
       off = (int64_t)kh * D;
       return;
     }
-    const int64_t t0 = t_begin + (int64_t)i * tile;
+    const int64_t t0 = t_begin + (int64_t)i * step_rows;
     n = (int)min((int64_t)tile, t_end - t0);
     const int32_t blk = block_id(t0 / BS);
     const bool ok = blk >= 0 && (int64_t)blk < NB;
@@ -366,10 +367,10 @@ __device__ __forceinline__ void decode_chunk(
 
   // Pipeline one tile deep over two K and two V buffers: step i issues the
   // loads of tile i+1 into the other buffers, then computes tile i.  The
-  // tiles of a chunk are processed in straight-line code (MAXT steps
+  // tiles of a walk are processed in straight-line code (MAXT steps
   // unrolled, with early exits), every step issuing the same loads, so the
   // compiler's in-order wait counts are exact: tile i waits only for its own
-  // loads.  Chunks longer than MAXT tiles are walked MAXT tiles at a time.
+  // loads.  Walks longer than MAXT tiles go MAXT tiles at a time.
   constexpr int MAXT = 8;
   typename W::KBuf ka0, ka1;
   typename W::VBuf va0, va1;
@@ -403,6 +404,29 @@ __device__ __forceinline__ void decode_chunk(
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // drain the look-ahead loads
   }
+  (void)lane;
+}
+
+// One wave: kv head kh of sequence b over context rows [t_begin, t_end)
+// (t_begin a multiple of `tile`, t_end <= Lc).  A range that is the whole
+// context (t_begin == 0, t_end >= Lc) writes the normalised bf16 output;
+// otherwise the unnormalised partial of query head kh*G + g goes to row
+// prow + g of the workspace (o: ws_o[row*D ..], (m, l): ws_ml[row*2 ..]).
+// pw: the wave's private LDS slice (T * GP floats).
+template <int D, int G>
+__device__ __forceinline__ void decode_chunk(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, const int32_t* __restrict__ btrow, float* __restrict__ ws_o,
+    float* __restrict__ ws_ml, uint16_t* __restrict__ out, int Hkv, int BS, int64_t NB, int tile,
+    float scale_log2, int b, int kh, int64_t t_begin, int64_t t_end, int64_t Lc, int64_t prow,
+    float* __restrict__ pw, int lane) {
+  using W = DecodeWave<D, G>;
+  W w(lane, Hkv);
+  const int Hq = Hkv * G;
+  typename W::QBuf qa;
+  w.load_q(qa, q, b, kh, Hq);
+  decode_walk<D, G>(w, qa, kc, vc, btrow, BS, NB, tile, scale_log2, kh, t_begin, t_end, 1,
+                    (t_end - 1) / BS + 1, pw);
   w.finish(t_begin == 0 && t_end >= Lc, out, ws_o, ws_ml, b, kh, Hq, prow);
 }
 
@@ -537,6 +561,103 @@ __global__ __launch_bounds__(256) void paged_decode_balanced(
       ++b;
       while (b < B && tp[b + 1] == tp[b]) ++b;  // sequences with no context
     }
+  }
+}
+
+// Single launch (blocks_per_split -1), one workgroup per (sequence, group of
+// HG kv heads): the workgroup's NW waves are HG heads x S = NW/HG
+// interleaved walks, wave s of a head taking the tiles s, s + S, s + 2S, ...
+// of the context, so the walks start at fixed block-table columns (their
+// first block ids load alongside the context length, not after it) and all
+// finish within a tile of each other.  The waves' partials (o, m, l) meet
+// in LDS and the log-sum-exp merge writes the bf16 output: no tile-count
+// scan, no second launch, no partial round trip through HBM.  With qo / qs
+// the workgroup also writes the act_quant codes and scales of its HG*G*D
+// output values, which must be whole 128-value groups (HG*G*D % 128 == 0).
+// Grid: B * ngrp workgroups, the head group fastest, so a sequence's groups
+// (adjacent pieces of the same token rows) are read at about the same time.
+// A workgroup's throughput is bounded by its CU (about 30 GB/s measured), so
+// this pays only when the grid covers every CU and no context is much
+// longer than the rest can hide: the host's default takes it for B * ngrp >=
+// CUs and tables of at most 8192 tokens.
+template <int D, int G, int HG, int NW>
+__global__ __launch_bounds__(64 * NW) void paged_decode_pairs(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+    const int64_t* __restrict__ ctx_lens, const int32_t* __restrict__ bt, int64_t bt_stride,
+    uint16_t* __restrict__ out, uint8_t* __restrict__ qo, float* __restrict__ qs, int Hkv, int BS, int64_t NB,
+    int max_blocks, int tile, float scale_log2, int ngrp) {
+  using Geo = DecodeGeom<D>;
+  using W = DecodeWave<D, G>;
+  constexpr int S = NW / HG;
+  constexpr int E = HG * G * D;  // output values of the workgroup
+  __shared__ __attribute__((aligned(16))) float p_lds[NW][Geo::T * W::GP];
+  __shared__ __attribute__((aligned(16))) float part_o[NW][G * D];
+  __shared__ float part_m[NW][G], part_l[NW][G];
+  __shared__ __attribute__((aligned(16))) uint16_t vals[E];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int hl = wave / S, s = wave - hl * S;
+  const int b = blockIdx.x / ngrp, grp = blockIdx.x - b * ngrp;
+  const int kh = grp * HG + hl;
+  const int Hq = Hkv * G;
+  const int64_t Lc = min(ctx_lens[b], (int64_t)max_blocks * BS);
+  if (kh < Hkv) {
+    W w(lane, Hkv);
+    typename W::QBuf qa;
+    w.load_q(qa, q, b, kh, Hq);
+    if (Lc > (int64_t)s * tile)
+      decode_walk<D, G>(w, qa, kc, vc, bt + (int64_t)b * bt_stride, BS, NB, tile, scale_log2, kh,
+                        (int64_t)s * tile, Lc, S, max_blocks, p_lds[wave]);
+    w.reduce_lanes();
+    if (w.ts == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float* dst = &part_o[wave][g * D + w.dc * 8];
+        *reinterpret_cast<float4*>(dst) = make_float4(w.acc[g][0], w.acc[g][1], w.acc[g][2], w.acc[g][3]);
+        *reinterpret_cast<float4*>(dst + 4) = make_float4(w.acc[g][4], w.acc[g][5], w.acc[g][6], w.acc[g][7]);
+      }
+    }
+    if (lane < G) {
+      part_m[wave][lane] = w.m_run;
+      part_l[wave][lane] = w.l_run;
+    }
+  }
+  __syncthreads();
+  // log-sum-exp merge of the S walks of each head (L = 0: zeros)
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    const int h2 = e / (G * D), r = e - h2 * (G * D), g = r / D;
+    if (grp * HG + h2 >= Hkv) continue;
+    const int w0 = h2 * S;
+    float M = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < S; ++t) M = fmaxf(M, part_m[w0 + t][g]);
+    float num = 0.f, den = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int t = 0; t < S; ++t) {
+        const float wt = exp2f(part_m[w0 + t][g] - M);
+        den = fmaf(wt, part_l[w0 + t][g], den);
+        num = fmaf(wt, part_o[w0 + t][r], num);
+      }
+    }
+    const uint16_t v = (uint16_t)f32_to_bf16(den > 0.f ? num / den : 0.f);
+    out[((int64_t)b * Hq + (int64_t)(grp * HG + h2) * G) * D + r] = v;
+    vals[e] = v;
+  }
+  if (qo == nullptr) return;
+  __syncthreads();
+  // act_quant of the workgroup's E / 128 groups, 16 lanes x 8 values each
+  const int t = threadIdx.x;
+  if (t < E / 8) {
+    float f[8];
+    unpack8(*reinterpret_cast<const uint4*>(&vals[t * 8]), f);
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[i]));
+    amax = group_max<16>(amax);
+    const float sc = scale_from_amax(amax, false);
+    const int64_t e0 = (int64_t)b * Hq * D + (int64_t)grp * E;  // first output value of the workgroup
+    *reinterpret_cast<uint2*>(qo + e0 + t * 8) = quant8(f, sc);
+    if ((t & 15) == 0) qs[e0 / 128 + t / 16] = sc;
   }
 }
 
@@ -712,6 +833,40 @@ bool dispatch_balanced(int G, unsigned nwg, dim3 block, hipStream_t st, const ui
 #undef LFS_G
 }
 
+template <int D, int HG, int NW>
+bool dispatch_pairs_hg(int G, unsigned nwg, hipStream_t st, const uint16_t* q, const uint16_t* kc,
+                       const uint16_t* vc, const int64_t* cl, const int32_t* bt, int64_t bts, uint16_t* out,
+                       uint8_t* qo, float* qs, int Hkv, int BS, int64_t NB, int max_blocks, int tile, float sl2,
+                       int ngrp) {
+#define LFS_G(GG)                                                                                            \
+  case GG:                                                                                                   \
+    hipLaunchKernelGGL((paged_decode_pairs<D, GG, HG, NW>), dim3(nwg), dim3(64 * NW), 0, st, q, kc, vc, cl,  \
+                       bt, bts, out, qo, qs, Hkv, BS, NB, max_blocks, tile, sl2, ngrp);                      \
+    return true;
+  switch (G) {
+    LFS_G(1) LFS_G(2) LFS_G(3) LFS_G(4) LFS_G(5) LFS_G(6) LFS_G(7) LFS_G(8)
+    default: return false;
+  }
+#undef LFS_G
+}
+
+template <int D>
+bool dispatch_pairs(int HG, int G, unsigned nwg, hipStream_t st, const uint16_t* q, const uint16_t* kc,
+                    const uint16_t* vc, const int64_t* cl, const int32_t* bt, int64_t bts, uint16_t* out,
+                    uint8_t* qo, float* qs, int Hkv, int BS, int64_t NB, int max_blocks, int tile, float sl2,
+                    int ngrp) {
+  return HG == 1 ? dispatch_pairs_hg<D, 1, 8>(G, nwg, st, q, kc, vc, cl, bt, bts, out, qo, qs, Hkv, BS, NB,
+                                               max_blocks, tile, sl2, ngrp)
+                 : dispatch_pairs_hg<D, 2, 8>(G, nwg, st, q, kc, vc, cl, bt, bts, out, qo, qs, Hkv, BS, NB,
+                                               max_blocks, tile, sl2, ngrp);
+}
+
+// kv heads per workgroup of the single-launch decode: two when Hkv is even
+// (a workgroup then reads 2*D*2 of each token row's Hkv*D*2 bytes: at the
+// cfg5 attention shape 46.1 us against 48.9 us with one head per
+// workgroup), else one.  The fused act_quant needs HG*G*D % 128 == 0.
+int pairs_heads_per_group(int Hkv) { return Hkv % 2 == 0 ? 2 : 1; }
+
 // compute units of the current device (the balanced split's grid)
 int decode_cu_count() {
   static int cached[64] = {0};
@@ -795,7 +950,8 @@ extern "C" int lfs_store_kvcache(const void* key, int64_t k_stride_t, const void
 extern "C" int64_t lfs_paged_decode_workspace_bytes(int64_t B, int32_t num_q_heads,
                                                     int32_t head_dim, int32_t max_blocks,
                                                     int32_t blocks_per_split) {
-  if (B < 0 || num_q_heads <= 0 || head_dim <= 0 || max_blocks < 0 || blocks_per_split < 0) return -1;
+  if (B < 0 || num_q_heads <= 0 || head_dim <= 0 || max_blocks < 0 || blocks_per_split < -1) return -1;
+  if (blocks_per_split == -1) return 0;  // single launch: the partials stay in LDS
   if (blocks_per_split == 0) {
     // balanced split: partial rows (nwg + B*ngroups)*wpg*G <= (8*CUs + 2*B)*Hq
     // (wpg*G <= Hq, nwg*wpg <= 4*CUs, ngroups*wpg < 2*Hkv), then B+1 ints
@@ -821,7 +977,8 @@ int paged_decode_impl(const void* q, const void* k_cache, const void* v_cache, c
   LFS_REQUIRE(Hq % Hkv == 0 && Hq / Hkv <= 8,
               "paged_decode: num_q_heads (%d) must be a multiple of num_kv_heads (%d), ratio <= 8", Hq, Hkv);
   LFS_REQUIRE(BS % 16 == 0, "paged_decode: block_size must be a multiple of 16 (got %d)", BS);
-  LFS_REQUIRE(blocks_per_split >= 0, "paged_decode: blocks_per_split must be >= 0 (0: balanced split)");
+  LFS_REQUIRE(blocks_per_split >= -1,
+              "paged_decode: blocks_per_split must be >= -1 (-1: single launch, 0: balanced split)");
   LFS_REQUIRE(blocks_per_split > 0 || B <= BAL_MAXB, "paged_decode: the balanced split (blocks_per_split 0) needs B <= %d",
               BAL_MAXB);
   LFS_REQUIRE(bt_stride >= max_blocks, "paged_decode: block table stride < max_blocks");
@@ -849,6 +1006,23 @@ int paged_decode_impl(const void* q, const void* k_cache, const void* v_cache, c
     if (BS % t == 0) { tile = t; break; }
   const float sl2 = scale * 1.4426950408889634f;
   const int G = Hq / Hkv;
+  if (blocks_per_split == -1) {
+    const int HG = pairs_heads_per_group(Hkv);
+    LFS_REQUIRE(q_out == nullptr || (HG * G * D) % 128 == 0,
+                "paged_decode: the single launch (blocks_per_split -1) cannot quantise this output "
+                "(Hkv = %d, G*D = %d: needs an even Hkv or G*D a multiple of 128)", Hkv, G * D);
+    const int ngrp = (Hkv + HG - 1) / HG;
+    LFS_REQUIRE(B * ngrp < (1ll << 31), "paged_decode: too many (sequence, kv head) workgroups");
+    const bool ok = D == 64
+        ? dispatch_pairs<64>(HG, G, (unsigned)(B * ngrp), st, (const uint16_t*)q, (const uint16_t*)k_cache,
+                             (const uint16_t*)v_cache, context_lens, block_tables, bt_stride, (uint16_t*)out,
+                             (uint8_t*)q_out, q_scale, Hkv, BS, num_blocks, max_blocks, tile, sl2, ngrp)
+        : dispatch_pairs<128>(HG, G, (unsigned)(B * ngrp), st, (const uint16_t*)q, (const uint16_t*)k_cache,
+                              (const uint16_t*)v_cache, context_lens, block_tables, bt_stride, (uint16_t*)out,
+                              (uint8_t*)q_out, q_scale, Hkv, BS, num_blocks, max_blocks, tile, sl2, ngrp);
+    LFS_REQUIRE(ok, "paged_decode: unsupported group size %d", G);
+    return check_launch("paged_decode(single launch)");
+  }
   PartMap pm{};
   if (blocks_per_split == 0) {
     const BalancedGeom bg = balanced_geom(Hkv);

@@ -262,14 +262,34 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
 BALANCED_MAX_BATCH = 8192  # the balanced split scans the batch's tile counts in LDS
 
 
-def default_blocks_per_split(batch: int, num_kv_heads: int, max_blocks: int, block_size: int) -> int:
+PAIRS_MAX_CONTEXT = 8192  # longest table (tokens) the single-launch decode is the default for
+
+
+def _cu_count() -> int:
+    if torch.cuda.is_available():
+        return torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count
+    return 256
+
+
+def default_blocks_per_split(batch: int, num_kv_heads: int, max_blocks: int, block_size: int,
+                             cus: Optional[int] = None) -> int:
     """Split of the decode context (shapes only, so the choice is capturable).
+
+    -1 selects the single launch: one workgroup per (sequence, pair of kv
+    heads), whose waves walk interleaved tiles and merge through LDS (no
+    second launch, no workspace).  A workgroup streams at most ~30 GB/s, so
+    it is the default only when Hkv is even, the B * Hkv / 2 workgroups
+    cover every CU (at most four rounds) and the table holds at most
+    PAIRS_MAX_CONTEXT tokens.  Measured on MI355X at the cfg5 attention
+    shape (B 128, GQA 12/4, D 64, act_quant fused): contexts U[256, 2048]
+    46.1 against 47.5 us balanced, all 2048 tokens 54.8 against 60.3 us; at
+    B 64 the balanced split wins (35.1 against 42.9 us).
 
     0 selects the balanced split: a fixed grid of one 4-wave workgroup per
     CU, each taking an equal share of the (sequence, kv-head group, tile)
-    work, whatever the context lengths.  Measured on MI355X: cfg4 (B 256,
-    lengths log-uniform to 32k) 1169 us against 1523 us for the best fixed
-    chunking; cfg3 44.3 us against 49.7 us.
+    work, whatever the context lengths, then a merge launch.  Measured on
+    MI355X: cfg4 (B 256, lengths log-uniform to 32k) 1169 us against 1523 us
+    for the best fixed chunking; cfg3 44.3 us against 49.7 us.
 
     Above BALANCED_MAX_BATCH sequences, fixed chunks of the returned number
     of blocks, one wave per (sequence, kv head, chunk): with fewer than 1024
@@ -277,6 +297,11 @@ def default_blocks_per_split(batch: int, num_kv_heads: int, max_blocks: int, blo
     256 tokens); with more, chunks grow until the grid has at most 32768
     potential waves (cfg4: 2000 / 1826 / 1683 / 1634 us at 1 / 2 / 4 / 8
     blocks per chunk)."""
+    cus = _cu_count() if cus is None else cus
+    groups = batch * num_kv_heads // 2
+    if (num_kv_heads % 2 == 0 and cus <= groups <= 4 * cus
+            and max_blocks * block_size <= PAIRS_MAX_CONTEXT):
+        return -1
     if batch <= BALANCED_MAX_BATCH:
         return 0
     base = max(1, 256 // max(block_size, 1))
@@ -306,10 +331,11 @@ def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     context_lens int64 [B] (0 = padding row, output zeros); block_tables
     int32 [B, max_blocks] padded with -1.  scale defaults to 1/sqrt(D) as
     SDPA (model/attention/GQA.py:130).  Returns bf16 [B, Hq, D].
-    ``blocks_per_split`` 0 (the default up to BALANCED_MAX_BATCH sequences)
-    shares the context tiles evenly over a fixed grid; n > 0 splits every
-    context into chunks of n blocks.  Either way the grid depends only on
-    the shapes, so the call can be captured in a HIP graph (pass a
+    ``blocks_per_split`` -1 runs one launch with a workgroup per (sequence,
+    kv-head pair), 0 shares the context tiles evenly over a fixed grid, n > 0
+    splits every context into chunks of n blocks (default_blocks_per_split
+    picks one from the shapes).  Either way the grid depends only on the
+    shapes, so the call can be captured in a HIP graph (pass a
     preallocated ``workspace`` of ``paged_decode_workspace_bytes`` bytes to
     keep the capture free of allocations).  With ``quant`` the merge also quantises each output row
     for the next FP8 linear and the call returns (o, codes e4m3fn

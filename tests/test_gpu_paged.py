@@ -104,11 +104,14 @@ def make_q(case, seed):
                        dtype=torch.bfloat16)
 
 
-def test_paged_decode_cfg3_full():
+@pytest.mark.parametrize("bps", [None, 0, -1])
+def test_paged_decode_cfg3_full(bps):
+    """cfg3 against the float64 oracle: the default split, the balanced
+    split and the single launch (one workgroup per (sequence, kv head))."""
     case = W.paged_case("cfg3", seed=2)
     kc, vc = W.fill_pool(case, seed=2, device=DEV, only_referenced=False)
     q = make_q(case, 2)
-    o = run_decode(case, kc, vc, q)
+    o = run_decode(case, kc, vc, q, bps)
     torch.cuda.synchronize()
     qh, kh, vh, bth = host_inputs(case, kc, vc, q)
     ref = P.paged_decode(qh, kh, vh, case.context_lens, bth, case.scale)
@@ -165,7 +168,7 @@ def test_paged_decode_split_independence():
     case = W.paged_case("cfg3", seed=5, batch=12)
     kc, vc = W.fill_pool(case, seed=5, device=DEV)
     q = make_q(case, 5)
-    outs = [run_decode(case, kc, vc, q, bps).float() for bps in (0, 1, 2, 3, 16)]
+    outs = [run_decode(case, kc, vc, q, bps).float() for bps in (0, 1, 2, 3, 16, -1)]
     for o in outs[1:]:
         assert_close(o.cpu().numpy(), outs[0].cpu().numpy(), "split")
 
@@ -189,16 +192,18 @@ def test_paged_decode_shapes(Hq, Hkv, D, BS):
     vc = torch.randn(NB, BS, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
     q = torch.randn(B, Hq, D, generator=g, device=DEV).to(torch.bfloat16)
     scale = 1 / math.sqrt(D)
-    o = K.paged_attention_decode(q, kc, vc, torch.from_numpy(lens).to(DEV), torch.from_numpy(bt).to(DEV))
-    torch.cuda.synchronize()
     ref = P.paged_decode(q.float().cpu().numpy(), kc.float().cpu().numpy(), vc.float().cpu().numpy(),
                          lens, bt, scale)
-    got = o.float().cpu().numpy()
-    assert_close(got, ref, f"Hq={Hq} Hkv={Hkv} D={D} BS={BS}")
-    assert np.all(got[1] == 0)  # padding row
     G = Hq // Hkv
     v0 = vc[int(bt[0, 0]), 0].float().cpu().numpy()  # L=1 -> v0 of the matching kv head
-    assert_close(got[0], np.repeat(v0, G, axis=0), "L=1")
+    for bps in (None, -1):  # the default split and the single launch
+        o = K.paged_attention_decode(q, kc, vc, torch.from_numpy(lens).to(DEV), torch.from_numpy(bt).to(DEV),
+                                     blocks_per_split=bps)
+        torch.cuda.synchronize()
+        got = o.float().cpu().numpy()
+        assert_close(got, ref, f"Hq={Hq} Hkv={Hkv} D={D} BS={BS} bps={bps}")
+        assert np.all(got[1] == 0)  # padding row
+        assert_close(got[0], np.repeat(v0, G, axis=0), f"L=1 bps={bps}")
 
 
 @pytest.mark.parametrize("Hq,Hkv,D,BS", [(12, 4, 64, 256), (16, 2, 128, 32), (6, 2, 64, 48)])
@@ -222,7 +227,10 @@ def test_paged_decode_fused_quant_equals_act_quant(Hq, Hkv, D, BS):
     vc = torch.randn(NB, BS, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
     q = torch.randn(B, Hq, D, generator=g, device=DEV).to(torch.bfloat16)
     cl, btd = torch.from_numpy(lens).to(DEV), torch.from_numpy(bt).to(DEV)
-    for bps in (0, 1, 2):  # balanced (7 rows over the whole grid), chunks of one and two blocks
+    # balanced (7 rows over the whole grid), chunks of one and two blocks, and
+    # the single launch (its act_quant inside the workgroup: one kv head per
+    # workgroup when G*D is a multiple of 128, else two)
+    for bps in (0, 1, 2, -1):
         o, oq, os_ = K.paged_attention_decode(q, kc, vc, cl, btd, blocks_per_split=bps, quant=True)
         plain = K.paged_attention_decode(q, kc, vc, cl, btd, blocks_per_split=bps)
         assert torch.equal(o, plain)
