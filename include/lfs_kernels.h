@@ -341,7 +341,7 @@ int lfs_add_rmsnorm(const void* x, const void* residual, const float* weight, vo
  * [nparts][T][d], summed in order from 0.f) + bias[t]): the output of
  * lfs_fp8_gemm_splitk_partials followed by the reduction lfs_fp8_gemm_splitk
  * performs, bit for bit, without its launch.  bias: NULL, fp32 [d]
- * (bias_ld 0) or rows bias_ld >= d floats apart.  d % 8 == 0, d <= 1024.
+ * (bias_ld 0) or rows bias_ld >= d floats apart.  d % 8 == 0, d <= 8192.
  */
 int lfs_add_rmsnorm_partials(const float* parts, int32_t nparts, const float* bias, int64_t bias_ld,
                              const void* residual, const float* weight, void* out, void* residual_out, void* q,

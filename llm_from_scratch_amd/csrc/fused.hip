@@ -180,13 +180,13 @@ __global__ __launch_bounds__(128) void add_rmsnorm_kernel(
 
 // add_rmsnorm whose x is the split-K reduction of a GEMM (its partials and
 // bias), so that the reduction needs no launch of its own
-template <bool QUANT>
+template <int CPT, bool QUANT>
 __global__ __launch_bounds__(128) void add_rmsnorm_parts_kernel(
     RowParts rp, const uint16_t* __restrict__ residual, const float* __restrict__ w, uint16_t* __restrict__ out,
     uint16_t* __restrict__ res_out, uint8_t* __restrict__ q, float* __restrict__ qs, int d, float eps) {
   __shared__ float red[2];
-  add_rmsnorm_row<1, QUANT, 2, true>(nullptr, residual, w, out, res_out, q, qs, d, eps, blockIdx.x, red, nullptr,
-                                     rp);
+  add_rmsnorm_row<CPT, QUANT, 2, true>(nullptr, residual, w, out, res_out, q, qs, d, eps, blockIdx.x, red,
+                                       nullptr, rp);
 }
 
 // ----------------------------------------------------- qk_norm_rope_store --
@@ -620,6 +620,18 @@ int launch_add_rmsnorm(bool quant, const void* x, const void* residual, const fl
   return check_launch("add_rmsnorm");
 }
 
+template <int CPT>
+int launch_add_rmsnorm_parts(const RowParts& rp, const void* residual, const float* w, void* out, void* res_out,
+                             void* q, float* qs, int64_t T, int d, float eps, hipStream_t st) {
+  if (q != nullptr)
+    hipLaunchKernelGGL((add_rmsnorm_parts_kernel<CPT, true>), dim3((unsigned)T), dim3(128), 0, st, rp,
+                       (const uint16_t*)residual, w, (uint16_t*)out, (uint16_t*)res_out, (uint8_t*)q, qs, d, eps);
+  else
+    hipLaunchKernelGGL((add_rmsnorm_parts_kernel<CPT, false>), dim3((unsigned)T), dim3(128), 0, st, rp,
+                       (const uint16_t*)residual, w, (uint16_t*)out, (uint16_t*)res_out, (uint8_t*)q, qs, d, eps);
+  return check_launch("add_rmsnorm_partials");
+}
+
 }  // namespace
 }  // namespace lfs
 
@@ -654,7 +666,8 @@ extern "C" int lfs_add_rmsnorm_partials(const float* parts, int32_t nparts, cons
                                         const void* residual, const float* weight, void* out, void* residual_out,
                                         void* q, float* q_scale, int64_t T, int32_t d, float eps, void* stream) {
   LFS_REQUIRE(T >= 0 && d > 0 && nparts >= 1, "add_rmsnorm_partials: bad shape");
-  LFS_REQUIRE(d % 8 == 0 && d <= 128 * 8, "add_rmsnorm_partials: d=%d must be a multiple of 8 and <= 1024", d);
+  LFS_REQUIRE(d % 8 == 0 && d <= 128 * 8 * 8, "add_rmsnorm_partials: d=%d must be a multiple of 8 and <= 8192",
+              d);
   LFS_REQUIRE((residual == nullptr) == (residual_out == nullptr),
               "add_rmsnorm_partials: residual and residual_out go together");
   LFS_REQUIRE((q == nullptr) == (q_scale == nullptr), "add_rmsnorm_partials: q and q_scale go together");
@@ -669,15 +682,11 @@ extern "C" int lfs_add_rmsnorm_partials(const float* parts, int32_t nparts, cons
   LFS_REQUIRE(T < (1ll << 31), "add_rmsnorm_partials: too many rows");
   const RowParts rp{parts, nparts, T * d, bias, bias_ld};
   hipStream_t st = (hipStream_t)stream;
-  if (q != nullptr)
-    hipLaunchKernelGGL((add_rmsnorm_parts_kernel<true>), dim3((unsigned)T), dim3(128), 0, st, rp,
-                       (const uint16_t*)residual, weight, (uint16_t*)out, (uint16_t*)residual_out, (uint8_t*)q,
-                       q_scale, d, eps);
-  else
-    hipLaunchKernelGGL((add_rmsnorm_parts_kernel<false>), dim3((unsigned)T), dim3(128), 0, st, rp,
-                       (const uint16_t*)residual, weight, (uint16_t*)out, (uint16_t*)residual_out, (uint8_t*)q,
-                       q_scale, d, eps);
-  return check_launch("add_rmsnorm_partials");
+  const int cpr = d / 8;
+  if (cpr <= 128) return launch_add_rmsnorm_parts<1>(rp, residual, weight, out, residual_out, q, q_scale, T, d, eps, st);
+  if (cpr <= 256) return launch_add_rmsnorm_parts<2>(rp, residual, weight, out, residual_out, q, q_scale, T, d, eps, st);
+  if (cpr <= 512) return launch_add_rmsnorm_parts<4>(rp, residual, weight, out, residual_out, q, q_scale, T, d, eps, st);
+  return launch_add_rmsnorm_parts<8>(rp, residual, weight, out, residual_out, q, q_scale, T, d, eps, st);
 }
 
 extern "C" int lfs_qk_norm_rope_store(const void* qkv, int64_t ld, const float* q_weight,

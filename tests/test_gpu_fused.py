@@ -205,7 +205,9 @@ def test_add_rmsnorm_route_equals_norm_then_gate(T, d, E, S, top_k, with_res):
 
 
 @pytest.mark.parametrize("T,d,Kd,splits,bias_kind", [(128, 768, 4608, 6, "matrix"), (37, 512, 2048, 3, "vector"),
-                                                    (5, 1024, 1536, 12, None), (64, 256, 3072, 8, "matrix")])
+                                                    (5, 1024, 1536, 12, None), (64, 256, 3072, 8, "matrix"),
+                                                    (32, 2048, 3840, 5, "matrix"), (9, 4096, 2048, 4, "vector"),
+                                                    (3, 8192, 1536, 3, None)])
 def test_add_rmsnorm_partials_equals_reduce_then_norm(T, d, Kd, splits, bias_kind):
     """add & norm over a split-K GEMM's partials (the cfg5 MoE down
     projection feeding the next layer's att_norm) equals the split-K GEMM's

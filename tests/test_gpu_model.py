@@ -42,7 +42,7 @@ from llm_from_scratch_amd.context import reset_context
 from llm_from_scratch_amd.decode_model import DecodeModel, DecodeModelConfig
 from llm_from_scratch_amd.engine import BlockManager, LLMEngine, ModelRunner, SamplingParams, Sequence
 from llm_from_scratch_amd.fp8_linear import FP8Linear
-from llm_from_scratch_amd import workloads
+from llm_from_scratch_amd import kernels, workloads
 from oracle import fp8 as ofp8
 from oracle import model as om
 
@@ -399,6 +399,45 @@ def test_decode_steps_match_full_forward_small(block_size):
             worst[k] = max(worst.get(k, 0.0), v)
     print(f"\nsmall model: e2e rel err max {max(errs):.4f} median {np.median(errs):.4f}; "
           f"per-stage max " + ", ".join(f"{k} {v:.2e}" for k, v in worst.items()))
+
+
+WIDE = DecodeModelConfig(vocab_size=1024, d_model=2048, num_layers=2, num_heads=16, num_kv_heads=4,
+                         d_ff=768, n_routed_experts=4, num_experts_per_tok=2, max_model_length=512)
+
+
+@torch.inference_mode()
+def test_decode_step_wide_model_down_projection_partials(block_size):
+    """d_model 2048, above the 1024 columns a 128-thread row of 8-value
+    chunks covers: at 32 tokens the dense MoE dispatch splits the down
+    projection (K = 5 x 768) over K and hands its fp32 partials to the next
+    layer's att_norm (and the last layer's to the final norm).  Graph replay
+    equals eager, and the logits stay within the end-to-end bound of a full
+    causal forward."""
+    BS = 16
+    Sequence.block_size = BS
+    T = 32
+    model = DecodeModel(WIDE, device="cuda", seed=12)
+    N, Kd = model.layers[0].ffn.w2.weight.shape
+    assert N == 2048 and not kernels.use_skinny_gemm(T, N, Kd)
+    assert kernels.splitk_used(Kd, kernels.default_gemm_splits(T, N, Kd)) >= 2
+    runner = ModelRunner(model, WIDE.runner_config(block_size=BS, num_kv_blocks=1024, max_num_seqs=T))
+    bm = BlockManager(1024, BS)
+    rng = np.random.default_rng(12)
+    seqs = [Sequence(rng.integers(0, WIDE.vocab_size, int(n)).tolist()) for n in rng.integers(20, 300, T)]
+    for s in seqs:
+        bm.allocate(s)
+    _prefill(runner, seqs)
+    for s in seqs:
+        s.append_token(int(rng.integers(0, WIDE.vocab_size)))
+        assert bm.can_append(s)
+        bm.append(s)
+    g = _decode(runner, seqs, eager=False)
+    e = _decode(runner, seqs, eager=True)
+    assert torch.isfinite(g).all()
+    assert (rel_err_rows(g, e) <= 1e-2).all(), "graph vs eager"
+    for i in (0, 5, 17, 31):
+        err = rel_err_rows(g[i], ref_logits(model, seqs[i].token_ids)[-1]).item()
+        assert err <= e2e_tol(WIDE.num_layers), f"seq {i} len {len(seqs[i])} rel err {err:.4f}"
 
 
 GOLDEN = Path(__file__).with_name("golden") / "model_forward.npz"
