@@ -814,7 +814,9 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_big(
 // XCD w % 8 and takes position (w % 8) * (nwg / 8) + w / 8 of each round, so
 // the tiles an XCD runs concurrently are consecutive in the grouped order
 // and share A and B panels in that XCD's L2.
-// Requires N % 256 == 0, M * N * 2 < 2^31, 256 * K < 2^31, nwg % 8 == 0;
+// Requires N % 256 == 0, M * N * 2 < 2^31, ceil(M / 256) * 256 * N * 2 < 2^32
+// (the 32-bit store offsets of padded rows stay past C), 256 * K < 2^31,
+// nwg % 8 == 0;
 // bias: null or an fp32 vector of N (16-byte aligned).
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
@@ -1161,13 +1163,15 @@ bool use_big_tiles(int64_t M, int64_t N, int64_t K) {
 
 // The persistent 256x256 kernel: N a multiple of 256 (its stores write 16-byte
 // row segments and rely on the buffer range for rows only), a vector bias or
-// none, byte offsets of C and of a 256-row panel within 32 bits, and at
-// least half a round of 256x256 tiles (fewer leave most CUs idle; the
-// 128x128 kernel fills them).
+// none, byte offsets of C and of a 256-row panel within 32 bits -- including
+// the padded rows of the last row of tiles, whose 32-bit store offsets must
+// not wrap back into C -- and at least half a round of 256x256 tiles (fewer
+// leave most CUs idle; the 128x128 kernel fills them).
 bool use_persistent(int64_t M, int64_t N, int64_t K, const float* bias, int64_t bias_ld) {
-  const int64_t t = ((M + BIG - 1) / BIG) * (N / BIG);
+  const int64_t tm = (M + BIG - 1) / BIG;
+  const int64_t t = tm * (N / BIG);
   return N % BIG == 0 && bias_ld == 0 && ((uintptr_t)bias & 15u) == 0 && M * N * 2 < (1ll << 31) &&
-         256 * K < (1ll << 31) && K >= 256 && 2 * t >= cu_count();
+         tm * BIG * N * 2 < (1ll << 32) && 256 * K < (1ll << 31) && K >= 256 && 2 * t >= cu_count();
 }
 
 // reduce == false: split-K partials only (ws[s][M][N] fp32, no bias, C not
