@@ -78,6 +78,48 @@ def test_store_kvcache_skips_all_padding():
     assert bool((kc == 1).all()) and bool((vc == 1).all())
 
 
+def test_store_kvcache_cfg4_full_pool_past_2_31_elements():
+    """cfg4's whole 65536-block pool (2^34 bf16 elements per cache): the
+    decode slots of all 256 sequences (most of them past element 2^31), the
+    pool's last slot, -1 padding and one slot past the pool (skipped) are
+    written into NaN-poisoned caches.  The written blocks equal the oracle's
+    store on a compacted copy of those blocks bit for bit, and a reduction on
+    the GPU finds every other element still poisoned."""
+    case = W.paged_case("cfg4", seed=3)
+    NB, BS, Hkv, D = case.num_blocks, case.block_size, case.num_kv_heads, case.head_dim
+    assert NB == 65536 and NB * BS * Hkv * D == 1 << 34
+    slots = np.concatenate([case.slot_mapping, [NB * BS - 1, -1, NB * BS, 5]]).astype(np.int64)
+    T = len(slots)
+    valid = (slots >= 0) & (slots < NB * BS)
+    assert (slots[valid] * Hkv * D >= 1 << 31).sum() > T // 2
+    POISON = -1  # 0xFFFF: a bf16 NaN
+    kc = torch.full((NB, BS, Hkv, D), POISON, dtype=torch.int16, device=DEV).view(torch.bfloat16)
+    vc = torch.full((NB, BS, Hkv, D), POISON, dtype=torch.int16, device=DEV).view(torch.bfloat16)
+    g = torch.Generator(device=DEV).manual_seed(31)
+    key = torch.randn(T, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
+    val = torch.randn(T, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
+    K.store_kvcache(key, val, kc, vc, torch.from_numpy(slots).to(DEV))
+    torch.cuda.synchronize()
+    blocks = np.unique(slots[valid] // BS)
+    remap = {int(b): i for i, b in enumerate(blocks)}
+    local = np.array([remap[int(s_) // BS] * BS + int(s_) % BS if ok else -1 for s_, ok in zip(slots, valid)],
+                     np.int64)
+    k0 = np.full((len(blocks), BS, Hkv, D), POISON, np.int16)
+    v0 = k0.copy()
+    P.store_kvcache(bits(key), bits(val), k0, v0, local)
+    idx = torch.from_numpy(blocks).to(DEV)
+    np.testing.assert_array_equal(kc.view(torch.int16)[idx].cpu().numpy(), k0)
+    np.testing.assert_array_equal(vc.view(torch.int16)[idx].cpu().numpy(), v0)
+    for cache in (kc, vc):  # nothing outside the written slots changed (checked in 8 slices of 4 GiB)
+        rows = cache.view(torch.int16).view(NB * BS, Hkv * D)
+        step = NB * BS // 8
+        hit = np.concatenate([torch.nonzero((rows[i:i + step] != POISON).any(dim=1)).flatten().cpu().numpy() + i
+                              for i in range(0, NB * BS, step)])
+        np.testing.assert_array_equal(hit, np.unique(slots[valid]))
+    del kc, vc
+    torch.cuda.empty_cache()
+
+
 # ------------------------------------------------------------ paged decode --
 def host_inputs(case, kc, vc, q):
     """Copy only the referenced blocks to the host for the oracle."""

@@ -159,6 +159,71 @@ def test_prefill_large_grid_subtiles_vs_torch_fp32(B, L, Hq, Hkv, D):
         worst = max(worst, err.max().item())
 
 
+def _torch_causal_ref(qs, ks, vs, G, D, scale):
+    """Causal attention of one sequence in float32 with torch on the GPU:
+    qs [lq, Hq, D] are the last lq positions of ks / vs [lk, Hkv, D]."""
+    lq, lk = qs.size(0), ks.size(0)
+    qf = qs.float().permute(1, 0, 2).contiguous()                       # [Hq, lq, D]
+    kf = ks.float().repeat_interleave(G, 1).permute(1, 2, 0).contiguous()  # [Hq, D, lk]
+    vf = vs.float().repeat_interleave(G, 1).permute(1, 0, 2).contiguous()  # [Hq, lk, D]
+    s = torch.matmul(qf, kf) * scale
+    pos = torch.arange(lk - lq, lk, device=DEV)[:, None]
+    s = s.masked_fill(torch.arange(lk, device=DEV)[None, :] > pos, float("-inf"))
+    return torch.matmul(torch.softmax(s, -1), vf).permute(1, 0, 2)
+
+
+def test_prefill_large_grid_four_subtiles_d128():
+    """Four 16-query sub-tiles per workgroup at D = 128 and G = 4 (the cfg4
+    heads, 32 / 8): 4 x 4096-token prompts fill every CU eight times with
+    64-query workgroups.  Against causal attention per sequence in float32."""
+    B, L, Hq, Hkv, D = 4, 4096, 32, 8, 128
+    g = torch.Generator(device=DEV).manual_seed(14)
+    q = torch.randn(B * L, Hq, D, generator=g, device=DEV).to(torch.bfloat16)
+    k = torch.randn(B * L, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
+    v = torch.randn(B * L, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
+    cu = torch.arange(0, (B + 1) * L, L, dtype=torch.int32, device=DEV)
+    o = K.flash_attn_varlen_func(q, k, v, cu, cu, L, L)
+    for b in range(B):
+        sl = slice(b * L, (b + 1) * L)
+        ref = _torch_causal_ref(q[sl], k[sl], v[sl], Hq // Hkv, D, D ** -0.5)
+        err = (o[sl].float() - ref).abs()
+        assert bool((err <= ATOL + RTOL * ref.abs()).all()), f"sequence {b}: worst {err.max().item():.4g}"
+
+
+@pytest.mark.parametrize("B,lq,cached,Hq,Hkv,D", [(16, 2048, 1536, 12, 4, 64), (8, 2048, 512, 32, 8, 128)])
+def test_prefill_large_grid_paged_cached_prefix_subtiles(B, lq, cached, Hq, Hkv, D):
+    """The paged kernel (a prefix-cache hit: `cached` keys already in the
+    pool) on a grid large enough for four 16-query sub-tiles per workgroup:
+    block size 256, a randomly permuted pool, -1-padded tables.  Against
+    causal attention per sequence in float32 over the gathered keys."""
+    BS = 256
+    lk = cached + lq
+    rng = np.random.default_rng(B + lq + D)
+    nblk = -(-lk // BS)
+    NB = B * nblk + 3
+    perm = rng.permutation(NB)
+    bt = np.full((B, nblk + 1), -1, np.int32)
+    for b in range(B):
+        bt[b, :nblk] = perm[b * nblk:(b + 1) * nblk]
+    g = torch.Generator(device=DEV).manual_seed(15)
+    kc = torch.randn(NB, BS, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
+    vc = torch.randn(NB, BS, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
+    q = torch.randn(B * lq, Hq, D, generator=g, device=DEV).to(torch.bfloat16)
+    cu_q = torch.arange(0, (B + 1) * lq, lq, dtype=torch.int32, device=DEV)
+    cu_k = torch.arange(0, (B + 1) * lk, lk, dtype=torch.int32, device=DEV)
+    btd = torch.from_numpy(bt).to(DEV)
+    scale = D ** -0.5
+    o = K.flash_attn_varlen_func(q, kc, vc, cu_q, cu_k, lq, lk, scale, block_table=btd)
+    for b in range(B):
+        ids = torch.from_numpy(bt[b, :nblk].astype(np.int64)).to(DEV)
+        ks = kc[ids].reshape(-1, Hkv, D)[:lk]
+        vs = vc[ids].reshape(-1, Hkv, D)[:lk]
+        sl = slice(b * lq, (b + 1) * lq)
+        ref = _torch_causal_ref(q[sl], ks, vs, Hq // Hkv, D, scale)
+        err = (o[sl].float() - ref).abs()
+        assert bool((err <= ATOL + RTOL * ref.abs()).all()), f"sequence {b}: worst {err.max().item():.4g}"
+
+
 def test_prefill_argument_errors():
     q = torch.zeros(4, 8, 64, dtype=torch.bfloat16, device=DEV)
     kv = torch.zeros(4, 2, 64, dtype=torch.bfloat16, device=DEV)

@@ -6,6 +6,11 @@ bit-identical.  Two calls in a row, the second on a smaller batch, check
 that the static array's leftover contents from the first call do not leak
 into the second; a shape whose workspace exceeds the array is rejected.
 """
+import os
+import subprocess
+import sys
+import textwrap
+
 import numpy as np
 import pytest
 import torch
@@ -53,3 +58,43 @@ def test_noalloc_rejects_shape_beyond_scratch():
     bt = torch.zeros(B, 1, dtype=torch.int32, device=DEV)
     with pytest.raises(ValueError, match="static scratch"):
         K.paged_attention_decode_noalloc(q, kc, kc, cl, bt, None, 0)
+
+
+_CAPTURE_CHILD = textwrap.dedent("""
+    import sys, torch
+    sys.path.insert(0, sys.argv[1])
+    from llm_from_scratch_amd import kernels as K
+    from llm_from_scratch_amd import workloads as W
+    case = W.paged_case("cfg3", seed=3, batch=24)
+    kc, vc = W.fill_pool(case, seed=3, device="cuda")
+    g = torch.Generator(device="cuda").manual_seed(10)
+    q = torch.randn(case.batch, case.num_q_heads, case.head_dim, generator=g, device="cuda").to(torch.bfloat16)
+    cl = torch.from_numpy(case.context_lens).to("cuda")
+    bt = torch.from_numpy(case.block_tables).to("cuda")
+    out = torch.empty_like(q)
+    torch.cuda.synchronize()
+    print("child: capturing the process's first noalloc call", flush=True)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        K.paged_attention_decode_noalloc(q, kc, vc, cl, bt, case.scale, 0, out=out)
+    ref = K.paged_attention_decode(q, kc, vc, cl, bt, case.scale, 0)
+    for r in range(2):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"replay {r} differs"
+        _ = (q.float() * 2).sum().item()  # eager work between the replays
+    print("child: OK", flush=True)
+""")
+
+
+def test_noalloc_first_call_under_graph_capture():
+    """In a fresh process the first lfs_paged_decode_noalloc call (and so the
+    first lookup of the static array's device address) happens inside a
+    torch.cuda.graph capture; two replays, with eager work between them, are
+    bit-identical to lfs_paged_decode with a caller-owned workspace."""
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print("noalloc: graph capture in a child process", flush=True)
+    res = subprocess.run([sys.executable, "-c", _CAPTURE_CHILD, repo], capture_output=True, text=True,
+                         timeout=300)
+    assert res.returncode == 0 and "child: OK" in res.stdout, res.stdout[-2000:] + res.stderr[-3000:]
