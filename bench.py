@@ -16,9 +16,10 @@ flushed before every timed call.  ``traffic`` and ``kernel_us`` figures come
 from the rocprofv3 summaries under profiles/, used only when the kernel
 source they were measured on is the one built (sha256 recorded there).
 ``cpu_baseline`` times the CPU restatements on all host cores (1 warm-up,
-median of 5; 3 for cfg4): the numpy oracle's blockwise fp32 GEMM on the
-three M=4096 shapes (the headline ``value``), plus act_quant, paged decode
-(cfg3, a 16-sequence cfg4 subset) and store_kvcache in torch CPU ops.
+median of 5; 3 for cfg4 and cfg5): the numpy oracle's blockwise fp32 GEMM on
+the three M=4096 shapes (the headline ``value``), plus act_quant, paged
+decode (cfg3, a 16-sequence cfg4 subset), store_kvcache, the cfg1 FP8
+linear and the cfg5 decode step (32 of its 128 sequences) in torch CPU ops.
 """
 from __future__ import annotations
 
@@ -547,13 +548,161 @@ def _compact_case(name, seed, nseq=None):
     return case, lens, bt_c, kc, vc, q
 
 
+def _cfg5_cpu_weights(dims, seed):
+    """Random weights of the cfg5 model in the reference's state-dict layout
+    (the names oracle.model reads), fp32 on the host.  Every projection
+    weight is an FP8 weight: random finite e4m3fn codes times one scale per
+    128x128 block (1 / (448 sqrt(fan_in)) times a random factor in [0.5, 1]),
+    decoded exactly and stored transposed for x @ W; biases uniform in
+    +-1/sqrt(fan_in), norms in [0.5, 1.5], the gate bf16-valued, the expert
+    bias in +-0.5."""
+    g = torch.Generator().manual_seed(seed)
+    d, Fd, V, E = dims.d_model, dims.d_ff, dims.vocab_size, dims.n_routed_experts
+    kv = dims.num_kv_heads * dims.head_dim
+    w = {}
+
+    def uni(name, shape, lo, hi):
+        w[name] = lo + (hi - lo) * torch.rand(shape, generator=g)
+
+    def lin(name, n_out, n_in):
+        # random bytes read as e4m3fn codes (the two NaN codes count as 0)
+        codes = torch.empty(n_out * n_in // 4, dtype=torch.int32).random_(generator=g).view(torch.uint8)
+        vals = torch.nan_to_num_(codes.view(torch.float8_e4m3fn).float(), nan=0.0).view(n_out, n_in)
+        sc = (0.5 + 0.5 * torch.rand(-(-n_out // 128), n_in // 128, generator=g)) / (448.0 * math.sqrt(n_in))
+        sc = sc.repeat_interleave(128, 0)[:n_out].repeat_interleave(128, 1)
+        w[name + ".weight"] = (vals * sc).t().contiguous()
+        uni(name + ".bias", (n_out,), -1 / math.sqrt(n_in), 1 / math.sqrt(n_in))
+
+    def mlp(name):
+        lin(name + ".w1", Fd, d)
+        lin(name + ".w3", Fd, d)
+        lin(name + ".w2", d, Fd)
+
+    uni("token_embeddings.weight", (V, d), -math.sqrt(3.0), math.sqrt(3.0))
+    for i in range(dims.num_layers):
+        p = f"layers.{i}."
+        lin(p + "att.q_proj", d, d)
+        lin(p + "att.k_proj", kv, d)
+        lin(p + "att.v_proj", kv, d)
+        lin(p + "att.output_proj", d, d)
+        uni(p + "att.q_norm.weight", (d,), 0.5, 1.5)
+        uni(p + "att.k_norm.weight", (kv,), 0.5, 1.5)
+        for e in range(E):
+            mlp(p + f"ffn.experts.{e}")
+        mlp(p + "ffn.shared_expert")
+        uni(p + "ffn.gate.weight", (E, d), -1 / math.sqrt(d), 1 / math.sqrt(d))
+        w[p + "ffn.gate.weight"] = w[p + "ffn.gate.weight"].to(torch.bfloat16).float()
+        uni(p + "ffn.gate.expert_bias", (E,), -0.5, 0.5)
+        uni(p + "att_norm.weight", (d,), 0.5, 1.5)
+        uni(p + "ffn_norm.weight", (d,), 0.5, 1.5)
+    uni("final_norm.weight", (d,), 0.5, 1.5)
+    lin("lm_head", V, d)
+    return w
+
+
+def _cpu_fp8_linear(w):
+    """The FP8 linear in torch CPU ops: dequant(act_quant(x)) @ dequant(W)^T
+    + b, rounded to bf16 (the product FP8Linear's arithmetic up to fp32
+    summation order)."""
+    def linear(p, x):
+        xq, xs = _cpu_act_quant(x.to(torch.bfloat16))
+        xd = (xq.float().view(x.shape[0], -1, 128) * xs[..., None]).view(x.shape[0], -1)
+        y = xd @ w[p + ".weight"]
+        b = w.get(p + ".bias")
+        return (y if b is None else y + b).to(torch.bfloat16)
+    return linear
+
+
+def _cpu_decode_step_baseline(nseq, runs):
+    """cfg5 decode step on the host: oracle/model.py's decoder block
+    (model/transformer.py:90-118, 162-183) with the FP8-emulating linear,
+    each layer storing the new token's K/V at its slot and attending over the
+    sequence's context in torch CPU fp32 (paged, compacted pool per layer),
+    then final norm, lm_head and Gumbel-max sampling (utils/sampler.py:35-53)
+    -- for the first `nseq` sequences of the GPU line's batch (same length
+    draw), random weights and KV."""
+    from oracle import model as om
+    dims = om.ModelDims(32000, 768, 12, 12, 4, 512, 8, 2, 1)
+    w = _cfg5_cpu_weights(dims, seed=4)
+    BS, Hkv, D, Hq = 256, dims.num_kv_heads, dims.head_dim, dims.num_heads
+    G = Hq // Hkv
+    rng = np.random.default_rng(4)
+    lens = rng.integers(256, 2049, 128)[:nseq]  # the draw of bench_decode_step
+    nblk = -(-lens // BS)
+    total = int(nblk.sum())
+    perm = rng.permutation(total)
+    bt = np.full((nseq, 16), -1, np.int64)
+    off = 0
+    for b in range(nseq):
+        bt[b, :nblk[b]] = perm[off:off + nblk[b]]
+        off += nblk[b]
+    g = torch.Generator().manual_seed(4)
+    shape = (total, BS, Hkv, D)
+    base = torch.randn(shape, generator=g).to(torch.bfloat16)  # every layer's K and V pool starts as a copy
+    pools = [(base.clone(), base.clone()) for _ in range(dims.num_layers)]
+    tokens = torch.from_numpy(rng.integers(0, dims.vocab_size, nseq))
+    pos = torch.from_numpy(lens - 1)
+    slots = torch.from_numpy(bt[np.arange(nseq), (lens - 1) // BS] * BS + (lens - 1) % BS)
+    blocks = [torch.from_numpy(bt[b, :nblk[b]]) for b in range(nseq)]
+    linear = _cpu_fp8_linear(w)
+    scale = 1.0 / math.sqrt(D)
+
+    def step():
+        x = w["token_embeddings.weight"][tokens].to(torch.bfloat16)
+        residual = None
+        for i in range(dims.num_layers):
+            kc, vc = pools[i]
+
+            def attend(q, k, v):
+                kc.view(-1, Hkv, D)[slots] = k
+                vc.view(-1, Hkv, D)[slots] = v
+                o = torch.empty(nseq, Hq, D)
+                for b in range(nseq):
+                    L = int(lens[b])
+                    kb = kc[blocks[b]].reshape(-1, Hkv, D)[:L].float().permute(1, 2, 0)
+                    vb = vc[blocks[b]].reshape(-1, Hkv, D)[:L].float().permute(1, 0, 2)
+                    p = torch.softmax(torch.matmul(q[b].float().view(Hkv, G, D), kb) * scale, dim=-1)
+                    o[b] = torch.matmul(p, vb).reshape(Hq, D)
+                return o.view(nseq, -1)
+            x, residual = om.block(w, i, x, residual, pos, dims, linear, attend)
+        h, _ = om.rms_norm(x, w["final_norm.weight"], dims.rms_eps, residual)
+        probs = torch.softmax(linear("lm_head", h).float(), -1)
+        return (probs / torch.empty_like(probs).exponential_(1).clamp_min(1e-10)).argmax(-1)
+
+    t = _median_time(step, runs)
+    return {"config": "cfg5", "sample": f"first {nseq} of the 128 sequences ({int(lens.sum())} context tokens), "
+                                        f"random weights and KV, median of {runs}",
+            "batch": nseq, "ms": t * 1e3, "tokens/s": nseq / t}
+
+
+def _cpu_cfg1_baseline(runs):
+    """cfg1 FP8 linear on the host: act_quant (torch CPU ops) of x [256, 512]
+    then the numpy oracle's blockwise fp32 fp8_gemm with W [1344, 512]
+    (128x128 scales) -- the latency the GPU line cfg1_linear reports."""
+    from oracle import fp8 as F
+    from llm_from_scratch_amd import workloads as W
+    x = torch.randn(256, 512, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16)
+    b, b_s = F.weight_quant(W.weight(1344, 512, seed=0).float().numpy())
+
+    def fn():
+        xq, xs = _cpu_act_quant(x)
+        return F.fp8_gemm(xq.view(torch.uint8).numpy(), xs.numpy(), b, b_s, accum=np.float32)
+
+    t = _median_time(fn, runs)
+    return {"shape": {"M": 256, "K": 512, "N": 1344}, "us": t * 1e6,
+            "TFLOP/s": 2.0 * 256 * 512 * 1344 / t / 1e12, "runs": runs}
+
+
 def cpu_baseline(device):
     """CPU restatements on all host cores (1 warm-up, median of 5; 3 for
-    cfg4): the headline is the numpy oracle's blockwise fp32 GEMM on the
-    three cfg2 M=4096 shapes; act_quant, paged decode and store_kvcache run
-    the same formulas in torch CPU ops.  The act_quant codes and the decode
-    output are checked against the GPU on the same inputs (bit-exact codes;
-    decode within the 1e-2 / 2e-2 bar)."""
+    cfg4 and the cfg5 step): the headline is the numpy oracle's blockwise
+    fp32 GEMM on the three cfg2 M=4096 shapes; act_quant, paged decode and
+    store_kvcache run the same formulas in torch CPU ops; cfg1 is act_quant
+    plus the oracle's GEMM at 256x512x1344; decode_step is the cfg5 step
+    (oracle/model.py's blocks with FP8-emulating linears, paged attention,
+    lm_head, Gumbel-max) on the first 32 of its 128 sequences.  The act_quant
+    codes and the decode output are checked against the GPU on the same
+    inputs (bit-exact codes; decode within the 1e-2 / 2e-2 bar)."""
     from threadpoolctl import threadpool_limits
     from oracle import fp8 as F
     from llm_from_scratch_amd import kernels as K
@@ -615,6 +764,8 @@ def cpu_baseline(device):
     t = _median_time(store, 5) / 100
     nbytes = 2 * kn.numel() * 2 * 2 + 8 * len(slots)
     out["store_kvcache"] = {"config": "cfg3", "tokens": len(slots), "us": t * 1e6, "GB/s": nbytes / t / 1e9}
+    out["cfg1"] = _cpu_cfg1_baseline(5)
+    out["decode_step"] = _cpu_decode_step_baseline(32, 3)
     out["sample"] = ("GEMM: numpy oracle fp8_gemm (blockwise fp32) on cfg2 M=4096 x 3 (K,N), median of 5; "
                      f"{time.perf_counter() - t_start:.1f} s of CPU baselines in total")
     return out
