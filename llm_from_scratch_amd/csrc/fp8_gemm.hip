@@ -580,6 +580,172 @@ __global__ __launch_bounds__(64 * KW * WGM) void fp8_gemm_skinny(
 }
 
 // ---------------------------------------------------------------------------
+// One-shot GEMM for decode-sized M (<= 16 * MT <= 128).  A workgroup owns all
+// M rows, NC 16-column tiles (n0 = 16 * NC * blockIdx.x) and a range of at
+// most KBM K blocks (blockIdx.y-th split of kps blocks), and copies every
+// operand byte it needs -- the A rows and B rows of its K range -- global ->
+// LDS in one burst before its first MFMA: a call is one memory round trip,
+// its MFMAs and its store, instead of a pipeline that pays a round trip per
+// stage refill.  Waves are WR row groups x WK K groups: wave (rg, kg)
+// multiplies row tiles rg*MT/WR .. +MT/WR-1 by all NC column tiles over the
+// K blocks kg, kg + WK, ... of the range; the WK partial sums of a row group
+// are added through LDS in K-group order.  With one split the result is
+// bf16(sum + bias); with several, the fp32 partial tile goes to
+// ws[split][M][N] (no bias) for a reduction or a consumer that sums them.
+// LDS: K block j of the range holds A (16 * MT rows) then, after all A
+// blocks, B (16 * NC rows), 128-byte rows in the swizzled chunk order of the
+// tile kernels.
+template <int MT, int NC, int KBM, int WR, int WK>
+__global__ __launch_bounds__(64 * WR * WK) void fp8_gemm_flat(
+    const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ B,
+    const float* __restrict__ Bs, const float* __restrict__ bias, int64_t bias_ld, uint16_t* __restrict__ C,
+    float* __restrict__ ws, int M, int N, int K, int kps) {
+  constexpr int NW = WR * WK;
+  constexpr int RT = MT / WR;                  // row tiles per wave
+  constexpr int KW = (KBM + WK - 1) / WK;      // K blocks per wave (at most)
+  constexpr int A_BLK = MT * 16 * BK, B_BLK = NC * 16 * BK;
+  constexpr int SEGS = 2 * (MT + NC);          // 1 KB copies per K block
+  static_assert(MT % WR == 0 && 16 * NC <= 128 && 128 % (16 * NC) == 0, "flat GEMM geometry");
+  static_assert((WK - 1) * WR * RT * NC * 1024 <= KBM * (A_BLK + B_BLK), "K-group sums must fit the LDS");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[KBM * (A_BLK + B_BLK)];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rg = wave / WK, kg = wave % WK;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16 * NC;
+  const int m0 = blockIdx.z * 16 * MT;  // first row of this workgroup's row tiles
+  const int KT = K / BK;
+  const int kb0 = blockIdx.y * kps;
+  const int nkb = min(kps, KT - kb0);  // K blocks of this workgroup (1 .. KBM)
+  const unsigned lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
+
+  // ---- every copy of the workgroup, spread over its waves
+  const int lrow = lane >> 3;
+  for (int i = wave; i < nkb * SEGS; i += NW) {
+    const int j = i / SEGS, seg = i - j * SEGS;
+    const bool isA = seg < 2 * MT;
+    const int r = 8 * (isA ? seg : seg - 2 * MT) + lrow;  // tile row of this lane
+    const int c = (lane & 7) ^ (((r >> 1) & 7) ^ ((r & 1) << 2));
+    const uint8_t* src = isA ? A + (size_t)min(m0 + r, M - 1) * K : B + (size_t)min(n0 + r, N - 1) * K;
+    const unsigned dst = lds0 + (isA ? j * A_BLK + (r - lrow) * BK : KBM * A_BLK + j * B_BLK + (r - lrow) * BK);
+    dma16(src + (size_t)(kb0 + j) * BK + c * 16, dst);
+  }
+  // scales of this wave's rows and K blocks, and the bias vector, in the same round trip
+  float sa[RT][KW], sb[KW];
+#pragma unroll
+  for (int jj = 0; jj < KW; ++jj) {
+    const int j = kg + WK * jj;
+    const int kb = kb0 + min(j, nkb - 1);
+    sb[jj] = Bs[(size_t)(n0 / 128) * KT + kb];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) sa[t][jj] = As[(size_t)min(m0 + 16 * (rg * RT + t) + r16, M - 1) * KT + kb];
+  }
+  float bvec[NC][4];
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int col = n0 + 16 * c + 4 * g + r;
+      bvec[c][r] = (bias != nullptr && bias_ld == 0 && ws == nullptr && col < N) ? bias[col] : 0.f;
+    }
+  wait_vm<0>();
+  __syncthreads();
+
+  v4f acc[RT][NC];
+#pragma unroll
+  for (int t = 0; t < RT; ++t)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc[t][c] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int jj = 0; jj < KW; ++jj) {
+    const int j = kg + WK * jj;
+    if (j >= nkb) break;
+    const uint8_t* at = smem + j * A_BLK;
+    const uint8_t* bt = smem + KBM * A_BLK + j * B_BLK;
+    v8i fb[NC], fa[RT];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) fb[c] = frag(bt, swz(16 * c + r16, g), swz(16 * c + r16, g + 4));
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      const int rt = rg * RT + t;
+      fa[t] = frag(at, swz(16 * rt + r16, g), swz(16 * rt + r16, g + 4));
+    }
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      const float sc = sa[t][jj] * sb[jj];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const v4f p = mfma_fp8(fb[c], fa[t]);  // lane: row 16 rt + r16, columns 16 c + 4 g .. +3
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[t][c][r] = fmaf(p[r], sc, acc[t][c][r]);
+      }
+    }
+  }
+
+  if constexpr (WK > 1) {  // K groups 1 .. WK-1 into group 0, in order, through the operand LDS
+    __syncthreads();
+    v4f* part = reinterpret_cast<v4f*>(smem);  // [WK-1][WR][RT][NC][64]
+    if (kg > 0) {
+#pragma unroll
+      for (int t = 0; t < RT; ++t)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) part[((((kg - 1) * WR + rg) * RT + t) * NC + c) * 64 + lane] = acc[t][c];
+    }
+    __syncthreads();
+    if (kg > 0) return;
+#pragma unroll
+    for (int k2 = 1; k2 < WK; ++k2)
+#pragma unroll
+      for (int t = 0; t < RT; ++t)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const v4f x = part[((((k2 - 1) * WR + rg) * RT + t) * NC + c) * 64 + lane];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[t][c][r] += x[r];
+        }
+  }
+
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const int row = m0 + 16 * (rg * RT + t) + r16;
+    if (row >= M) continue;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int col = n0 + 16 * c + 4 * g;
+      if (ws != nullptr) {
+        float* dst = ws + (size_t)blockIdx.y * M * N + (size_t)row * N + col;
+        if (col + 3 < N && (N & 3) == 0) {
+          *reinterpret_cast<float4*>(dst) = make_float4(acc[t][c][0], acc[t][c][1], acc[t][c][2], acc[t][c][3]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (col + r < N) dst[r] = acc[t][c][r];
+        }
+        continue;
+      }
+      float bv[4] = {bvec[c][0], bvec[c][1], bvec[c][2], bvec[c][3]};
+      if (bias != nullptr && bias_ld != 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (col + r < N) bv[r] = bias[(int64_t)row * bias_ld + col + r];
+      }
+      uint16_t* dst = C + (size_t)row * N + col;
+      if (col + 3 < N && (N & 3) == 0) {
+        uint2 o;
+        o.x = pack_bf16x2(acc[t][c][0] + bv[0], acc[t][c][1] + bv[1]);
+        o.y = pack_bf16x2(acc[t][c][2] + bv[2], acc[t][c][3] + bv[3]);
+        *reinterpret_cast<uint2*>(dst) = o;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (col + r < N) dst[r] = (uint16_t)f32_to_bf16(acc[t][c][r] + bv[r]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // 256x256 tile, 8 waves (2 x 4), 128 x 64 per wave (8 x 4 MFMA tiles).
 //
 // Half the global->LDS bytes per flop of the 128x128 tile and 3/4 of its LDS
@@ -1174,6 +1340,59 @@ bool use_persistent(int64_t M, int64_t N, int64_t K, const float* bias, int64_t 
          tm * BIG * N * 2 < (1ll << 32) && 256 * K < (1ll << 31) && K >= 256 && 2 * t >= cu_count();
 }
 
+// One-shot configurations for 16 < M <= 128 (fp8_gemm_flat<MT, NC, KBM, WR,
+// WK>), picked from the shape alone.  Measured on MI355X, calls back to back
+// in a graph over rotating weight copies, against the 128x128 tile kernel:
+//   FLAT_R32_C16  (2, 1, 8, 2, 2): K <= 1024, ceil(M/32) * ceil(N/16) <= 512
+//                  workgroups -- M = 128, K = 768: N = 1280 4.4 us (6.8),
+//                  N = 768 4.3 us (6.6);
+//   FLAT_R32_C32  (2, 2, 8, 2, 2): K <= 1024 with <= 512 such workgroups --
+//                  M = 128, K = 1024, N = 4096 6.8 us (9.6); also the split
+//                  partials of 8 K blocks each -- M = 128, K = 4608, N = 768
+//                  in 5 splits 6.3 us (6 tile splits 11.5 us; with the
+//                  consumer add_rmsnorm_partials 10.4 against 15.5 us);
+//   FLAT_R128_C64 (8, 4, 6, 4, 2): K <= 768, ceil(N/64) <= 256 workgroups --
+//                  M = 128, K = 768, N = 9216 9.6 us (11.0);
+//   FLAT_R16_C16  (1, 1, 32, 1, 8): K <= 4096, ceil(M/16) * ceil(N/16) <= 512
+//                  -- M = 128, K = 4096, N = 1024 10.2 us (15.5).
+// A workgroup streams its operands at roughly 30 GB/s (a per-CU limit seen
+// in every kernel here), so the smaller the workgroup's operand footprint
+// ((rows + columns) x K bytes) at a grid of one or two rounds, the shorter
+// the call; wider N (lm_head, N = 32000: 18 us against 13 us) stays on the
+// tile kernel.
+enum FlatVariant { FLAT_NONE = -1, FLAT_R32_C16, FLAT_R32_C32, FLAT_R128_C64, FLAT_R16_C16 };
+
+FlatVariant flat_variant(int64_t M, int64_t N, int64_t K, int64_t kps, bool split) {
+  if (M <= 16 || M > 128) return FLAT_NONE;
+  const int64_t kb = K / 128;
+  const int64_t r32 = (M + 31) / 32, c16 = (N + 15) / 16, c32 = (N + 31) / 32;
+  if (split) return kps <= 8 && r32 * c32 * ((kb + kps - 1) / kps) <= 1024 ? FLAT_R32_C32 : FLAT_NONE;
+  if (kb <= 8 && r32 * c16 <= 512) return FLAT_R32_C16;
+  if (kb <= 8 && r32 * c32 <= 512) return FLAT_R32_C32;
+  if (kb <= 6 && (N + 63) / 64 <= 256) return FLAT_R128_C64;
+  if (kb <= 32 && ((M + 15) / 16) * c16 <= 512) return FLAT_R16_C16;
+  return FLAT_NONE;
+}
+
+void launch_flat(FlatVariant v, const void* a, const float* a_s, const void* b, const float* b_s, const float* bias,
+                 int64_t bias_ld, void* c, float* ws, int64_t M, int64_t N, int64_t K, int kps, hipStream_t st) {
+  const int nsplit = (int)((K / 128 + kps - 1) / kps);
+#define LFS_FLAT(MT, NC, KBM, WR, WK)                                                                               \
+  hipLaunchKernelGGL((fp8_gemm_flat<MT, NC, KBM, WR, WK>),                                                           \
+                     dim3((unsigned)((N + 16 * NC - 1) / (16 * NC)), (unsigned)nsplit,                               \
+                          (unsigned)((M + 16 * MT - 1) / (16 * MT))),                                                \
+                     dim3(64 * WR * WK), 0, st, (const uint8_t*)a, a_s, (const uint8_t*)b, b_s, bias, bias_ld,       \
+                     (uint16_t*)c, ws, (int)M, (int)N, (int)K, kps)
+  switch (v) {
+    case FLAT_R32_C16: LFS_FLAT(2, 1, 8, 2, 2); break;
+    case FLAT_R32_C32: LFS_FLAT(2, 2, 8, 2, 2); break;
+    case FLAT_R128_C64: LFS_FLAT(8, 4, 6, 4, 2); break;
+    case FLAT_R16_C16: LFS_FLAT(1, 1, 32, 1, 8); break;
+    default: break;
+  }
+#undef LFS_FLAT
+}
+
 // reduce == false: split-K partials only (ws[s][M][N] fp32, no bias, C not
 // written); at least two K splits must result.
 int fp8_gemm_impl(const void* a, const float* a_s, const void* b, const float* b_s, const float* bias,
@@ -1210,6 +1429,22 @@ int fp8_gemm_impl(const void* a, const float* a_s, const void* b, const float* b
   LFS_REQUIRE(reduce || ws != nullptr, "fp8_gemm_splitk_partials: K=%lld in %d splits gives one split",
               (long long)K, splits);
   hipStream_t st = (hipStream_t)stream;
+  const FlatVariant fv = flat_variant(M, N, K, kps, ws != nullptr);
+  if (fv != FLAT_NONE) {
+    launch_flat(fv, a, a_s, b, b_s, ws != nullptr ? nullptr : bias, bias_ld, c, ws, M, N, K, kps, st);
+    int rc = check_launch("fp8_gemm(flat)");
+    if (rc != 0 || ws == nullptr || !reduce) return rc;
+    if (N % 8 == 0 && ((uintptr_t)c & 15u) == 0 && M * (N / 8) < (1ll << 31) - 256) {
+      const int64_t octs = M * (N / 8);
+      hipLaunchKernelGGL(splitk_reduce8, dim3((unsigned)((octs + 255) / 256)), dim3(256), 0, st, ws, used, bias,
+                         bias_ld, (uint16_t*)c, (int)M, (int)N);
+      return check_launch("fp8_gemm split-K reduce");
+    }
+    const int64_t quads = M * ((N + 3) / 4);
+    hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, st, ws, used, bias,
+                       bias_ld, (uint16_t*)c, M, N);
+    return check_launch("fp8_gemm split-K reduce");
+  }
   if (ws == nullptr && use_persistent(M, N, K, bias, bias_ld)) {
     const int64_t bm = (M + BIG - 1) / BIG, bn = N / BIG;
     const int nwg = (int)std::min<int64_t>(std::max(8, cu_count() / 8 * 8), (bm * bn + 7) / 8 * 8);
@@ -1357,3 +1592,4 @@ extern "C" int lfs_fp8_gemm_skinny(const void* a, const float* a_s, const void* 
 #undef LFS_SK
   return check_launch("fp8_gemm_skinny");
 }
+

@@ -122,22 +122,53 @@ def weight_dequant(x: torch.Tensor, s: torch.Tensor, block_size: int = 128) -> t
     return y
 
 
+def flat_gemm_variant(M: int, N: int, K: int, kps: Optional[int] = None) -> Optional[str]:
+    """The one-shot GEMM fp8_gemm runs for 16 < M <= 128 (None: another
+    kernel).  The same rule as flat_variant in csrc/fp8_gemm.hip: unsplit
+    (``kps`` None) K <= 1024 with <= 512 workgroups of 32 rows x 16 (else 32)
+    columns, K <= 768 with <= 256 workgroups of 128 x 64, K <= 4096 with <=
+    512 workgroups of 16 x 16; split-K partials of at most 8 K blocks each in
+    <= 1024 workgroups of 32 x 32."""
+    if M <= 16 or M > 128:
+        return None
+    kb = K // 128
+    r32, c16, c32 = -(-M // 32), -(-N // 16), -(-N // 32)
+    if kps is not None:
+        return "r32c32" if kps <= 8 and r32 * c32 * -(-kb // kps) <= 1024 else None
+    if kb <= 8 and r32 * c16 <= 512:
+        return "r32c16"
+    if kb <= 8 and r32 * c32 <= 512:
+        return "r32c32"
+    if kb <= 6 and -(-N // 64) <= 256:
+        return "r128c64"
+    if kb <= 32 and -(-M // 16) * c16 <= 512:
+        return "r16c16"
+    return None
+
+
 def default_gemm_splits(M: int, N: int, K: int) -> int:
-    """K splits for fp8_gemm: 1 when the 128x128 output tiles alone give
-    >= 192 workgroups or K has fewer than 12 blocks of 128.  Below that grid
-    each workgroup already runs two K slices, and a call takes about 6.5 us
-    plus 1.1 us per K block of a slice (measured back to back on MI355X at
-    M = 128-512, K 2048 / 4096, N 1536-8192), so splitting pays where it
-    shortens long slices by more than the fp32 partials and their reduction
-    cost: with >= 24 K blocks, max(4, K blocks / 6) splits (K = 4096: 16-22 %
-    faster than unsplit at 12-64 tiles; K = 4608, N = 768 at 6 splits 14.7
-    us); with 12-23 K blocks only for <= 16 tiles (4 splits, 15.4 -> 14.0
+    """K splits for fp8_gemm.  For 16 < M <= 128: 1 when the one-shot
+    kernel covers the whole K (flat_gemm_variant), else blocks of 8 K blocks
+    when its split partials fit (M = 128, K = 4608, N = 768: 5 splits, 6.3 us
+    against 11.5 us for 6 tile-kernel splits).  Otherwise 1 when the 128x128
+    output tiles alone give >= 192 workgroups or K has fewer than 12 blocks
+    of 128.  Below that grid each tile-kernel workgroup already runs two K
+    slices, and a call takes about 6.5 us plus 1.1 us per K block of a slice
+    (measured back to back on MI355X at M = 128-512, K 2048 / 4096, N
+    1536-8192), so splitting pays where it shortens long slices by more than
+    the fp32 partials and their reduction cost: with >= 24 K blocks, max(4,
+    K blocks / 6) splits (K = 4096: 16-22 % faster than unsplit at 12-64
+    tiles); with 12-23 K blocks only for <= 16 tiles (4 splits, 15.4 -> 14.0
     us at M = 128, K = 2048, N = 1536), since from 24 tiles up the unsplit
     call is the fastest (N = 5632: 15.9 us against 18.2 at 2 splits).  At
     most ~256 workgroups and 32 MB of partials (M = 128, K = 4096, N = 8192:
     4 splits 22.0 us, unsplit 25.9)."""
-    tiles = -(-M // 128) * -(-N // 128)
     kt = K // 128
+    if flat_gemm_variant(M, N, K) is not None:
+        return 1
+    if kt > 8 and flat_gemm_variant(M, N, K, kps=8) is not None:
+        return -(-kt // 8)
+    tiles = -(-M // 128) * -(-N // 128)
     if tiles >= 192 or kt < 12:
         return 1
     if kt >= 24:
@@ -154,18 +185,14 @@ SKINNY_MAX_M = 128  # the skinny kernel's row limit
 
 
 def use_skinny_gemm(M: int, N: int, K: int) -> bool:
-    """Decode-sized GEMMs with short K and at most 128 column groups run
-    the skinny kernel.  Measured in the cfg5 decode step (M = 128): QKV
-    (N 1280, K 768) 8.0 vs 12.5 us and the output projection (N 768, K 768)
-    8.0 vs 12.8 us; longer K (the down projection, K 4608: 31.9 vs 16.0 us
-    with split-K) and wide N (w13, N 9216: 15.8 vs 13.1; lm_head, N 32000:
-    30.6 vs 14.6 -- every workgroup re-reads all of A) stay on the tile
-    kernel.  With one 16-row tile (M <= 16) the kernel splits the K blocks
-    over 8 or 16 waves and re-reading A costs little, so any K up to 16384
-    and any N run it (M = 1, K = 4096, N = 1024: split-K tiles 15-16 us)."""
-    if 0 < M <= 16 and K <= 16384:
-        return True
-    return 0 < M <= SKINNY_MAX_M and K <= 1024 and N <= 4096
+    """M <= 16 with K <= 16384 runs the skinny kernel: one 16-row tile, the
+    K blocks split over 8 or 16 waves, and re-reading A costs little (M = 1,
+    K = 4096, N = 1024: 5.0 us; split-K tiles 15-16 us).  Larger decode
+    shapes (16 < M <= 128) run the one-shot kernel of flat_gemm_variant when
+    it applies, which measured faster than the skinny kernel on every cfg5
+    and cfg2 shape at M = 128 (the output projection, N 768 / K 768: 4.3
+    against 6.6 us)."""
+    return 0 < M <= 16 and K <= 16384
 
 
 def fp8_gemm(a: torch.Tensor, a_s: torch.Tensor, b: torch.Tensor, b_s: torch.Tensor,
@@ -179,12 +206,11 @@ def fp8_gemm(a: torch.Tensor, a_s: torch.Tensor, b: torch.Tensor, b_s: torch.Ten
     fp32 accumulator, the bias is added in fp32, and the result is rounded
     once to bf16 [..., N].  ``splits`` > 1 splits the K blocks over that many
     workgroups per output tile (fp32 partials, then one reduction).  By
-    default the shapes ``use_skinny_gemm`` selects -- M <= 16 with K <= 16384
-    and any N, or M <= 128 with K <= 1024 and N <= 4096 -- run the skinny
-    kernel (the K blocks split across the waves of one workgroup per 32
-    output columns, or per 16 when N <= 4096), other shapes that
-    cannot fill the GPU are split, and the rest run the tile kernels;
-    ``splits=1`` forces the tile kernel.
+    default M <= 16 with K <= 16384 runs the skinny kernel (the K blocks
+    split across the waves of one workgroup per 16 or 32 output columns),
+    16 < M <= 128 the one-shot kernel where flat_gemm_variant applies (every
+    operand byte of a workgroup copied to LDS in one burst), other shapes
+    that cannot fill the GPU are split, and the rest run the tile kernels.
     """
     assert a.is_contiguous() and b.is_contiguous(), "Input tensors must be contiguous"
     assert a_s.is_contiguous() and b_s.is_contiguous(), "Scaling factor tensors must be contiguous"

@@ -146,3 +146,20 @@ def test_default_decode_split_rule():
     assert K.default_blocks_per_split(128, 3, 16, 256, cus=256) == 0    # odd Hkv
     assert K.default_blocks_per_split(1024, 4, 16, 256, cus=256) == 0   # more than four rounds
     assert K.default_blocks_per_split(8200, 1, 4, 16, cus=256) > 0      # above the balanced limit
+
+
+def test_decode_gemm_dispatch_rule():
+    """Which GEMM kernel a decode-sized call gets (shapes only): the skinny
+    kernel for M <= 16, the one-shot kernel for the cfg5 step's M = 128
+    projections and the split partials of its down projection, the tile
+    kernel for lm_head's 32000 columns."""
+    from llm_from_scratch_amd import kernels as K
+    assert K.use_skinny_gemm(16, 1024, 4096) and not K.use_skinny_gemm(17, 1024, 4096)
+    assert K.flat_gemm_variant(128, 1280, 768) == "r32c16"     # fused QKV
+    assert K.flat_gemm_variant(128, 768, 768) == "r32c16"      # output projection
+    assert K.flat_gemm_variant(128, 9216, 768) == "r128c64"    # stacked w13
+    assert K.flat_gemm_variant(128, 32000, 768) is None        # lm_head
+    assert K.flat_gemm_variant(128, 768, 4608) is None         # down projection: split instead
+    assert K.default_gemm_splits(128, 768, 4608) == 5
+    assert K.flat_gemm_variant(128, 768, 4608, kps=8) == "r32c32"
+    assert K.default_gemm_splits(128, 9216, 768) == 1

@@ -276,21 +276,61 @@ def test_fp8_gemm_split_k(splits):
         assert np.abs(f32(got) - f32(one)).max() <= 2e-2 + 1e-2 * np.abs(f32(one)).max()
 
 
-@pytest.mark.parametrize("M,N,Kd", [(1, 768, 768), (5, 1282, 128), (17, 250, 384), (33, 96, 1024),
-                                    (100, 4096, 768), (128, 1280, 768), (128, 31, 512),
+def _random_codes(rng, M, N, Kd):
+    """Every e4m3 byte pattern but NaN, distinct scales per block."""
+    ac = rng.integers(0, 256, (M, Kd), dtype=np.uint8)
+    bc = rng.integers(0, 256, (N, Kd), dtype=np.uint8)
+    ac[(ac & 0x7F) == 0x7F] = 0
+    bc[(bc & 0x7F) == 0x7F] = 0
+    a = torch.from_numpy(ac).view(torch.float8_e4m3fn).to(DEV)
+    b = torch.from_numpy(bc).view(torch.float8_e4m3fn).to(DEV)
+    a_s = torch.from_numpy(rng.uniform(1e-3, 1e-2, (M, Kd // 128)).astype(np.float32)).to(DEV)
+    b_s = torch.from_numpy(rng.uniform(1e-3, 1e-2, (-(-N // 128), Kd // 128)).astype(np.float32)).to(DEV)
+    return a, a_s, b, b_s
+
+
+@pytest.mark.parametrize("M,N,Kd,variant", [(17, 250, 384, "r32c16"), (33, 96, 1024, "r32c16"),
+                                            (128, 1280, 768, "r32c16"), (128, 31, 512, "r32c16"),
+                                            (100, 4096, 768, "r32c32"), (128, 4090, 1024, "r32c32"),
+                                            (128, 9216, 768, "r128c64"), (100, 8200, 256, "r128c64"),
+                                            (128, 1024, 4096, "r16c16"), (40, 1000, 1536, "r16c16"),
+                                            (128, 1536, 1536, None), (128, 768, 4608, None)])
+def test_fp8_gemm_flat(M, N, Kd, variant):
+    """The one-shot decode kernel (16 < M <= 128: every operand byte of a
+    workgroup copied to LDS in one burst) in each of its four geometries --
+    32 x 16 and 32 x 32 (row x column) workgroups for K <= 1024, 128 x 64
+    for wide N at K <= 768, 16 x 16 for K <= 4096 -- and as split-K partials
+    of 8 K blocks with the reduction (variant None: K = 1536 in 2 splits,
+    the cfg5 down projection's K = 4608 in 5): ragged M and N (not
+    multiples of 16, 32, 64 or 4), 2 to 36 K blocks, bias vector and per-row
+    bias matrix, against the oracle."""
+    assert K.flat_gemm_variant(M, N, Kd) == variant
+    if variant is None:
+        splits = K.default_gemm_splits(M, N, Kd)
+        assert splits > 1 and K.flat_gemm_variant(M, N, Kd, kps=-(-(Kd // 128) // splits)) == "r32c32"
+    rng = np.random.default_rng(M * 5 + N + Kd)
+    a, a_s, b, b_s = _random_codes(rng, M, N, Kd)
+    bias = torch.from_numpy(rng.standard_normal(N).astype(np.float32)).to(DEV)
+    bm = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32)).to(DEV)
+    for bb, what in ((None, "nobias"), (bias, "bias"), (bm, "bias matrix")):
+        got = K.fp8_gemm(a, a_s, b, b_s, bb)
+        assert_close(f32(got), gemm_oracle(a, a_s, b, b_s, bb), f"flat {M}x{N}x{Kd} {what}")
+
+
+@pytest.mark.parametrize("M,N,Kd", [(1, 768, 768), (5, 1282, 128), (16, 1280, 768), (13, 31, 512),
                                     (1, 1024, 4096), (7, 5632, 2048), (16, 96, 1536), (3, 250, 3072),
                                     (1, 200, 3200), (16, 96, 16384), (16, 1024, 4608), (9, 4096, 1024),
                                     (16, 4097, 2048), (2, 24, 256)])
 def test_fp8_gemm_skinny(M, N, Kd):
-    """The decode-batch kernel (M <= 128, K blocks split over the waves of a
-    workgroup: four, or 8 / 16 for one 16-row tile and 12 / 24+ K blocks;
-    16-column groups for N <= 4096, 32 otherwise):
-    every byte pattern but NaN, distinct scales, ragged M and N (N not a
-    multiple of 16, 32 or 4), 1 to 128 K blocks (fewer than and not a
-    multiple of the waves; K = 16384 the longest K the dispatch sends here,
-    (16, 1024, 4608) the cfg5 down projection at 16 sequences), N on both
-    sides of the 4096 column-group switch, bias vector and per-row bias
-    matrix; against the oracle and the 128 x 128 tile kernel."""
+    """The decode-batch kernel for M <= 16 (K blocks split over the waves of
+    a workgroup: four, or 8 / 16 for 12 / 24+ K blocks; 16-column groups for
+    N <= 4096, 32 otherwise): every byte pattern but NaN, distinct scales,
+    ragged M and N (N not a multiple of 16, 32 or 4), 1 to 128 K blocks
+    (fewer than and not a multiple of the waves; K = 16384 the longest K the
+    dispatch sends here, (16, 1024, 4608) the cfg5 down projection at 16
+    sequences), N on both sides of the 4096 column-group switch, bias vector
+    and per-row bias matrix; against the oracle and the 128 x 128 tile
+    kernel."""
     assert K.use_skinny_gemm(M, N, Kd)
     rng = np.random.default_rng(M * 7 + N + Kd)
     ac = rng.integers(0, 256, (M, Kd), dtype=np.uint8)
@@ -312,10 +352,15 @@ def test_fp8_gemm_skinny(M, N, Kd):
 
 def test_fp8_gemm_skinny_exact_small_integers():
     """Small-integer codes with unit scales: every partial sum is an exact
-    fp32 integer, so the wave-split sum is bit-exact in any order."""
-    rng = np.random.default_rng(22)
-    M, N, Kd = 100, 200, 1024
-    assert K.use_skinny_gemm(M, N, Kd)
+    fp32 integer, so the wave-split sum is bit-exact in any order (the
+    skinny kernel at M = 16, the one-shot kernel at M = 100)."""
+    for M, N, Kd in ((16, 200, 1024), (100, 200, 1024)):
+        _exact_small_integers(M, N, Kd)
+
+
+def _exact_small_integers(M, N, Kd):
+    rng = np.random.default_rng(22 + M)
+    assert K.use_skinny_gemm(M, N, Kd) or K.flat_gemm_variant(M, N, Kd) is not None
     ints = np.arange(-8, 9, dtype=np.float32)
     a = torch.from_numpy(F.e4m3_encode(rng.choice(ints, (M, Kd)))).view(torch.float8_e4m3fn).to(DEV)
     b = torch.from_numpy(F.e4m3_encode(rng.choice(ints, (N, Kd)))).view(torch.float8_e4m3fn).to(DEV)

@@ -402,14 +402,14 @@ def test_decode_steps_match_full_forward_small(block_size):
 
 
 WIDE = DecodeModelConfig(vocab_size=1024, d_model=2048, num_layers=2, num_heads=16, num_kv_heads=4,
-                         d_ff=768, n_routed_experts=4, num_experts_per_tok=2, max_model_length=512)
+                         d_ff=1024, n_routed_experts=4, num_experts_per_tok=2, max_model_length=512)
 
 
 @torch.inference_mode()
 def test_decode_step_wide_model_down_projection_partials(block_size):
     """d_model 2048, above the 1024 columns a 128-thread row of 8-value
     chunks covers: at 32 tokens the dense MoE dispatch splits the down
-    projection (K = 5 x 768) over K and hands its fp32 partials to the next
+    projection (K = 5 x 1024) over K and hands its fp32 partials to the next
     layer's att_norm (and the last layer's to the final norm).  Graph replay
     equals eager, and the logits stay within the end-to-end bound of a full
     causal forward."""
