@@ -400,6 +400,44 @@ def bench_moe(device, reps):
     return out
 
 
+def _probe_lib():
+    """The benchmark's read-ceiling library (llm_from_scratch_amd/csrc/
+    probe.hip, built next to the kernel library), or None if absent."""
+    import ctypes
+    path = os.path.join(REPO, "llm_from_scratch_amd", "liblfs_probe.so")
+    if not os.path.exists(path):
+        return None
+    lib = ctypes.CDLL(path)
+    lib.lfs_probe_read_chunks.restype = ctypes.c_int
+    lib.lfs_probe_read_chunks.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32,
+                                          ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p]
+    return lib
+
+
+def _decode_read_chunks(case, kc, vc, device):
+    """4 KB chunks (absolute address, bytes) of every K and V row the decode
+    reads: per (sequence, block) the block's valid rows, contiguous in the
+    pool (rows of Hkv * D * 2 bytes)."""
+    BS = case.block_size
+    row = case.num_kv_heads * case.head_dim * 2
+    lens = case.context_lens.astype(np.int64)
+    nblk = -(-lens // BS)
+    seq = np.repeat(np.arange(len(lens)), nblk)
+    idx = np.arange(int(nblk.sum())) - np.repeat(np.cumsum(nblk) - nblk, nblk)
+    blk = case.block_tables[seq, idx].astype(np.int64)
+    seg_bytes = np.minimum(BS, lens[seq] - idx * BS) * row
+    seg_off = blk * BS * row
+    nch = -(-seg_bytes // 4096)
+    cseg = np.repeat(np.arange(len(seg_bytes)), nch)
+    cidx = np.arange(int(nch.sum())) - np.repeat(np.cumsum(nch) - nch, nch)
+    off = seg_off[cseg] + cidx * 4096
+    nbytes = np.minimum(4096, seg_bytes[cseg] - cidx * 4096).astype(np.uint32)
+    addr = np.concatenate([kc.data_ptr() + off, vc.data_ptr() + off]).astype(np.uint64)
+    nbytes = np.concatenate([nbytes, nbytes])
+    return (torch.from_numpy(addr.view(np.int64)).to(device), torch.from_numpy(nbytes.view(np.int32)).to(device),
+            int(nbytes.astype(np.int64).sum()))
+
+
 def bench_decode(name, device, reps, flush_buf):
     from llm_from_scratch_amd import kernels as K
     from llm_from_scratch_amd import workloads as W
@@ -422,6 +460,25 @@ def bench_decode(name, device, reps, flush_buf):
            "head_dim": case.head_dim, "tokens": int(case.context_lens.sum()), "us": t * 1e6,
            "GB/s": nbytes / t / 1e9, "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "bytes": nbytes,
            "blocks_per_split": bps}
+    # the read ceiling at this size: the same K / V bytes read once with
+    # nothing computed (liblfs_probe.so), timed the same way
+    probe = _probe_lib()
+    if probe is not None:
+        addr, nb, read_bytes = _decode_read_chunks(case, kc, vc, device)
+        n = addr.numel()
+        groups = max(1024, -(-n // 1024))
+        sink = torch.empty(groups * 256, dtype=torch.float32, device=device)
+
+        def read():
+            rc = probe.lfs_probe_read_chunks(addr.data_ptr(), nb.data_ptr(), n, groups, 16, sink.data_ptr(),
+                                             torch.cuda.current_stream().cuda_stream)
+            assert rc == 0, f"read probe: {rc}"
+
+        read()
+        torch.cuda.synchronize()
+        tr = timed_launches([read], reps, flush=lambda: flush_buf.add_(1))[0]
+        out["read_ceiling"] = {"us": tr * 1e6, "bytes": read_bytes, "GB/s": read_bytes / tr / 1e9,
+                               "frac": read_bytes / tr / 1e9 / HBM_PEAK_GBS, "decode_vs_read": tr / t}
     # split + merge kernel time and fabric bytes of the same call from the
     # rocprofv3 summary (the event window also holds the launch gap)
     prof = profile_figures("paged_decode_cfg3_cfg4.md", "paged_decode_" + name, "paged_kv.hip")

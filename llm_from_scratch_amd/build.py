@@ -22,6 +22,10 @@ REPO = PKG_DIR.parent
 CSRC = PKG_DIR / "csrc"
 LIB_PATH = PKG_DIR / "liblfs_kernels.so"
 SOURCES = ["capi.hip", "quant.hip", "fp8_gemm.hip", "paged_kv.hip", "fused.hip", "prefill.hip", "sampler.hip", "indexer.hip", "moe.hip"]
+# benchmark instrument (the decode's read ceiling), a library of its own that
+# nothing in the package loads: only bench.py does
+PROBE_PATH = PKG_DIR / "liblfs_probe.so"
+PROBE_SOURCES = ["probe.hip"]
 
 HIPCC_FLAGS = [
     "-O3",
@@ -60,20 +64,23 @@ def _run(cmd, verbose):
 
 
 def build(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compile every HIP source into LIB_PATH (always recompiles): one object
-    per source, compiled in parallel, then one shared-library link."""
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+    """Compile every HIP source into LIB_PATH, and the benchmark probe into
+    PROBE_PATH (always recompiles): one object per source, compiled in
+    parallel, then one shared-library link per library."""
     flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    libs = ((LIB_PATH, SOURCES), (PROBE_PATH, PROBE_SOURCES))
     with tempfile.TemporaryDirectory(prefix="lfs_build_") as d:
-        objs = [str(Path(d) / (s.rsplit(".", 1)[0] + ".o")) for s in SOURCES]
+        objs = {lib: [str(Path(d) / (s.rsplit(".", 1)[0] + ".o")) for s in srcs] for lib, srcs in libs}
         cmds = [[hipcc(), *flags, f"-I{REPO / 'include'}", "-c", str(CSRC / s), "-o", o]
-                for s, o in zip(SOURCES, objs)]
+                for lib, srcs in libs for s, o in zip(srcs, objs[lib])]
         n = jobs or max(1, min(len(cmds), os.cpu_count() or 1, 8))
         with ThreadPoolExecutor(max_workers=n) as ex:
             for f in [ex.submit(_run, c, verbose) for c in cmds]:
                 f.result()
-        _run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", str(tmp)], verbose)
-    os.replace(tmp, LIB_PATH)
+        for lib, _ in libs:
+            tmp = lib.with_suffix(".so.tmp")
+            _run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *objs[lib], "-o", str(tmp)], verbose)
+            os.replace(tmp, lib)
     return LIB_PATH
 
 
