@@ -198,7 +198,11 @@ def qkv_heads(q, k, v, qn_w, kn_w, pos, dims: ModelDims, act_dtype):
 
 
 def route(h, gate_weight, expert_bias, top_k):
-    """(indices [T, k], weights [T, k]) of the gate (moe.py:45-90)."""
+    """(indices [T, k], weights [T, k]) of the gate (moe.py:45-90), every
+    step in fp32 -- the build's choice (route_bf16 is the reference's bf16
+    arithmetic; the two pick different experts only on bf16 near-ties, as
+    tests/test_oracle_model.py checks against the reference's own bf16 picks
+    in tests/golden/gate_bf16.npz)."""
     logits = h.float() @ gate_weight.float().t()
     scores = torch.sigmoid(logits)
     idx = torch.topk(logits + expert_bias.float(), top_k, -1).indices
@@ -206,6 +210,23 @@ def route(h, gate_weight, expert_bias, top_k):
     if top_k > 1:
         wts = wts / (wts.sum(-1, keepdim=True) + 1e-10)
     return idx, wts
+
+
+def route_bf16(h, gate_weight, expert_bias, top_k):
+    """The gate as a bf16 TransformerLM runs it (moe.py:45-69): logits = h
+    @ W^T rounded to bf16, sigmoid scores in bf16, the fp32 expert bias cast
+    to bf16 and added in bf16, top-k of those biased logits
+    (torch.topk(sorted=False)), the picked scores renormalised in bf16 by
+    their bf16 sum + 1e-10.  h, gate_weight bf16; returns (indices [T, k],
+    weights bf16 [T, k], biased logits bf16 [T, E])."""
+    logits = h.to(torch.bfloat16) @ gate_weight.to(torch.bfloat16).t()
+    scores = torch.sigmoid(logits)
+    biased = logits + expert_bias.to(logits.dtype).unsqueeze(0)
+    idx = torch.topk(biased, top_k, -1, sorted=False).indices
+    wts = torch.gather(scores, -1, idx)
+    if top_k > 1:
+        wts = wts / (wts.sum(-1, keepdim=True) + 1e-10)
+    return idx, wts, biased
 
 
 def swiglu(a, b):

@@ -240,3 +240,29 @@ def test_add_rmsnorm_partials_equals_reduce_then_norm(T, d, Kd, splits, bias_kin
     torch.cuda.synchronize()
     assert torch.equal(h2, h) and torch.equal(r2, r)
     assert torch.equal(q2.view(torch.uint8), q.view(torch.uint8)) and torch.equal(qs2, qs)
+
+
+def test_moe_route_vs_reference_bf16_gate():
+    """The fp32 GPU gate against the reference's own bf16 Gate
+    (tests/golden/gate_bf16.npz, cfg5 shape: 4096 tokens, 8 experts, top-2):
+    the same picks on every token but bf16 near-ties (the reference's k-th
+    and (k+1)-th biased logits within two bf16 ulps), and on the others the
+    weights within four bf16 roundings of the reference's."""
+    import sys
+    from pathlib import Path
+    sys.path.insert(0, str(Path(__file__).with_name("golden")))
+    from make_gate_golden import TOP_K, gate_inputs
+    from test_oracle_gate import _fixture, _sorted_picks, near_tie_tokens
+    x, w, bias = gate_inputs()
+    ref_biased, ref_idx, ref_wts = _fixture()
+    h = torch.from_numpy(x).to(torch.bfloat16).to(DEV)
+    gw = torch.from_numpy(w).to(torch.bfloat16).to(DEV)
+    eb = torch.from_numpy(bias).to(DEV)
+    _, _, idx, wt = K.moe_route(h, gw, eb, None, TOP_K, 0, dense=False, return_topk=True)
+    torch.cuda.synchronize()
+    pi, pw = _sorted_picks(idx.cpu().numpy(), wt.cpu().numpy())
+    differ = (pi != ref_idx).any(-1)
+    ties = near_tie_tokens(ref_biased, TOP_K)
+    assert not (differ & ~ties).any(), f"{int((differ & ~ties).sum())} tokens differ without a bf16 near-tie"
+    assert differ.sum() <= 0.02 * len(differ)
+    np.testing.assert_allclose(pw[~differ], ref_wts.float().numpy()[~differ], rtol=2 ** -6, atol=0)
