@@ -438,6 +438,41 @@ def _decode_read_chunks(case, kc, vc, device):
             int(nbytes.astype(np.int64).sum()))
 
 
+def bench_read_rate(device, reps, flush_buf):
+    """How fast workgroups of 256 threads stream from HBM as their number
+    grows (the probe of liblfs_probe.so over a plain 512 MB buffer, 256 KB
+    per workgroup, 16 loads of 16 bytes in flight per thread, cache flushed
+    before every call): per-workgroup and whole-chip GB/s at 32 .. 2048
+    workgroups (1/8 .. 8 per CU)."""
+    probe = _probe_lib()
+    if probe is None:
+        return {"error": "liblfs_probe.so not built"}
+    buf = torch.empty(512 << 20, dtype=torch.uint8, device=device)
+    per_group = 256 << 10
+    out = []
+    for groups in (32, 64, 128, 256, 512, 1024, 2048):
+        n = groups * per_group // 4096
+        if n * 4096 > buf.numel():
+            break
+        addr = torch.from_numpy((buf.data_ptr() + np.arange(n, dtype=np.int64) * 4096).view(np.int64)).to(device)
+        nb = torch.full((n,), 4096, dtype=torch.int32, device=device)
+        sink = torch.empty(groups * 256, dtype=torch.float32, device=device)
+
+        def read():
+            rc = probe.lfs_probe_read_chunks(addr.data_ptr(), nb.data_ptr(), n, groups, 16, sink.data_ptr(),
+                                             torch.cuda.current_stream().cuda_stream)
+            assert rc == 0, f"read probe: {rc}"
+
+        read()
+        torch.cuda.synchronize()
+        t = timed_launches([read], reps, flush=lambda: flush_buf.add_(1))[0]
+        out.append({"workgroups": groups, "bytes": n * 4096, "us": t * 1e6, "GB/s": n * 4096 / t / 1e9,
+                    "GB/s per workgroup": per_group / t / 1e9})
+    del buf
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_decode(name, device, reps, flush_buf):
     from llm_from_scratch_amd import kernels as K
     from llm_from_scratch_amd import workloads as W
@@ -841,7 +876,8 @@ def main():
                          "shapes, for context), cfg1 (FP8 linear latency), act_quant (every cfg2 "
                          "shape), gemm_small (cfg2 M <= 128), store_kvcache, cfg3, cfg3_4k, cfg4 (paged "
                          "decode), prefill (varlen prefill attention), indexer (DSA fp8_index), moe (MoE "
-                         "layer, grouped vs dense dispatch), cfg5 (decode step)")
+                         "layer, grouped vs dense dispatch), cfg5 (decode step); not in the default list: "
+                         "read_rate (HBM read rate per workgroup at 32-2048 workgroups)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 4 plain device copies of 256 MiB (a known-traffic kernel for "
                          "scaling FETCH_SIZE / WRITE_SIZE counters)")
@@ -908,7 +944,7 @@ def main():
         out["roofline"]["kernel_us_rocprof"] = gprof.get("kernel_us")
     try:
         decode = [n for n in ("cfg3", "cfg3_4k", "cfg4") if n in extras]
-        flushed = decode or extras & {"act_quant", "gemm_small", "store_kvcache"}
+        flushed = decode or extras & {"act_quant", "gemm_small", "store_kvcache", "read_rate"}
         if flushed:
             flush_buf = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev).zero_()
         if "vendor" in extras:
@@ -926,6 +962,9 @@ def main():
         if "gemm_small" in extras:
             log("bench: fp8_gemm at M <= 128")
             out["gemm_small"] = bench_gemm_small(dev, 20, flush_buf)
+        if "read_rate" in extras:
+            log("bench: HBM read rate per workgroup")
+            out["read_rate"] = bench_read_rate(dev, 10, flush_buf)
         if "store_kvcache" in extras:
             log("bench: store_kvcache")
             out["store_kvcache"] = bench_store_kvcache(dev, 20, flush_buf)
