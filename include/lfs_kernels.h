@@ -148,7 +148,10 @@ int lfs_weight_dequant(const void* w, const float* s, void* y, int64_t N, int64_
  * (a per-row bias matrix, bias_ld >= N) otherwise; bias may be NULL.
  * a: e4m3fn [M, K]; a_s: fp32 [M, K/128]; b: e4m3fn [N, K] (nn.Linear
  * weight layout); b_s: fp32 [ceil(N/128), K/128]; c: bf16 [M, N].
- * All contiguous; K % 128 == 0.
+ * All contiguous; K % 128 == 0.  The kernel follows from the shape: for
+ * 16 < M <= 128 and short K a one-shot kernel (each workgroup copies all
+ * its operands to LDS at once), for large M persistent 256x256 tiles, else
+ * 128x128 tiles; the results differ only in fp32 summation order.
  */
 int lfs_fp8_gemm(const void* a, const float* a_s, const void* b, const float* b_s,
                  const float* bias, int64_t bias_ld, void* c, int64_t M, int64_t N, int64_t K,
@@ -182,9 +185,9 @@ int lfs_fp8_gemm_splitk_partials(const void* a, const float* a_s, const void* b,
 
 /*
  * fp8_gemm for decode-sized batches, M <= 128: the same result as
- * lfs_fp8_gemm up to fp32 summation order (the K blocks are split over the
- * four waves of a workgroup and the partials added through LDS, in wave
- * order).  One workgroup per 32 output columns; no workspace.
+ * lfs_fp8_gemm up to fp32 summation order (the K blocks are split over 4, 8
+ * or 16 waves of a workgroup and the partials added through LDS, in wave
+ * order).  One workgroup per 16 or 32 output columns; no workspace.
  */
 int lfs_fp8_gemm_skinny(const void* a, const float* a_s, const void* b, const float* b_s, const float* bias,
                         int64_t bias_ld, void* c, int64_t M, int64_t N, int64_t K, void* stream);
