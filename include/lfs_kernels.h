@@ -44,6 +44,10 @@
  *                           decode call of the same absent layer; math of
  *                           model/attention/GQA.py:118-130, metadata contract
  *                           engine/model_runner.py:253-278 and :288-312
+ *   lfs_paged_decode_rope   qk_norm_rope_store + the slot write + the
+ *                           single-launch decode of one new token per
+ *                           sequence, fused (GQA.py:80-95 and :118-130,
+ *                           model_runner.py:226-230)
  *   lfs_paged_decode_noalloc  the same decode with a library-owned static
  *                           workspace; no reference counterpart (for callers
  *                           that cannot allocate)
@@ -101,7 +105,7 @@
 extern "C" {
 #endif
 
-#define LFS_ABI_VERSION 13
+#define LFS_ABI_VERSION 14
 
 /* argument errors (negative); launch errors are positive hipError_t values */
 #define LFS_EINVAL (-1)
@@ -244,6 +248,33 @@ int lfs_paged_decode(const void* q, const void* k_cache, const void* v_cache,
                      int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                      int32_t block_size, int64_t num_blocks, int32_t max_blocks, float scale,
                      int32_t blocks_per_split, void* q_out, float* q_scale, void* stream);
+
+/*
+ * The decode step's qk_norm_rope_store followed by lfs_paged_decode with
+ * blocks_per_split -1, in one launch (no counterpart in the reference as one
+ * call: it replaces model/attention/GQA.py:80-95's q/k norms and RoPE, the
+ * KV slot write of engine/model_runner.py:226-230, and the decode attention
+ * of GQA.py:118-130 for one new token per sequence).  For sequence b:
+ * qkv[b] (bf16, row stride ld) is normalised and rotated as
+ * lfs_qk_norm_rope_store does (same bits); its k and v rows are written to
+ * the cache slot slot_mapping[b] (skipped outside [0, num_blocks *
+ * block_size), or when slot_mapping is NULL); the attention then runs over
+ * the context_lens[b] tokens of the sequence, the first L-1 read from the
+ * pool and the newest (position L-1) taken from the row itself, so nothing
+ * written by the call is read back.  out, q_out / q_scale as for
+ * lfs_paged_decode (q_out needs an even num_kv_heads or G*D % 128 == 0);
+ * q_rot (optional, bf16 [B, Hq, D]) receives the rotated q.  Needs
+ * (Hq + Hkv) * D / 16 <= 256 besides lfs_paged_decode's shape limits.  The
+ * results equal the two calls' up to fp32 summation order (the newest token
+ * enters the softmax first).
+ */
+int lfs_paged_decode_rope(const void* qkv, int64_t ld, const float* q_weight, const float* k_weight,
+                          const float* cos_sin, int64_t max_positions, const int64_t* positions,
+                          const int64_t* slot_mapping, float eps, void* q_rot, void* k_cache, void* v_cache,
+                          const int64_t* context_lens, const int32_t* block_tables, int64_t bt_stride,
+                          void* out, int64_t B, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                          int32_t block_size, int64_t num_blocks, int32_t max_blocks, float scale,
+                          void* q_out, float* q_scale, void* stream);
 
 /*
  * lfs_paged_decode without a caller workspace: the split partials live in a

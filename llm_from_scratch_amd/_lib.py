@@ -11,7 +11,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "liblfs_kernels.so"
-ABI_VERSION = 13
+ABI_VERSION = 14
 # size of the library's static paged-decode workspace (LFS_DECODE_SCRATCH_BYTES)
 DECODE_SCRATCH_BYTES = 64 << 20
 
@@ -37,6 +37,9 @@ SIGNATURES = {
     "lfs_paged_decode": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64,
                                         _c_i32, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_f, _c_i32,
                                         _c_p, _c_p, _c_p]),
+    "lfs_paged_decode_rope": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_f, _c_p, _c_p,
+                                             _c_p, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i32, _c_i32, _c_i32,
+                                             _c_i32, _c_i64, _c_i32, _c_f, _c_p, _c_p, _c_p]),
     "lfs_paged_decode_noalloc": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i32, _c_i32,
                                                 _c_i32, _c_i32, _c_i64, _c_i32, _c_f, _c_i32, _c_p, _c_p, _c_p]),
     "lfs_add_rmsnorm": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_f, _c_p]),

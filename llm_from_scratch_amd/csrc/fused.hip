@@ -29,6 +29,7 @@
 // different order than torch's reduction kernels, so their results can differ
 // in the last fp32 bit.
 #include "common.h"
+#include "rope.h"
 
 namespace lfs {
 namespace {
@@ -47,10 +48,6 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   for (int w = 0; w < NW; ++w) t += red[w];
   return t;
 }
-
-__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
-__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
-__device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, b); }
 
 // ------------------------------------------------------------ add_rmsnorm --
 // One workgroup of 128 threads per row; thread c handles 16-byte chunks
@@ -190,47 +187,23 @@ __global__ __launch_bounds__(128) void add_rmsnorm_parts_kernel(
 }
 
 // ----------------------------------------------------- qk_norm_rope_store --
-// One workgroup of 256 threads per token.  A "unit" is one head's pair of
-// 8-element chunks (d0..d0+7, D/2+d0..D/2+d0+7) that RoPE combines; q has
-// Hq*D/16 units, k has Hkv*D/16.  Each thread keeps up to UPT units in
-// registers between the norm reduction and the rotation.
-constexpr int kRopeUPT = 4;
-
+// One workgroup of 256 threads per token (RopeRow: thread t owns the units
+// t, t + 256, ... of q then k).
 __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(
     const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ qw,
     const float* __restrict__ kw, const float* __restrict__ cos_sin, const int64_t* __restrict__ pos,
     const int64_t* __restrict__ slots, uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc,
     uint16_t* __restrict__ vc, int Hq, int Hkv, int D, int64_t num_slots, int64_t max_pos,
     float eps) {
-  __shared__ float red[4];
+  __shared__ float red[8];
   const int64_t t = blockIdx.x;
   const uint16_t* row = qkv + t * ld;
-  const int half = D / 2, upr = D / 16;  // units per head
-  const int uq = Hq * upr, uk = Hkv * upr;
+  const int half = D / 2;
   int64_t p = pos[t];
   p = p < 0 ? 0 : (p >= max_pos ? max_pos - 1 : p);
   const float* cs = cos_sin + p * D;  // [cos(0..D/2) | sin(0..D/2)]
   const int64_t slot = slots != nullptr ? slots[t] : -1;
   const bool store = slot >= 0 && slot < num_slots;
-
-  float a[kRopeUPT][8], b[kRopeUPT][8];
-  float ssq = 0.f, ssk = 0.f;
-#pragma unroll
-  for (int i = 0; i < kRopeUPT; ++i) {
-    const int u = threadIdx.x + 256 * i;
-    if (u < uq + uk) {
-      const bool isq = u < uq;
-      const int uu = isq ? u : u - uq;
-      const int h = uu / upr, d0 = (uu % upr) * 8;
-      const uint16_t* src = row + (isq ? 0 : Hq * D) + h * D;
-      unpack8(*reinterpret_cast<const uint4*>(src + d0), a[i]);
-      unpack8(*reinterpret_cast<const uint4*>(src + half + d0), b[i]);
-      float s = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s = add_rn(s, add_rn(mul_rn(a[i][e], a[i][e]), mul_rn(b[i][e], b[i][e])));
-      if (isq) ssq = add_rn(ssq, s); else ssk = add_rn(ssk, s);
-    }
-  }
   // v: straight copy into the cache slot (Hkv*D/8 chunks)
   if (store) {
     const int64_t dst = slot * (int64_t)Hkv * D;
@@ -238,52 +211,21 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(
       *reinterpret_cast<uint4*>(vc + dst + c * 8) =
           *reinterpret_cast<const uint4*>(row + (Hq + Hkv) * D + c * 8);
   }
-  // two block sums at once
-  ssq = group_sum<64>(ssq);
-  ssk = group_sum<64>(ssk);
-  const int wave = threadIdx.x >> 6;
-  __shared__ float redk[4];
-  if ((threadIdx.x & 63) == 0) { red[wave] = ssq; redk[wave] = ssk; }
-  __syncthreads();
-  const float tq = add_rn(add_rn(red[0], red[1]), add_rn(red[2], red[3]));
-  const float tk = add_rn(add_rn(redk[0], redk[1]), add_rn(redk[2], redk[3]));
-  const float invq = rsqrtf(add_rn(mul_rn(tq, 1.0f / (float)(Hq * D)), eps));
-  const float invk = rsqrtf(add_rn(mul_rn(tk, 1.0f / (float)(Hkv * D)), eps));
-#pragma unroll
-  for (int i = 0; i < kRopeUPT; ++i) {
-    const int u = threadIdx.x + 256 * i;
-    if (u < uq + uk) {
-      const bool isq = u < uq;
-      const int uu = isq ? u : u - uq;
-      const int h = uu / upr, d0 = (uu % upr) * 8;
-      const float* wt = (isq ? qw : kw) + h * D;
-      const float inv = isq ? invq : invk;
-      float y1[8], y2[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        // norm output rounded to bf16 (the norm returns the input dtype)
-        const float x1 = bf16_to_f32(f32_to_bf16(mul_rn(mul_rn(wt[d0 + e], a[i][e]), inv)));
-        const float x2 = bf16_to_f32(f32_to_bf16(mul_rn(mul_rn(wt[half + d0 + e], b[i][e]), inv)));
-        const float c = cs[d0 + e], s = cs[half + d0 + e];
-        y1[e] = sub_rn(mul_rn(x1, c), mul_rn(x2, s));
-        y2[e] = add_rn(mul_rn(x2, c), mul_rn(x1, s));
-      }
-      uint4 o1, o2;
-      o1.x = pack_bf16x2(y1[0], y1[1]); o1.y = pack_bf16x2(y1[2], y1[3]);
-      o1.z = pack_bf16x2(y1[4], y1[5]); o1.w = pack_bf16x2(y1[6], y1[7]);
-      o2.x = pack_bf16x2(y2[0], y2[1]); o2.y = pack_bf16x2(y2[2], y2[3]);
-      o2.z = pack_bf16x2(y2[4], y2[5]); o2.w = pack_bf16x2(y2[6], y2[7]);
-      uint16_t* dst;
-      if (isq) {
-        dst = q_out + (t * Hq + h) * D;
-      } else {
-        if (!store) continue;
-        dst = kc + (slot * Hkv + h) * D;
-      }
-      *reinterpret_cast<uint4*>(dst + d0) = o1;
-      *reinterpret_cast<uint4*>(dst + half + d0) = o2;
+  RopeRow<kRopeUPT> rr;
+  rr.load(row, Hq, Hkv, D, threadIdx.x);
+  rr.load_weights(qw, kw);
+  rr.load_rope(cs);
+  rr.finish(eps, red, [&](bool isq, int h, int d0, const uint4& o1, const uint4& o2) {
+    uint16_t* dst;
+    if (isq) {
+      dst = q_out + (t * Hq + h) * D;
+    } else {
+      if (!store) return;
+      dst = kc + (slot * Hkv + h) * D;
     }
-  }
+    *reinterpret_cast<uint4*>(dst + d0) = o1;
+    *reinterpret_cast<uint4*>(dst + half + d0) = o2;
+  });
 }
 
 // --------------------------------------------------------------- moe_route --

@@ -23,6 +23,7 @@
 //   writes the group's act_quant codes and scale (the output projection's
 //   FP8 input).
 #include "common.h"
+#include "rope.h"
 
 #include <mutex>
 
@@ -168,6 +169,25 @@ struct DecodeWave {
       qa[c] = w;
     }
   }
+  // the same from a [G][D] bf16 block in LDS (this kv head's query rows)
+  __device__ __forceinline__ void load_q_lds(QBuf& qa, const uint16_t* ql) const {
+#pragma unroll
+    for (int c = 0; c < Geo::NDC; ++c) {
+      uint4 w = make_uint4(0, 0, 0, 0);
+      if (j < G) w = *reinterpret_cast<const uint4*>(ql + j * D + c * 32 + kq * 8);
+      qa[c] = w;
+    }
+  }
+  // a tile whose rows are all the one token row k / v (bf16 [D] each, in
+  // LDS): with n = 1 in tile() it adds that single token
+  __device__ __forceinline__ void row_tile(KBuf& ka, VBuf& va, const uint16_t* kl, const uint16_t* vl) const {
+#pragma unroll
+    for (int g16 = 0; g16 < Geo::NG; ++g16)
+#pragma unroll
+      for (int c = 0; c < Geo::NDC; ++c) ka[g16][c] = *reinterpret_cast<const uint4*>(kl + c * 32 + kq * 8);
+#pragma unroll
+    for (int i = 0; i < Geo::UV; ++i) va[i] = *reinterpret_cast<const uint4*>(vl + dc * 8);
+  }
   // Every load is issued unconditionally: rows past the valid count n read
   // row n-1 (row 0 of block 0 for a skipped block), whose scores are masked
   // and whose P is 0 (a skipped block's P.V is not run).  Offsets inside a
@@ -312,13 +332,17 @@ struct DecodeWave {
 // range of consecutive tiles is tstride 1 and every S-th tile from s*tile
 // is t_begin = s*tile, tstride S.  btrow: the sequence's block-table row;
 // block ids at or past id_end are never loaded.  pw: the wave's private
-// LDS slice (T * GP floats).
-template <int D, int G>
+// LDS slice (T * GP floats).  pro() runs once, after the first tile's loads
+// are issued and before anything reads qa (a caller may fill qa there).
+struct NoPrologue {
+  __device__ __forceinline__ void operator()() const {}
+};
+template <int D, int G, class Pro = NoPrologue>
 __device__ __forceinline__ void decode_walk(
     DecodeWave<D, G>& w, const typename DecodeWave<D, G>::QBuf& qa, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ btrow, int BS, int64_t NB, int tile,
     float scale_log2, int kh, int64_t t_begin, int64_t t_end, int tstride, int64_t id_end,
-    float* __restrict__ pw) {
+    float* __restrict__ pw, Pro&& pro = Pro()) {
   using W = DecodeWave<D, G>;
   const int lane = w.lane;
   const int64_t step_rows = (int64_t)tile * tstride;
@@ -326,8 +350,12 @@ __device__ __forceinline__ void decode_walk(
   // The walk's block ids, 256 at a time (window w0 .. w0 + 255 of the table
   // row): lane l holds ids 4l .. 4l+3 of the window, read back with
   // readlane, so no tile waits on a scalar load of its block id.  Ids at or
-  // past id_end are never read (loaded as 0 to stay in bounds).
-  const int64_t blk_first = t_begin / BS;
+  // past id_end are never read (loaded as 0 to stay in bounds).  The window
+  // is (re)loaded only where a group of MAXT tiles starts, and waited for
+  // there: the group's tiles then read ids with no load pending on them, so
+  // the compiler puts no vmcnt(0) between a tile's loads and the next
+  // tile's (which would drain the tile in flight).  A group spans
+  // (MAXT-1)*tstride*tile + tile <= 256*BS rows for tstride <= 36.
   int64_t w0 = -1;
   uint4 ids = make_uint4(0, 0, 0, 0);
   auto load_window = [&](int64_t wb) {
@@ -337,15 +365,14 @@ __device__ __forceinline__ void decode_walk(
 #pragma unroll
     for (int c = 0; c < 4; ++c) v[c] = e + c < id_end ? (uint32_t)btrow[e + c] : 0u;
     ids = make_uint4(v[0], v[1], v[2], v[3]);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
   };
   auto block_id = [&](int64_t bi) -> int32_t {
-    if (bi < w0 || bi >= w0 + 256) load_window(bi);  // walks longer than 256 blocks: next window
-    const int e = (int)(bi - w0);
+    const int e = __builtin_amdgcn_readfirstlane((int)(bi - w0));
     const int src = e >> 2, c = e & 3;
     const uint32_t x = c == 0 ? ids.x : c == 1 ? ids.y : c == 2 ? ids.z : ids.w;
     return (int32_t)__builtin_amdgcn_readlane((int)x, src);
   };
-  load_window(blk_first);
   // tile i of the walk: valid row count (0 for a skipped block) and the
   // element offset of its first row.  Tiles at or past `last` are
   // look-ahead fillers: n = 0 and row 0 of block 0, so their loads all hit
@@ -390,11 +417,17 @@ __device__ __forceinline__ void decode_walk(
   for (int base = 0; base < ntiles; base += MAXT) {
     last = min(ntiles, base + MAXT);
     {
+      const int64_t bf = (t_begin + (int64_t)base * step_rows) / BS;
+      const int64_t bl = (t_begin + (int64_t)(last - 1) * step_rows) / BS;
+      if (base == 0 || __builtin_amdgcn_readfirstlane((int)(bf < w0 || bl >= w0 + 256))) load_window(bf);
+    }
+    {
       int64_t o0;
       tile_at(base, nb0, o0);
       w.load_k(ka0, kc, nb0, o0);
       w.load_v(va0, vc, nb0, o0);
     }
+    if (base == 0) pro();
 #pragma unroll
     for (int u = 0; u < MAXT; u += 2) {
       if (base + u >= last) break;
@@ -580,12 +613,38 @@ __global__ __launch_bounds__(256) void paged_decode_balanced(
 // this pays only when the grid covers every CU and no context is much
 // longer than the rest can hide: the host's default takes it for B * ngrp >=
 // CUs and tables of at most 8192 tokens.
-template <int D, int G, int HG, int NW>
+//
+// ROPE: the decode step's qk_norm_rope_store runs inside the same launch.
+// The workgroup reads the new token's fused qkv row (q | k | v), normalises
+// and rotates q and k with RopeRow (the code qk_norm_rope_store runs, so
+// the same bits), writes the k and v rows of its own kv heads to the cache
+// slot, and keeps its q rows and the new k and v rows in LDS.  The walks
+// stop before the new token (context position L-1); the first walk of each
+// head adds it from LDS before its own tiles, so nothing this launch writes
+// is read back from memory.  The row's loads are issued at the start and
+// the arithmetic runs after the first tile's loads (the walk's prologue
+// hook), so it overlaps the first round trip.
+struct RopeIn {
+  const uint16_t* qkv;
+  int64_t ld;
+  const float* qw;
+  const float* kw;
+  const float* cos_sin;
+  const int64_t* pos;
+  const int64_t* slots;
+  uint16_t* kc;
+  uint16_t* vc;
+  uint16_t* q_out;  // optional copy of the rotated q rows
+  int64_t num_slots, max_pos;
+  float eps;
+};
+
+template <int D, int G, int HG, int NW, bool ROPE>
 __global__ __launch_bounds__(64 * NW) void paged_decode_pairs(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
     const int64_t* __restrict__ ctx_lens, const int32_t* __restrict__ bt, int64_t bt_stride,
     uint16_t* __restrict__ out, uint8_t* __restrict__ qo, float* __restrict__ qs, int Hkv, int BS, int64_t NB,
-    int max_blocks, int tile, float scale_log2, int ngrp) {
+    int max_blocks, int tile, float scale_log2, int ngrp, RopeIn ri) {
   using Geo = DecodeGeom<D>;
   using W = DecodeWave<D, G>;
   constexpr int S = NW / HG;
@@ -594,19 +653,91 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_pairs(
   __shared__ __attribute__((aligned(16))) float part_o[NW][G * D];
   __shared__ float part_m[NW][G], part_l[NW][G];
   __shared__ __attribute__((aligned(16))) uint16_t vals[E];
+  __shared__ __attribute__((aligned(16))) uint16_t new_q[ROPE ? E : 8];           // rotated q rows of the group
+  __shared__ __attribute__((aligned(16))) uint16_t new_kv[ROPE ? 2 * HG * D : 8];  // new token: k rows | v rows
+  __shared__ float red[8];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int hl = wave / S, s = wave - hl * S;
   const int b = blockIdx.x / ngrp, grp = blockIdx.x - b * ngrp;
   const int kh = grp * HG + hl;
   const int Hq = Hkv * G;
-  const int64_t Lc = min(ctx_lens[b], (int64_t)max_blocks * BS);
+  const int64_t L = ctx_lens[b];
+  // with ROPE the walks cover [0, L-1): the new token comes from the qkv row
+  const int64_t Lc = min(ROPE ? L - 1 : L, (int64_t)max_blocks * BS);
+
+  // the RoPE prologue's loads, all issued before the walk (the position's
+  // scalar load returns with the context length's, which the walk waits for
+  // anyway), so that its arithmetic in pro() waits for none of the walk's
+  // loads: issued after the first tile's, they would have to return first
+  constexpr int CPH = D / 8;  // 16-byte chunks per head row
+  const int h0 = grp * HG;    // first kv head of the workgroup
+  RopeRow<1> rr;
+  int64_t slot = -1, p = 0;
+  uint4 vnew = make_uint4(0, 0, 0, 0);
+  const uint16_t* row = nullptr;
+  if constexpr (ROPE) {
+    row = ri.qkv + (int64_t)b * ri.ld;
+    p = ri.pos[b];
+    p = p < 0 ? 0 : (p >= ri.max_pos ? ri.max_pos - 1 : p);
+    slot = ri.slots != nullptr ? ri.slots[b] : -1;
+    rr.load(row, Hq, Hkv, D, threadIdx.x);
+    rr.load_weights(ri.qw, ri.kw);
+    if (threadIdx.x < HG * CPH && h0 + (int)threadIdx.x / CPH < Hkv)
+      vnew = *reinterpret_cast<const uint4*>(row + (int64_t)(Hq + Hkv + h0) * D + threadIdx.x * 8);
+    rr.load_rope(ri.cos_sin + p * D);
+  }
+  bool pro_done = false;
+  auto prologue = [&]() {
+    if constexpr (ROPE) {
+      const bool store = slot >= 0 && slot < ri.num_slots;
+      if (threadIdx.x < HG * CPH && h0 + (int)threadIdx.x / CPH < Hkv) {
+        *reinterpret_cast<uint4*>(&new_kv[HG * D + threadIdx.x * 8]) = vnew;
+        if (store) *reinterpret_cast<uint4*>(ri.vc + (slot * Hkv + h0) * D + threadIdx.x * 8) = vnew;
+      }
+      rr.finish(ri.eps, red,
+                [&](bool isq, int h, int d0, const uint4& o1, const uint4& o2) {
+                  const int hk = isq ? h / G : h;
+                  if (hk < h0 || hk >= h0 + HG) return;  // another workgroup's head
+                  uint16_t* l = isq ? &new_q[(h - h0 * G) * D] : &new_kv[(hk - h0) * D];
+                  *reinterpret_cast<uint4*>(l + d0) = o1;
+                  *reinterpret_cast<uint4*>(l + D / 2 + d0) = o2;
+                  uint16_t* g = nullptr;
+                  if (isq) {
+                    if (ri.q_out != nullptr) g = ri.q_out + ((int64_t)b * Hq + h) * D;
+                  } else if (store) {
+                    g = ri.kc + (slot * Hkv + h) * D;
+                  }
+                  if (g != nullptr) {
+                    *reinterpret_cast<uint4*>(g + d0) = o1;
+                    *reinterpret_cast<uint4*>(g + D / 2 + d0) = o2;
+                  }
+                });
+      __syncthreads();
+    }
+    pro_done = true;
+  };
   if (kh < Hkv) {
     W w(lane, Hkv);
     typename W::QBuf qa;
-    w.load_q(qa, q, b, kh, Hq);
+    auto pro = [&]() {
+      prologue();
+      if constexpr (ROPE) {
+        w.load_q_lds(qa, &new_q[hl * G * D]);
+        // the new token, on the first walk of its head, while the walk's
+        // first tile is still in flight
+        if (s == 0 && L >= 1) {
+          typename W::KBuf ka;
+          typename W::VBuf va;
+          w.row_tile(ka, va, &new_kv[hl * D], &new_kv[(HG + hl) * D]);
+          w.tile(ka, va, qa, 1, scale_log2, p_lds[wave]);
+        }
+      }
+    };
+    if (!ROPE) w.load_q(qa, q, b, kh, Hq);
     if (Lc > (int64_t)s * tile)
       decode_walk<D, G>(w, qa, kc, vc, bt + (int64_t)b * bt_stride, BS, NB, tile, scale_log2, kh,
-                        (int64_t)s * tile, Lc, S, max_blocks, p_lds[wave]);
+                        (int64_t)s * tile, Lc, S, max_blocks, p_lds[wave], pro);
+    if (!pro_done) pro();
     w.reduce_lanes();
     if (w.ts == 0) {
 #pragma unroll
@@ -620,6 +751,8 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_pairs(
       part_m[wave][lane] = w.m_run;
       part_l[wave][lane] = w.l_run;
     }
+  } else {
+    prologue();  // a wave without a head still takes the prologue's barriers
   }
   __syncthreads();
   // log-sum-exp merge of the S walks of each head (L = 0: zeros)
@@ -833,15 +966,15 @@ bool dispatch_balanced(int G, unsigned nwg, dim3 block, hipStream_t st, const ui
 #undef LFS_G
 }
 
-template <int D, int HG, int NW>
+template <int D, int HG, int NW, bool ROPE>
 bool dispatch_pairs_hg(int G, unsigned nwg, hipStream_t st, const uint16_t* q, const uint16_t* kc,
                        const uint16_t* vc, const int64_t* cl, const int32_t* bt, int64_t bts, uint16_t* out,
                        uint8_t* qo, float* qs, int Hkv, int BS, int64_t NB, int max_blocks, int tile, float sl2,
-                       int ngrp) {
-#define LFS_G(GG)                                                                                            \
-  case GG:                                                                                                   \
-    hipLaunchKernelGGL((paged_decode_pairs<D, GG, HG, NW>), dim3(nwg), dim3(64 * NW), 0, st, q, kc, vc, cl,  \
-                       bt, bts, out, qo, qs, Hkv, BS, NB, max_blocks, tile, sl2, ngrp);                      \
+                       int ngrp, const RopeIn& ri) {
+#define LFS_G(GG)                                                                                               \
+  case GG:                                                                                                      \
+    hipLaunchKernelGGL((paged_decode_pairs<D, GG, HG, NW, ROPE>), dim3(nwg), dim3(64 * NW), 0, st, q, kc, vc,  \
+                       cl, bt, bts, out, qo, qs, Hkv, BS, NB, max_blocks, tile, sl2, ngrp, ri);                 \
     return true;
   switch (G) {
     LFS_G(1) LFS_G(2) LFS_G(3) LFS_G(4) LFS_G(5) LFS_G(6) LFS_G(7) LFS_G(8)
@@ -850,15 +983,19 @@ bool dispatch_pairs_hg(int G, unsigned nwg, hipStream_t st, const uint16_t* q, c
 #undef LFS_G
 }
 
-template <int D>
+template <int D, bool ROPE>
 bool dispatch_pairs(int HG, int G, unsigned nwg, hipStream_t st, const uint16_t* q, const uint16_t* kc,
                     const uint16_t* vc, const int64_t* cl, const int32_t* bt, int64_t bts, uint16_t* out,
                     uint8_t* qo, float* qs, int Hkv, int BS, int64_t NB, int max_blocks, int tile, float sl2,
-                    int ngrp) {
-  return HG == 1 ? dispatch_pairs_hg<D, 1, 8>(G, nwg, st, q, kc, vc, cl, bt, bts, out, qo, qs, Hkv, BS, NB,
-                                               max_blocks, tile, sl2, ngrp)
-                 : dispatch_pairs_hg<D, 2, 8>(G, nwg, st, q, kc, vc, cl, bt, bts, out, qo, qs, Hkv, BS, NB,
-                                               max_blocks, tile, sl2, ngrp);
+                    int ngrp, const RopeIn& ri) {
+  // the RoPE prologue runs on 4 waves per workgroup (one per SIMD, so up to
+  // 512 registers a wave): with 8 its registers and the walk's do not fit in
+  // 256 and spill inside the tile loop
+  constexpr int NW = ROPE ? 4 : 8;
+  return HG == 1 ? dispatch_pairs_hg<D, 1, NW, ROPE>(G, nwg, st, q, kc, vc, cl, bt, bts, out, qo, qs, Hkv, BS,
+                                                      NB, max_blocks, tile, sl2, ngrp, ri)
+                 : dispatch_pairs_hg<D, 2, NW, ROPE>(G, nwg, st, q, kc, vc, cl, bt, bts, out, qo, qs, Hkv, BS,
+                                                      NB, max_blocks, tile, sl2, ngrp, ri);
 }
 
 // kv heads per workgroup of the single-launch decode: two when Hkv is even
@@ -1013,13 +1150,16 @@ int paged_decode_impl(const void* q, const void* k_cache, const void* v_cache, c
                 "(Hkv = %d, G*D = %d: needs an even Hkv or G*D a multiple of 128)", Hkv, G * D);
     const int ngrp = (Hkv + HG - 1) / HG;
     LFS_REQUIRE(B * ngrp < (1ll << 31), "paged_decode: too many (sequence, kv head) workgroups");
+    const RopeIn none{};
     const bool ok = D == 64
-        ? dispatch_pairs<64>(HG, G, (unsigned)(B * ngrp), st, (const uint16_t*)q, (const uint16_t*)k_cache,
-                             (const uint16_t*)v_cache, context_lens, block_tables, bt_stride, (uint16_t*)out,
-                             (uint8_t*)q_out, q_scale, Hkv, BS, num_blocks, max_blocks, tile, sl2, ngrp)
-        : dispatch_pairs<128>(HG, G, (unsigned)(B * ngrp), st, (const uint16_t*)q, (const uint16_t*)k_cache,
-                              (const uint16_t*)v_cache, context_lens, block_tables, bt_stride, (uint16_t*)out,
-                              (uint8_t*)q_out, q_scale, Hkv, BS, num_blocks, max_blocks, tile, sl2, ngrp);
+        ? dispatch_pairs<64, false>(HG, G, (unsigned)(B * ngrp), st, (const uint16_t*)q, (const uint16_t*)k_cache,
+                                    (const uint16_t*)v_cache, context_lens, block_tables, bt_stride,
+                                    (uint16_t*)out, (uint8_t*)q_out, q_scale, Hkv, BS, num_blocks, max_blocks,
+                                    tile, sl2, ngrp, none)
+        : dispatch_pairs<128, false>(HG, G, (unsigned)(B * ngrp), st, (const uint16_t*)q,
+                                     (const uint16_t*)k_cache, (const uint16_t*)v_cache, context_lens,
+                                     block_tables, bt_stride, (uint16_t*)out, (uint8_t*)q_out, q_scale, Hkv, BS,
+                                     num_blocks, max_blocks, tile, sl2, ngrp, none);
     LFS_REQUIRE(ok, "paged_decode: unsupported group size %d", G);
     return check_launch("paged_decode(single launch)");
   }
@@ -1135,6 +1275,61 @@ extern "C" int lfs_paged_decode_noalloc(const void* q, const void* k_cache, cons
   return paged_decode_impl(q, k_cache, v_cache, context_lens, block_tables, bt_stride, out, ws,
                            kDecodeScratchBytes, B, num_q_heads, num_kv_heads, head_dim, block_size, num_blocks,
                            max_blocks, scale, blocks_per_split, q_out, q_scale, stream, true);
+}
+
+extern "C" int lfs_paged_decode_rope(const void* qkv, int64_t ld, const float* q_weight, const float* k_weight,
+                                     const float* cos_sin, int64_t max_positions, const int64_t* positions,
+                                     const int64_t* slot_mapping, float eps, void* q_rot, void* k_cache,
+                                     void* v_cache, const int64_t* context_lens, const int32_t* block_tables,
+                                     int64_t bt_stride, void* out, int64_t B, int32_t num_q_heads,
+                                     int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                     int64_t num_blocks, int32_t max_blocks, float scale, void* q_out,
+                                     float* q_scale, void* stream) {
+  const int Hq = num_q_heads, Hkv = num_kv_heads, D = head_dim, BS = block_size;
+  LFS_REQUIRE(B >= 0 && Hq > 0 && Hkv > 0 && BS > 0 && num_blocks >= 0 && max_blocks >= 0,
+              "paged_decode_rope: bad shape");
+  LFS_REQUIRE(D == 64 || D == 128, "paged_decode_rope: head_dim must be 64 or 128 (got %d)", D);
+  LFS_REQUIRE(Hq % Hkv == 0 && Hq / Hkv <= 8,
+              "paged_decode_rope: num_q_heads (%d) must be a multiple of num_kv_heads (%d), ratio <= 8", Hq, Hkv);
+  LFS_REQUIRE(BS % 16 == 0, "paged_decode_rope: block_size must be a multiple of 16 (got %d)", BS);
+  LFS_REQUIRE((Hq + Hkv) * D / 16 <= 256, "paged_decode_rope: (Hq+Hkv)*D/16 must be <= 256 (got %d)",
+              (Hq + Hkv) * D / 16);
+  LFS_REQUIRE(ld >= (int64_t)(Hq + 2 * Hkv) * D && ld % 8 == 0, "paged_decode_rope: bad qkv row stride");
+  LFS_REQUIRE(max_positions > 0, "paged_decode_rope: empty RoPE table");
+  LFS_REQUIRE(bt_stride >= max_blocks, "paged_decode_rope: block table stride < max_blocks");
+  LFS_REQUIRE(num_blocks >= 1 || max_blocks == 0, "paged_decode_rope: empty KV pool");
+  LFS_REQUIRE(B < 65536, "paged_decode_rope: batch too large");
+  if (B == 0) return 0;
+  LFS_REQUIRE(qkv && q_weight && k_weight && cos_sin && positions && k_cache && v_cache && context_lens && out,
+              "paged_decode_rope: null pointer");
+  LFS_REQUIRE(max_blocks == 0 || block_tables, "paged_decode_rope: null block table");
+  LFS_REQUIRE(((((uintptr_t)qkv) | ((uintptr_t)q_weight) | ((uintptr_t)k_weight) | ((uintptr_t)cos_sin) |
+                ((uintptr_t)q_rot) | ((uintptr_t)k_cache) | ((uintptr_t)v_cache) | ((uintptr_t)out)) & 15u) == 0,
+              "paged_decode_rope: qkv, weights, cos_sin, q_rot, caches and out must be 16-byte aligned");
+  LFS_REQUIRE((q_out == nullptr) == (q_scale == nullptr), "paged_decode_rope: q_out and q_scale go together");
+  const int G = Hq / Hkv;
+  const int HG = pairs_heads_per_group(Hkv);
+  LFS_REQUIRE(q_out == nullptr || (HG * G * D) % 128 == 0,
+              "paged_decode_rope: cannot quantise this output (Hkv = %d, G*D = %d: needs an even Hkv or G*D "
+              "a multiple of 128)", Hkv, G * D);
+  const int ngrp = (Hkv + HG - 1) / HG;
+  const int Tmax = D == 64 ? 64 : 32;
+  int tile = 16;
+  for (int t = Tmax; t >= 16; t >>= 1)
+    if (BS % t == 0) { tile = t; break; }
+  const RopeIn ri{(const uint16_t*)qkv, ld, q_weight, k_weight, cos_sin, positions, slot_mapping,
+                  (uint16_t*)k_cache, (uint16_t*)v_cache, (uint16_t*)q_rot, num_blocks * BS, max_positions, eps};
+  const float sl2 = scale * 1.4426950408889634f;
+  hipStream_t st = (hipStream_t)stream;
+  const bool ok = D == 64
+      ? dispatch_pairs<64, true>(HG, G, (unsigned)(B * ngrp), st, nullptr, (const uint16_t*)k_cache,
+                                 (const uint16_t*)v_cache, context_lens, block_tables, bt_stride, (uint16_t*)out,
+                                 (uint8_t*)q_out, q_scale, Hkv, BS, num_blocks, max_blocks, tile, sl2, ngrp, ri)
+      : dispatch_pairs<128, true>(HG, G, (unsigned)(B * ngrp), st, nullptr, (const uint16_t*)k_cache,
+                                  (const uint16_t*)v_cache, context_lens, block_tables, bt_stride, (uint16_t*)out,
+                                  (uint8_t*)q_out, q_scale, Hkv, BS, num_blocks, max_blocks, tile, sl2, ngrp, ri);
+  LFS_REQUIRE(ok, "paged_decode_rope: unsupported group size %d", G);
+  return check_launch("paged_decode_rope");
 }
 
 namespace {

@@ -403,6 +403,81 @@ def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     return (o, oq, os_) if quant else o
 
 
+def paged_attention_decode_rope(qkv: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor,
+                                cos_sin: torch.Tensor, positions: torch.Tensor, num_q_heads: int,
+                                num_kv_heads: int, eps: float, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                                slot_mapping: Optional[torch.Tensor], context_lens: torch.Tensor,
+                                block_tables: torch.Tensor, scale: Optional[float] = None, quant: bool = False,
+                                q_rot: Optional[torch.Tensor] = None):
+    """qk_norm_rope_store then paged_attention_decode(blocks_per_split=-1)
+    for one new token per sequence, in one launch (lfs_paged_decode_rope).
+
+    qkv: bf16 [B, (Hq + 2 Hkv) * D] (rows may be strided), the fused QKV
+    projection of each sequence's newest token; its q and k are normalised
+    and rotated with qk_norm_rope_store's arithmetic (same bits), its k and v
+    written to the caches at slot_mapping (None: no write).  The attention
+    covers context_lens[b] tokens, the newest from the row itself.  Returns
+    what paged_attention_decode returns (with ``quant`` the output's FP8
+    codes and scales too); ``q_rot`` (bf16 [B, Hq, D]) optionally receives
+    the rotated q.  Results equal the unfused pair up to fp32 summation
+    order.  use_fused_decode_rope says whether a shape is supported."""
+    assert qkv.dim() == 2 and qkv.stride(1) == 1
+    B = qkv.size(0)
+    D = cos_sin.size(1)
+    Hq, Hkv = num_q_heads, num_kv_heads
+    assert qkv.size(1) == (Hq + 2 * Hkv) * D, "qkv width mismatch"
+    assert k_cache.is_contiguous() and v_cache.is_contiguous() and k_cache.shape == v_cache.shape
+    assert k_cache.dim() == 4 and k_cache.shape[2:] == (Hkv, D), "caches must be [NB, BS, Hkv, D]"
+    assert block_tables.dim() == 2 and block_tables.stride(1) == 1 and block_tables.size(0) == B
+    assert context_lens.is_contiguous() and context_lens.numel() == B
+    _on_gpu(qkv, q_weight, k_weight, cos_sin, positions, k_cache, v_cache, context_lens, block_tables)
+    _dtype(qkv, torch.bfloat16, "qkv")
+    for t, n in ((k_cache, "k_cache"), (v_cache, "v_cache")):
+        _dtype(t, torch.bfloat16, n)
+    for t, n in ((q_weight, "q_weight"), (k_weight, "k_weight"), (cos_sin, "cos_sin")):
+        _dtype(t, torch.float32, n)
+        assert t.is_contiguous(), f"{n} must be contiguous"
+    assert q_weight.numel() == Hq * D and k_weight.numel() == Hkv * D
+    _dtype(positions, torch.int64, "positions")
+    _dtype(context_lens, torch.int64, "context_lens")
+    _dtype(block_tables, torch.int32, "block_tables")
+    if slot_mapping is not None:
+        _on_gpu(slot_mapping)
+        _dtype(slot_mapping, torch.int64, "slot_mapping")
+        assert slot_mapping.numel() == B and slot_mapping.is_contiguous()
+    NB, BS = k_cache.shape[:2]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    o = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=qkv.device)
+    oq = os_ = None
+    if quant:
+        oq = torch.empty(B, Hq * D, dtype=FP8, device=qkv.device)
+        os_ = torch.empty(B, Hq * D // 128, dtype=torch.float32, device=qkv.device)
+    if q_rot is not None:
+        assert q_rot.shape == (B, Hq, D) and q_rot.dtype == torch.bfloat16 and q_rot.is_contiguous()
+    rc = _lib.load().lfs_paged_decode_rope(
+        _ptr(qkv), qkv.stride(0), _ptr(q_weight), _ptr(k_weight), _ptr(cos_sin), cos_sin.size(0),
+        _ptr(positions), _ptr(slot_mapping), float(eps), _ptr(q_rot), _ptr(k_cache), _ptr(v_cache),
+        _ptr(context_lens), _ptr(block_tables), block_tables.stride(0), _ptr(o), B, Hq, Hkv, D, BS, NB,
+        block_tables.size(1), float(scale), _ptr(oq), _ptr(os_), _stream(qkv))
+    _lib.check(rc, "paged_attention_decode_rope")
+    return (o, oq, os_) if quant else o
+
+
+def use_fused_decode_rope(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, max_blocks: int,
+                          block_size: int, quant: bool = True) -> bool:
+    """Whether the decode step runs paged_attention_decode_rope: when the
+    default split is the single launch (default_blocks_per_split -1) and
+    the shape fits the fused prologue ((Hq + Hkv) * D / 16 <= 256; with the
+    quantised output an even Hkv or G * D % 128 == 0)."""
+    if default_blocks_per_split(batch, num_kv_heads, max_blocks, block_size) != -1:
+        return False
+    if head_dim not in (64, 128) or (num_q_heads + num_kv_heads) * head_dim // 16 > 256:
+        return False
+    G = num_q_heads // num_kv_heads
+    return not quant or num_kv_heads % 2 == 0 or (G * head_dim) % 128 == 0
+
+
 def paged_attention_decode_noalloc(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                                    context_lens: torch.Tensor, block_tables: torch.Tensor,
                                    scale: Optional[float] = None, blocks_per_split: Optional[int] = None,

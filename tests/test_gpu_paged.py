@@ -282,6 +282,87 @@ def test_paged_decode_fused_quant_equals_act_quant(Hq, Hkv, D, BS):
         assert bool((o[1] == 0).all())  # padding row
 
 
+def _rope_table(D, max_pos=4096):
+    inv = 1.0 / (10000.0 ** (torch.arange(0, D, 2, device=DEV).float() / D))
+    ang = torch.outer(torch.arange(max_pos, device=DEV).float(), inv)
+    return torch.cat([ang.cos(), ang.sin()], -1).contiguous()
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,BS,B", [(12, 4, 64, 256, 128), (16, 4, 64, 256, 64), (6, 3, 64, 48, 20),
+                                           (16, 2, 128, 32, 16), (8, 8, 128, 16, 9)])
+def test_paged_decode_rope_equals_store_then_decode(Hq, Hkv, D, BS, B):
+    """paged_attention_decode_rope (q/k norms, RoPE, slot write and the
+    single-launch decode in one kernel) against qk_norm_rope_store followed
+    by paged_attention_decode(-1, quant): the rotated q and the whole K/V
+    pools bit-identical, the output within the file's bar of the unfused
+    output and of the float64 oracle (the newest token enters the softmax in
+    another order), the output's FP8 codes equal act_quant of its bf16
+    output.  Rows: L = 1 (only the new token), a padding row (L = 0, slot
+    -1), block-boundary lengths and random ones up to 4 blocks."""
+    rng = np.random.default_rng(Hq * 100 + D + B)
+    lens = rng.integers(1, 4 * BS + 1, B).astype(np.int64)
+    lens[:5] = [1, 0, BS, BS + 1, 2 * BS]
+    nblk = -(-lens // BS)
+    NB = int(nblk.sum()) + 8
+    maxb = int(nblk.max()) + 1
+    perm = rng.permutation(NB)
+    bt = np.full((B, maxb), -1, np.int32)
+    off = 0
+    for b in range(B):
+        bt[b, :nblk[b]] = perm[off:off + nblk[b]]
+        off += int(nblk[b])
+    slots = np.where(lens > 0, bt[np.arange(B), np.maximum(lens - 1, 0) // BS].astype(np.int64) * BS
+                     + (np.maximum(lens - 1, 0) % BS), -1)
+    g = torch.Generator(device=DEV).manual_seed(B + D)
+    kc = torch.randn(NB, BS, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
+    vc = torch.randn(NB, BS, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
+    width = (Hq + 2 * Hkv) * D
+    qkv = torch.randn(B, width + 8, generator=g, device=DEV).to(torch.bfloat16)[:, :width]  # strided rows
+    qw = torch.rand(Hq * D, generator=g, device=DEV) + 0.5
+    kw = torch.rand(Hkv * D, generator=g, device=DEV) + 0.5
+    cos_sin = _rope_table(D)
+    pos = torch.from_numpy(np.maximum(lens - 1, 0)).to(DEV)
+    eps = torch.finfo(torch.float32).eps
+    cl, btd, sl = (torch.from_numpy(x).to(DEV) for x in (lens, bt, slots))
+    scale = 1 / math.sqrt(D)
+    print(f"rope decode: Hq {Hq} Hkv {Hkv} D {D} BS {BS} B {B}", flush=True)
+    kc_a, vc_a = kc.clone(), vc.clone()
+    q = K.qk_norm_rope_store(qkv, qw, kw, cos_sin, pos, Hq, Hkv, eps, kc_a, vc_a, sl)
+    o_a, _, _ = K.paged_attention_decode(q, kc_a, vc_a, cl, btd, scale, -1, quant=True)
+    q_b = torch.empty_like(q)
+    o_b, oq_b, os_b = K.paged_attention_decode_rope(qkv, qw, kw, cos_sin, pos, Hq, Hkv, eps, kc, vc, sl, cl, btd,
+                                                    scale, quant=True, q_rot=q_b)
+    torch.cuda.synchronize()
+    assert torch.equal(q_b.view(torch.int16), q.view(torch.int16)), "rotated q differs"
+    assert torch.equal(kc.view(torch.int16), kc_a.view(torch.int16)), "K pool differs"
+    assert torch.equal(vc.view(torch.int16), vc_a.view(torch.int16)), "V pool differs"
+    got = o_b.float().cpu().numpy()
+    assert_close(got, o_a.float().cpu().numpy(), "fused vs unfused")
+    ref = P.paged_decode(q.float().cpu().numpy(), kc_a.float().cpu().numpy(), vc_a.float().cpu().numpy(),
+                         lens, bt, scale)
+    assert_close(got, ref, "fused vs oracle")
+    assert np.all(got[1] == 0)  # padding row
+    rq, rs = K.act_quant(o_b.view(B, -1))
+    assert torch.equal(oq_b.view(torch.uint8), rq.view(torch.uint8)) and torch.equal(os_b, rs)
+    # and without the quantised output or the q copy
+    o_c = K.paged_attention_decode_rope(qkv, qw, kw, cos_sin, pos, Hq, Hkv, eps, kc, vc, sl, cl, btd, scale)
+    assert torch.equal(o_c, o_b)
+
+
+def test_paged_decode_rope_rejects_bad_shapes():
+    """The fused prologue holds one q/k unit per thread: (Hq + Hkv) * D / 16
+    above 256 is refused (use_fused_decode_rope says no for it)."""
+    B, Hq, Hkv, D, BS = 2, 32, 8, 128, 16
+    assert not K.use_fused_decode_rope(256, Hq, Hkv, D, 4, BS)
+    qkv = torch.zeros(B, (Hq + 2 * Hkv) * D, device=DEV, dtype=torch.bfloat16)
+    kc = torch.zeros(4, BS, Hkv, D, device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="must be <= 256"):
+        K.paged_attention_decode_rope(qkv, torch.ones(Hq * D, device=DEV), torch.ones(Hkv * D, device=DEV),
+                                      _rope_table(D), torch.zeros(B, dtype=torch.int64, device=DEV), Hq, Hkv,
+                                      1e-6, kc, kc.clone(), None, torch.ones(B, dtype=torch.int64, device=DEV),
+                                      torch.zeros(B, 1, dtype=torch.int32, device=DEV))
+
+
 def _short_sequences(B, BS, max_len, seed):
     rng = np.random.default_rng(seed)
     lens = rng.integers(0, max_len + 1, B).astype(np.int64)
