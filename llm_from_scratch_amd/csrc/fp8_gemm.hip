@@ -619,7 +619,10 @@ __global__ __launch_bounds__(64 * WR * WK) void fp8_gemm_flat(
   constexpr int KW = (KBM + WK - 1) / WK;      // K blocks per wave (at most)
   constexpr int A_BLK = MT * 16 * BK, B_BLK = NC * 16 * BK;
   constexpr int SEGS = 2 * (MT + NC);          // 1 KB copies per K block
-  static_assert(MT % WR == 0 && 16 * NC <= 128 && 128 % (16 * NC) == 0, "flat GEMM geometry");
+  static_assert(MT % WR == 0 && NC <= 8, "flat GEMM geometry");
+  // 128-column weight-scale blocks the workgroup's columns touch: one when
+  // 16*NC divides 128 (n0 is then a multiple of 16*NC inside one block)
+  constexpr bool ONE_SB = 128 % (16 * NC) == 0;
   static_assert((WK - 1) * WR * RT * NC * 1024 <= KBM * (A_BLK + B_BLK), "K-group sums must fit the LDS");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[KBM * (A_BLK + B_BLK)];
 
@@ -646,12 +649,14 @@ __global__ __launch_bounds__(64 * WR * WK) void fp8_gemm_flat(
     dma16(src + (size_t)(kb0 + j) * BK + c * 16, dst);
   }
   // scales of this wave's rows and K blocks, and the bias vector, in the same round trip
-  float sa[RT][KW], sb[KW];
+  constexpr int NSB = ONE_SB ? 1 : NC;  // weight scales per K block: per column tile unless one block
+  float sa[RT][KW], sb[NSB][KW];
 #pragma unroll
   for (int jj = 0; jj < KW; ++jj) {
     const int j = kg + WK * jj;
     const int kb = kb0 + min(j, nkb - 1);
-    sb[jj] = Bs[(size_t)(n0 / 128) * KT + kb];
+#pragma unroll
+    for (int c = 0; c < NSB; ++c) sb[c][jj] = Bs[(size_t)(min(n0 + 16 * c, N - 1) / 128) * KT + kb];
 #pragma unroll
     for (int t = 0; t < RT; ++t) sa[t][jj] = As[(size_t)min(m0 + 16 * (rg * RT + t) + r16, M - 1) * KT + kb];
   }
@@ -687,9 +692,9 @@ __global__ __launch_bounds__(64 * WR * WK) void fp8_gemm_flat(
     }
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
-      const float sc = sa[t][jj] * sb[jj];
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
+        const float sc = sa[t][jj] * sb[ONE_SB ? 0 : c][jj];
         const v4f p = mfma_fp8(fb[c], fa[t]);  // lane: row 16 rt + r16, columns 16 c + 4 g .. +3
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[t][c][r] = fmaf(p[r], sc, acc[t][c][r]);
@@ -1357,16 +1362,18 @@ bool use_persistent(int64_t M, int64_t N, int64_t K, const float* bias, int64_t 
 // One-shot configurations for 16 < M <= 128 (fp8_gemm_flat<MT, NC, KBM, WR,
 // WK>), picked from the shape alone.  Measured on MI355X, calls back to back
 // in a graph over rotating weight copies, against the 128x128 tile kernel:
-//   FLAT_R32_C16  (2, 1, 8, 2, 2): K <= 1024, ceil(M/32) * ceil(N/16) <= 512
-//                  workgroups -- M = 128, K = 768: N = 1280 4.4 us (6.8),
-//                  N = 768 4.3 us (6.6);
+//   FLAT_R32_C16  (2, 1, 8, 2, 4): K <= 1024, ceil(M/32) * ceil(N/16) <= 512
+//                  workgroups -- M = 128, K = 768: N = 1280 4.3 us (6.8),
+//                  N = 768 3.9 us (6.6) (4.4 / 4.1 us with two K groups);
 //   FLAT_R32_C32  (2, 2, 8, 2, 2): K <= 1024 with <= 512 such workgroups --
-//                  M = 128, K = 1024, N = 4096 6.8 us (9.6); also the split
-//                  partials of 8 K blocks each -- M = 128, K = 4608, N = 768
-//                  in 5 splits 6.3 us (6 tile splits 11.5 us; with the
-//                  consumer add_rmsnorm_partials 10.4 against 15.5 us);
-//   FLAT_R128_C64 (8, 4, 6, 4, 2): K <= 768, ceil(N/64) <= 256 workgroups --
-//                  M = 128, K = 768, N = 9216 9.6 us (11.0);
+//                  M = 128, K = 1024, N = 4096 6.8 us (9.6);
+//   FLAT_S32_C32  (2, 2, 8, 2, 4): the split partials of at most 8 K blocks
+//                  each -- M = 128, K = 4608, N = 768 in 5 splits 5.7 us
+//                  (6.4 us with two K groups, 6 tile splits 11.5 us);
+//   FLAT_R128_C48 (8, 3, 6, 8, 1): K <= 768, ceil(N/48) <= 256 workgroups --
+//                  M = 128, K = 768, N = 9216 8.1 us (r128c64 9.5, r64c96
+//                  8.9, r64c64 11.7; tile kernel 11.0);
+//   FLAT_R128_C64 (8, 4, 6, 4, 2): K <= 768, ceil(N/64) <= 256 workgroups;
 //   FLAT_R16_C16  (1, 1, 32, 1, 8): K <= 4096, ceil(M/16) * ceil(N/16) <= 512
 //                  -- M = 128, K = 4096, N = 1024 10.2 us (15.5).
 // A workgroup streams its operands at roughly 30 GB/s (a per-CU limit seen
@@ -1374,15 +1381,16 @@ bool use_persistent(int64_t M, int64_t N, int64_t K, const float* bias, int64_t 
 // ((rows + columns) x K bytes) at a grid of one or two rounds, the shorter
 // the call; wider N (lm_head, N = 32000: 18 us against 13 us) stays on the
 // tile kernel.
-enum FlatVariant { FLAT_NONE = -1, FLAT_R32_C16, FLAT_R32_C32, FLAT_R128_C64, FLAT_R16_C16 };
+enum FlatVariant { FLAT_NONE = -1, FLAT_R32_C16, FLAT_R32_C32, FLAT_S32_C32, FLAT_R128_C48, FLAT_R128_C64, FLAT_R16_C16 };
 
 FlatVariant flat_variant(int64_t M, int64_t N, int64_t K, int64_t kps, bool split) {
   if (M <= 16 || M > 128) return FLAT_NONE;
   const int64_t kb = K / 128;
   const int64_t r32 = (M + 31) / 32, c16 = (N + 15) / 16, c32 = (N + 31) / 32;
-  if (split) return kps <= 8 && r32 * c32 * ((kb + kps - 1) / kps) <= 1024 ? FLAT_R32_C32 : FLAT_NONE;
+  if (split) return kps <= 8 && r32 * c32 * ((kb + kps - 1) / kps) <= 1024 ? FLAT_S32_C32 : FLAT_NONE;
   if (kb <= 8 && r32 * c16 <= 512) return FLAT_R32_C16;
   if (kb <= 8 && r32 * c32 <= 512) return FLAT_R32_C32;
+  if (kb <= 6 && (N + 47) / 48 <= 256) return FLAT_R128_C48;
   if (kb <= 6 && (N + 63) / 64 <= 256) return FLAT_R128_C64;
   if (kb <= 32 && ((M + 15) / 16) * c16 <= 512) return FLAT_R16_C16;
   return FLAT_NONE;
@@ -1398,8 +1406,10 @@ void launch_flat(FlatVariant v, const void* a, const float* a_s, const void* b, 
                      dim3(64 * WR * WK), 0, st, (const uint8_t*)a, a_s, (const uint8_t*)b, b_s, bias, bias_ld,       \
                      (uint16_t*)c, ws, (int)M, (int)N, (int)K, kps)
   switch (v) {
-    case FLAT_R32_C16: LFS_FLAT(2, 1, 8, 2, 2); break;
+    case FLAT_R32_C16: LFS_FLAT(2, 1, 8, 2, 4); break;
     case FLAT_R32_C32: LFS_FLAT(2, 2, 8, 2, 2); break;
+    case FLAT_S32_C32: LFS_FLAT(2, 2, 8, 2, 4); break;
+    case FLAT_R128_C48: LFS_FLAT(8, 3, 6, 8, 1); break;
     case FLAT_R128_C64: LFS_FLAT(8, 4, 6, 4, 2); break;
     case FLAT_R16_C16: LFS_FLAT(1, 1, 32, 1, 8); break;
     default: break;

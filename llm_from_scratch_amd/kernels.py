@@ -126,19 +126,21 @@ def flat_gemm_variant(M: int, N: int, K: int, kps: Optional[int] = None) -> Opti
     """The one-shot GEMM fp8_gemm runs for 16 < M <= 128 (None: another
     kernel).  The same rule as flat_variant in csrc/fp8_gemm.hip: unsplit
     (``kps`` None) K <= 1024 with <= 512 workgroups of 32 rows x 16 (else 32)
-    columns, K <= 768 with <= 256 workgroups of 128 x 64, K <= 4096 with <=
-    512 workgroups of 16 x 16; split-K partials of at most 8 K blocks each in
-    <= 1024 workgroups of 32 x 32."""
+    columns, K <= 768 with <= 256 workgroups of 128 x 48 (else 128 x 64), K
+    <= 4096 with <= 512 workgroups of 16 x 16; split-K partials of at most 8
+    K blocks each in <= 1024 workgroups of 32 x 32 ("s32c32")."""
     if M <= 16 or M > 128:
         return None
     kb = K // 128
     r32, c16, c32 = -(-M // 32), -(-N // 16), -(-N // 32)
     if kps is not None:
-        return "r32c32" if kps <= 8 and r32 * c32 * -(-kb // kps) <= 1024 else None
+        return "s32c32" if kps <= 8 and r32 * c32 * -(-kb // kps) <= 1024 else None
     if kb <= 8 and r32 * c16 <= 512:
         return "r32c16"
     if kb <= 8 and r32 * c32 <= 512:
         return "r32c32"
+    if kb <= 6 and -(-N // 48) <= 256:
+        return "r128c48"
     if kb <= 6 and -(-N // 64) <= 256:
         return "r128c64"
     if kb <= 32 and -(-M // 16) * c16 <= 512:

@@ -157,9 +157,10 @@ def test_decode_gemm_dispatch_rule():
     assert K.use_skinny_gemm(16, 1024, 4096) and not K.use_skinny_gemm(17, 1024, 4096)
     assert K.flat_gemm_variant(128, 1280, 768) == "r32c16"     # fused QKV
     assert K.flat_gemm_variant(128, 768, 768) == "r32c16"      # output projection
-    assert K.flat_gemm_variant(128, 9216, 768) == "r128c64"    # stacked w13
+    assert K.flat_gemm_variant(128, 9216, 768) == "r128c48"    # stacked w13
+    assert K.flat_gemm_variant(128, 14000, 512) == "r128c64"
     assert K.flat_gemm_variant(128, 32000, 768) is None        # lm_head
     assert K.flat_gemm_variant(128, 768, 4608) is None         # down projection: split instead
     assert K.default_gemm_splits(128, 768, 4608) == 5
-    assert K.flat_gemm_variant(128, 768, 4608, kps=8) == "r32c32"
+    assert K.flat_gemm_variant(128, 768, 4608, kps=8) == "s32c32"
     assert K.default_gemm_splits(128, 9216, 768) == 1

@@ -292,14 +292,16 @@ def _random_codes(rng, M, N, Kd):
 @pytest.mark.parametrize("M,N,Kd,variant", [(17, 250, 384, "r32c16"), (33, 96, 1024, "r32c16"),
                                             (128, 1280, 768, "r32c16"), (128, 31, 512, "r32c16"),
                                             (100, 4096, 768, "r32c32"), (128, 4090, 1024, "r32c32"),
-                                            (128, 9216, 768, "r128c64"), (100, 8200, 256, "r128c64"),
+                                            (128, 9216, 768, "r128c48"), (100, 8200, 256, "r128c48"),
+                                            (128, 14000, 512, "r128c64"), (70, 12290, 768, "r128c64"),
                                             (128, 1024, 4096, "r16c16"), (40, 1000, 1536, "r16c16"),
                                             (128, 1536, 1536, None), (128, 768, 4608, None)])
 def test_fp8_gemm_flat(M, N, Kd, variant):
     """The one-shot decode kernel (16 < M <= 128: every operand byte of a
-    workgroup copied to LDS in one burst) in each of its four geometries --
-    32 x 16 and 32 x 32 (row x column) workgroups for K <= 1024, 128 x 64
-    for wide N at K <= 768, 16 x 16 for K <= 4096 -- and as split-K partials
+    workgroup copied to LDS in one burst) in each of its geometries --
+    32 x 16 and 32 x 32 (row x column) workgroups for K <= 1024, 128 x 48
+    and 128 x 64 for wide N at K <= 768 (48 columns straddle the weights'
+    128-row scale blocks), 16 x 16 for K <= 4096 -- and as split-K partials
     of 8 K blocks with the reduction (variant None: K = 1536 in 2 splits,
     the cfg5 down projection's K = 4608 in 5): ragged M and N (not
     multiples of 16, 32, 64 or 4), 2 to 36 K blocks, bias vector and per-row
@@ -307,7 +309,7 @@ def test_fp8_gemm_flat(M, N, Kd, variant):
     assert K.flat_gemm_variant(M, N, Kd) == variant
     if variant is None:
         splits = K.default_gemm_splits(M, N, Kd)
-        assert splits > 1 and K.flat_gemm_variant(M, N, Kd, kps=-(-(Kd // 128) // splits)) == "r32c32"
+        assert splits > 1 and K.flat_gemm_variant(M, N, Kd, kps=-(-(Kd // 128) // splits)) == "s32c32"
     rng = np.random.default_rng(M * 5 + N + Kd)
     a, a_s, b, b_s = _random_codes(rng, M, N, Kd)
     bias = torch.from_numpy(rng.standard_normal(N).astype(np.float32)).to(DEV)
