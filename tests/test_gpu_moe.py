@@ -85,11 +85,14 @@ def test_grouped_gemm_gather_bias_and_fp32():
     got32 = c32.cpu().numpy()[used]
     scale = np.abs(ref32).max(1, keepdims=True) + 1e-30
     assert np.all(np.abs(got32 - ref32) <= 1e-4 * scale), "fp32 out"
-    # bit-identical to the dense kernel on the gathered rows of each used tile
+    # bit-identical to the dense tile kernel on the gathered rows of each used
+    # tile (129 rows, so that the dense call takes the 128 x 128 tile kernel
+    # and not the one-shot kernel of M <= 128, which sums K in another order)
     for i in np.nonzero(te >= 0)[0][:4]:
         src = np.maximum(rt[i * 128:(i + 1) * 128], 0)
+        src = np.concatenate([src, src[:1]])
         e = te[i]
-        dense = K.fp8_gemm(fp8(xq[src]), dev(xs[src]), fp8(bq[e]), dev(bs[e]), dev(bias[e]), splits=1)
+        dense = K.fp8_gemm(fp8(xq[src]), dev(xs[src]), fp8(bq[e]), dev(bs[e]), dev(bias[e]), splits=1)[:128]
         assert torch.equal(dense, c[i * 128:(i + 1) * 128]), f"tile {i} differs from fp8_gemm"
 
 
