@@ -557,12 +557,11 @@ def bench_decode_step(device, reps):
     temps = runner.prepare_sample(seqs)
     runner.run_model(ids, pos, False)  # fills the static graph inputs
     graph = runner.graphs[B]
-    hidden = runner.graph_vars["outputs"][:B]
     gen = torch.Generator(device=device).manual_seed(0)
 
     def step():
         graph.replay()
-        return runner.sampler(model.compute_logits(hidden), temps, gen)
+        return runner.sampler(runner.graph_logits(B), temps, gen)
 
     for _ in range(3):
         step()

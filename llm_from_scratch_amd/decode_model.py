@@ -456,19 +456,31 @@ class DecodeModel(nn.Module):
                                                          ".w2.weight", ".w2.bias")) for m in mlps])
         return self
 
-    def forward(self, input_ids: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
+    def _forward(self, input_ids: torch.Tensor, positions: torch.Tensor, quant: bool):
         x = self.embed[input_ids]
         residual = None
         tr = self.trace
         for i, layer in enumerate(self.layers):
             x, residual = layer(x, residual, positions, None if tr is None else tr.setdefault(i, {}))
-        h, _, _, _ = self.final_norm(x, residual)
+        h, _, hq, hs = self.final_norm(x, residual, quant=quant)
         if tr is not None:
             tr["final"] = dict(x=x, residual=residual, h=h)
-        return h
+        return h, hq, hs
+
+    def forward(self, input_ids: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
+        return self._forward(input_ids, positions, quant=False)[0]
+
+    def forward_q(self, input_ids: torch.Tensor, positions: torch.Tensor):
+        """forward, plus the act_quant codes and scales of its output (the
+        lm_head's FP8 input) from the final norm's launch: (h, hq, hs)."""
+        return self._forward(input_ids, positions, quant=True)
 
     def compute_logits(self, hidden: torch.Tensor) -> torch.Tensor:
         logits = self.lm_head(hidden)
         if self.trace is not None:
             self.trace["final"].update(head_in=hidden, logits=logits)
         return logits
+
+    def compute_logits_q(self, hq: torch.Tensor, hs: torch.Tensor) -> torch.Tensor:
+        """compute_logits on an input already quantised (forward_q)."""
+        return self.lm_head.gemm(hq, hs)

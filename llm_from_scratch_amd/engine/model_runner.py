@@ -238,7 +238,19 @@ class ModelRunner:
         v["block_tables"].fill_(-1)
         v["block_tables"][:bs, :ctx.block_tables.size(1)] = ctx.block_tables
         self.graphs[graph_bs].replay()
-        return self.model.compute_logits(v["outputs"][:bs])
+        return self.graph_logits(bs)
+
+    def graph_logits(self, bs: int) -> torch.Tensor:
+        """Logits of the first bs rows of the last replay of the graph that
+        serves batch size bs.  A model with forward_q (its output's act_quant
+        from the final norm's own launch) captured that, and its lm_head
+        skips its own act_quant (the same codes and scales, so the same
+        logits)."""
+        graph_bs = next(b for b in sorted(self.graphs) if b >= bs)
+        h, hq, hs = self.graph_outputs[graph_bs]
+        if hq is not None:
+            return self.model.compute_logits_q(hq[:bs], hs[:bs])
+        return self.model.compute_logits(h[:bs])
 
     def run(self, seqs: list[Sequence], is_prefill: bool,
             generator: Optional[torch.Generator] = None) -> list[int]:
@@ -267,20 +279,25 @@ class ModelRunner:
         slot_mapping = torch.full((max_bs,), -1, dtype=torch.int64, device=dev)
         context_lens = torch.zeros(max_bs, dtype=torch.int64, device=dev)
         block_tables = torch.full((max_bs, max_blocks), -1, dtype=torch.int32, device=dev)
-        outputs = torch.zeros(max_bs, cfg["hidden_size"], dtype=torch.bfloat16, device=dev)
         sizes = [b for b in [1, 2, 4, 8] + list(range(16, max_bs + 1, 16)) if b <= max_bs]
+        self.graph_outputs = {}
         pool = None
         for bs in reversed(sizes):
             graph = torch.cuda.CUDAGraph()
             set_context(False, slot_mapping=slot_mapping[:bs], context_lens=context_lens[:bs],
                         block_tables=block_tables[:bs])
-            outputs[:bs] = self.model(input_ids[:bs], positions[:bs])  # warm up outside capture
+            fwd = getattr(self.model, "forward_q", None)
+            run = (lambda: fwd(input_ids[:bs], positions[:bs])) if fwd is not None else \
+                (lambda: (self.model(input_ids[:bs], positions[:bs]), None, None))
+            run()  # warm up outside capture
             with torch.cuda.graph(graph, pool):
-                outputs[:bs] = self.model(input_ids[:bs], positions[:bs])
+                # the graph's own output tensors (in its pool), read after each
+                # replay: no copy into a shared buffer
+                self.graph_outputs[bs] = run()
             if pool is None:
                 pool = graph.pool()
             self.graphs[bs] = graph
             torch.cuda.synchronize()
             reset_context()
         self.graph_vars = dict(input_ids=input_ids, positions=positions, slot_mapping=slot_mapping,
-                               context_lens=context_lens, block_tables=block_tables, outputs=outputs)
+                               context_lens=context_lens, block_tables=block_tables)
