@@ -1019,11 +1019,18 @@ __device__ __forceinline__ int opaque(int x) {
   return x;
 }
 
-template <bool HAS_BIAS>
+// HALF: the tail launch for a last round of at most half the CUs' worth of
+// tiles -- tiles ntiles .. tiles_m * tiles_n - 1 of the grouped order, each
+// as two 256 x 128 halves (workgroup 2h + p: tile ntiles + h, columns
+// 128 p ..), so that twice as many CUs share the round.  A half is
+// computed by waves 0-3 (one per SIMD, as 2 x 2 waves of 128 x 64); waves
+// 4-7 only copy and take the barriers.  Otherwise workgroups walk tiles
+// 0 .. ntiles - 1.
+template <bool HAS_BIAS, bool HALF>
 __global__ __launch_bounds__(512, 1) void fp8_gemm_persist(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ B,
     const float* __restrict__ Bs, const float* __restrict__ bias, uint16_t* __restrict__ C, int M, int N, int K,
-    int tiles_m, int tiles_n) {
+    int tiles_m, int tiles_n, int ntiles) {
   constexpr int A_BYTES = BIG * BK;
   constexpr int STAGE = 2 * A_BYTES;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
@@ -1033,12 +1040,12 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_persist(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 2, wn = wave & 3;
+  const int wm = HALF ? (wave >> 1) & 1 : wave >> 2, wn = HALF ? wave & 1 : wave & 3;
+  const bool active = !HALF || wave < 4;
   const int KT = K / BK;
   const int nch = (KT + SCKB - 1) / SCKB;  // scale chunks per tile
   const int nbs = N / 128;
   const int r16 = lane & 15, g = lane >> 4;
-  const int ntiles = tiles_m * tiles_n;
   const int nwg = gridDim.x;
   auto tile_of = [&](int t, int& m0, int& n0) {
     const int group = t / (GROUP_M_BIG * tiles_n);
@@ -1047,10 +1054,15 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_persist(
     m0 = (first_m + (t % gsize)) * BIG;
     n0 = ((t % (GROUP_M_BIG * tiles_n)) / gsize) * BIG;
   };
-  int t = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);
-  if (t >= ntiles) return;  // whole workgroup, before any barrier
+  int t = HALF ? 0 : (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);
+  if (!HALF && t >= ntiles) return;  // whole workgroup, before any barrier
   int m0, n0;
-  tile_of(t, m0, n0);
+  if constexpr (HALF) {
+    tile_of(ntiles + (int)(blockIdx.x >> 1), m0, n0);
+    n0 += (blockIdx.x & 1) * 128;
+  } else {
+    tile_of(t, m0, n0);
+  }
 
   const unsigned lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
   const unsigned lsas = __builtin_amdgcn_readfirstlane(lds_addr(&sas[0][0][0]));
@@ -1102,7 +1114,7 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_persist(
 #pragma unroll
   for (int u = 0; u < 4; ++u) dma16s(tileA, offA[u], lds0 + (wave + 8 * u) * 1024);
 #pragma unroll
-  for (int u = 0; u < 4; ++u) dma16s(tileB, offB[u], lds0 + A_BYTES + (wave + 8 * u) * 1024);
+  for (int u = 0; u < (HALF ? 2 : 4); ++u) dma16s(tileB, offB[u], lds0 + A_BYTES + (wave + 8 * u) * 1024);
 
   // block 0's operands
   wait_vm<0>();
@@ -1125,7 +1137,7 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_persist(
   int cbase = 0;  // scale chunks done (scale buffer parity)
   for (;;) {
     const int t_next = t + nwg;
-    const bool has_next = t_next < ntiles;
+    const bool has_next = !HALF && t_next < ntiles;
     int m0n = m0, n0n = n0;
     if (has_next) tile_of(t_next, m0n, n0n);
     for (int kt = 0; kt < KT; ++kt, ++gk) {
@@ -1150,6 +1162,15 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_persist(
       float sc[8];
       float4 s0n, s1n;
       float bsvn;
+      if (HALF && !active) {  // an idle wave's copies of block kt + 1, then the block's barrier
+#pragma unroll
+        for (int u = 0; u < 4; ++u) dma16s(dA + (size_t)kn * BK, offA[u], nbase + (wave + 8 * u) * 1024);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) dma16s(dB + (size_t)kn * BK, offB[u], nbase + A_BYTES + (wave + 8 * u) * 1024);
+        wait_vm<0>();
+        __syncthreads();
+        continue;
+      }
       v4f tp[32];
 #pragma unroll
       for (int k = 0; k < 34; ++k) {
@@ -1161,7 +1182,7 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_persist(
         if ((k & 1) == 0 && k < 16) {
           const int u = (k >> 1) & 3;
           if (k < 8) dma16s(dA + (size_t)kn * BK, offA[u], nbase + (wave + 8 * u) * 1024);
-          else dma16s(dB + (size_t)kn * BK, offB[u], nbase + A_BYTES + (wave + 8 * u) * 1024);
+          else if (!HALF || u < 2) dma16s(dB + (size_t)kn * BK, offB[u], nbase + A_BYTES + (wave + 8 * u) * 1024);
         }
         if ((k & 3) == 0 && (k >> 2) + 1 < 8) {
           const int i1 = (k >> 2) + 1;
@@ -1199,6 +1220,7 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_persist(
       bsv = bsvn;
     }
     // ---- epilogue: bias, bf16 pairs, permlane16 swap, 16 stores per wave
+    if (!active) break;  // (a half's idle waves; a half is its workgroup's only item)
     float bv[4][4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -1471,13 +1493,31 @@ int fp8_gemm_impl(const void* a, const float* a_s, const void* b, const float* b
   }
   if (ws == nullptr && use_persistent(M, N, K, bias, bias_ld)) {
     const int64_t bm = (M + BIG - 1) / BIG, bn = N / BIG;
-    const int nwg = (int)std::min<int64_t>(std::max(8, cu_count() / 8 * 8), (bm * bn + 7) / 8 * 8);
+    const int64_t ntiles = bm * bn;
+    const int nwg = (int)std::min<int64_t>(std::max(8, cu_count() / 8 * 8), (ntiles + 7) / 8 * 8);
+    // a last round of at most half the workgroups' worth of tiles runs as a
+    // second launch of 256 x 128 halves
+    const int64_t rem = ntiles % nwg;
+    const int64_t nmain = rem > 0 && 2 * rem <= nwg && ntiles > nwg ? ntiles - rem : ntiles;
     if (bias != nullptr)
-      hipLaunchKernelGGL(fp8_gemm_persist<true>, dim3((unsigned)nwg), dim3(512), 0, st, (const uint8_t*)a, a_s,
-                         (const uint8_t*)b, b_s, bias, (uint16_t*)c, (int)M, (int)N, (int)K, (int)bm, (int)bn);
+      hipLaunchKernelGGL((fp8_gemm_persist<true, false>), dim3((unsigned)nwg), dim3(512), 0, st, (const uint8_t*)a,
+                         a_s, (const uint8_t*)b, b_s, bias, (uint16_t*)c, (int)M, (int)N, (int)K, (int)bm, (int)bn,
+                         (int)nmain);
     else
-      hipLaunchKernelGGL(fp8_gemm_persist<false>, dim3((unsigned)nwg), dim3(512), 0, st, (const uint8_t*)a, a_s,
-                         (const uint8_t*)b, b_s, bias, (uint16_t*)c, (int)M, (int)N, (int)K, (int)bm, (int)bn);
+      hipLaunchKernelGGL((fp8_gemm_persist<false, false>), dim3((unsigned)nwg), dim3(512), 0, st, (const uint8_t*)a,
+                         a_s, (const uint8_t*)b, b_s, bias, (uint16_t*)c, (int)M, (int)N, (int)K, (int)bm, (int)bn,
+                         (int)nmain);
+    if (nmain < ntiles) {
+      const unsigned nh = (unsigned)(2 * (ntiles - nmain));
+      if (bias != nullptr)
+        hipLaunchKernelGGL((fp8_gemm_persist<true, true>), dim3(nh), dim3(512), 0, st, (const uint8_t*)a, a_s,
+                           (const uint8_t*)b, b_s, bias, (uint16_t*)c, (int)M, (int)N, (int)K, (int)bm, (int)bn,
+                           (int)nmain);
+      else
+        hipLaunchKernelGGL((fp8_gemm_persist<false, true>), dim3(nh), dim3(512), 0, st, (const uint8_t*)a, a_s,
+                           (const uint8_t*)b, b_s, bias, (uint16_t*)c, (int)M, (int)N, (int)K, (int)bm, (int)bn,
+                           (int)nmain);
+    }
     return check_launch("fp8_gemm");
   }
   if (ws == nullptr && use_big_tiles(M, N, K)) {

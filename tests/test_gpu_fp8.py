@@ -449,6 +449,26 @@ def test_fp8_gemm_cfg2_shapes(M, KN):
     assert_close(got, ref, f"M={M} K={Kd} N={N}")
 
 
+def test_fp8_gemm_persistent_half_tail_bit_identical():
+    """A last round of at most half a round of 256x256 tiles runs as a second
+    launch of 256 x 128 halves (four waves each).  M = 4096, N = 5632, K =
+    2048: 352 tiles, the last 96 as 192 halves; the same rows of an M = 16384
+    product (1408 tiles; those rows there in whole tiles of the first
+    rounds) must be bit-identical, every byte pattern of e4m3 but NaN, with a
+    bias vector; and the halves' rows against the oracle."""
+    rng = np.random.default_rng(77)
+    Kd, N = 2048, 5632
+    a, a_s, b, b_s = _random_codes(rng, 16384, N, Kd)
+    bias = torch.from_numpy(rng.standard_normal(N).astype(np.float32)).to(DEV)
+    print("half tail: M 4096 / 16384, K 2048, N 5632", flush=True)
+    small = K.fp8_gemm(a[:4096].contiguous(), a_s[:4096].contiguous(), b, b_s, bias)
+    big = K.fp8_gemm(a, a_s, b, b_s, bias)
+    torch.cuda.synchronize()
+    assert torch.equal(small.view(torch.int16), big[:4096].view(torch.int16)), "half tiles differ from whole tiles"
+    rows = np.array([2048, 2300, 3071, 3072, 3500, 4095])  # rows of tail tiles
+    assert_close(f32(small)[rows], gemm_oracle(a, a_s, b, b_s, bias, rows=rows), "half tail")
+
+
 @pytest.mark.parametrize("KN", W.GEMM_KN)
 def test_fp8_gemm_m16384_sampled_rows(KN):
     """The three cfg2 headline shapes at M = 16384 (the bench's launches):
