@@ -1021,8 +1021,9 @@ __device__ __forceinline__ int opaque(int x) {
 
 // HALF: the tail launch for a last round of at most half the CUs' worth of
 // tiles -- tiles ntiles .. tiles_m * tiles_n - 1 of the grouped order, each
-// as two 256 x 128 halves (workgroup 2h + p: tile ntiles + h, columns
-// 128 p ..), so that twice as many CUs share the round.  A half is
+// as two 256 x 128 halves (half 2i + p: tile ntiles + i, columns 128 p ..;
+// a grid of a multiple of 8 workgroups), so that twice as many CUs share the
+// round.  A half is
 // computed by waves 0-3 (one per SIMD, as 2 x 2 waves of 128 x 64); waves
 // 4-7 only copy and take the barriers.  Otherwise workgroups walk tiles
 // 0 .. ntiles - 1.
@@ -1058,8 +1059,12 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_persist(
   if (!HALF && t >= ntiles) return;  // whole workgroup, before any barrier
   int m0, n0;
   if constexpr (HALF) {
-    tile_of(ntiles + (int)(blockIdx.x >> 1), m0, n0);
-    n0 += (blockIdx.x & 1) * 128;
+    // halves h = 2 i + p in XCD order (workgroup w runs on XCD w mod 8): the
+    // two halves of a tile, and consecutive tiles, share one XCD's L2
+    const int h = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);
+    if (h >= 2 * (tiles_m * tiles_n - ntiles)) return;  // whole workgroup, before any barrier
+    tile_of(ntiles + (h >> 1), m0, n0);
+    n0 += (h & 1) * 128;
   } else {
     tile_of(t, m0, n0);
   }
@@ -1508,7 +1513,7 @@ int fp8_gemm_impl(const void* a, const float* a_s, const void* b, const float* b
                          a_s, (const uint8_t*)b, b_s, bias, (uint16_t*)c, (int)M, (int)N, (int)K, (int)bm, (int)bn,
                          (int)nmain);
     if (nmain < ntiles) {
-      const unsigned nh = (unsigned)(2 * (ntiles - nmain));
+      const unsigned nh = (unsigned)((2 * (ntiles - nmain) + 7) / 8 * 8);
       if (bias != nullptr)
         hipLaunchKernelGGL((fp8_gemm_persist<true, true>), dim3(nh), dim3(512), 0, st, (const uint8_t*)a, a_s,
                            (const uint8_t*)b, b_s, bias, (uint16_t*)c, (int)M, (int)N, (int)K, (int)bm, (int)bn,
