@@ -876,17 +876,27 @@ __device__ __forceinline__ float merge_element(const float* __restrict__ ws_o, c
   return res;
 }
 
-// One workgroup per (head, sequence), one lane per head dim.
-__global__ __launch_bounds__(128) void paged_decode_merge(
+// One thread per output element: workgroup (x, b) merges elements
+// x*256 .. x*256+255 of sequence b's Hq*D outputs (whole heads for D = 64 /
+// 128).  256-thread workgroups, one per CU at the cfg3 shapes: the same
+// arithmetic as one 64 / 128-thread workgroup per (head, sequence), bit for
+// bit, and 0.1-0.2 us (cfg3) to 2 us (cfg4) less kernel time -- fewer
+// workgroups to dispatch; the two dependent round trips (lengths and scan,
+// then the partials) remain.
+constexpr int MERGE_THREADS = 256;
+__global__ __launch_bounds__(MERGE_THREADS) void paged_decode_merge(
     const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
     const int64_t* __restrict__ ctx_lens, uint16_t* __restrict__ out, int Hq, int D, int BS,
     int max_blocks, PartMap pm) {
-  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  const int b = blockIdx.y;
+  const int e = blockIdx.x * MERGE_THREADS + threadIdx.x;
+  if (e >= Hq * D) return;
+  const int h = e / D, d = e - h * D;
   const int64_t Lc = min(ctx_lens[b], (int64_t)max_blocks * BS);
   int64_t r0, rs;
   const int ns = part_span(pm, b, h, Hq, Lc, BS, r0, rs);
-  if (ns == 1 || d >= D) return;
-  out[((int64_t)b * Hq + h) * D + d] = (uint16_t)f32_to_bf16(merge_element(ws_o, ws_ml, r0, rs, ns, D, d));
+  if (ns == 1) return;
+  out[(int64_t)b * Hq * D + e] = (uint16_t)f32_to_bf16(merge_element(ws_o, ws_ml, r0, rs, ns, D, d));
 }
 
 // The merge fused with the act_quant of its output row (the output
@@ -1341,8 +1351,8 @@ int paged_decode_merge_launch(float* ws_o, float* ws_ml, const int64_t* context_
                        ws_o, ws_ml, context_lens, (uint16_t*)out, (uint8_t*)q_out, q_scale, Hq, D, BS, max_blocks, pm);
     return check_launch("paged_decode(merge + quant)");
   }
-  hipLaunchKernelGGL(paged_decode_merge, dim3((unsigned)Hq, (unsigned)B), dim3((unsigned)D), 0, st,
-                     ws_o, ws_ml, context_lens, (uint16_t*)out, Hq, D, BS, max_blocks, pm);
+  hipLaunchKernelGGL(paged_decode_merge, dim3((unsigned)((Hq * D + MERGE_THREADS - 1) / MERGE_THREADS), (unsigned)B),
+                     dim3(MERGE_THREADS), 0, st, ws_o, ws_ml, context_lens, (uint16_t*)out, Hq, D, BS, max_blocks, pm);
   return check_launch("paged_decode(merge)");
 }
 }  // namespace
