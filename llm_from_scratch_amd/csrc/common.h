@@ -148,17 +148,79 @@ __device__ __forceinline__ uint2 quant8(const float* f, float s) {
 }
 
 // ------------------------------------------------------- wave reductions --
-// xor-butterfly over groups of W consecutive lanes (W a power of two <= 64)
+// The value of lane (lane ^ O), O = 1 .. 32 -- the partner __shfl_xor(v, O,
+// 64) reads -- moved without the LDS permute unit: DPP quad permutations
+// for O = 1, 2; for O = 4 a row shift left into banks 0 and 2 (lanes 0-3,
+// 8-11 of each 16) and right into banks 1 and 3; a row rotation by 8 for
+// O = 8; the permlane swaps for 16 and 32, which return the values of lanes
+// l & ~O and l | O.  One or two VALU instructions instead of an LDS round
+// trip in a dependent chain.  The lanes read must be active: every group of
+// 2*O lanes all in or all out.
+template <int O>
+__device__ __forceinline__ int xor_partner(int v) {
+  static_assert(O == 1 || O == 2 || O == 4 || O == 8 || O == 16 || O == 32, "xor distance");
+  if constexpr (O == 1) {
+    return __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false);  // quad_perm [1, 0, 3, 2]
+  } else if constexpr (O == 2) {
+    return __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false);  // quad_perm [2, 3, 0, 1]
+  } else if constexpr (O == 4) {
+    const int t = __builtin_amdgcn_update_dpp(v, v, 0x104, 0xF, 0x5, false);  // row_shl:4
+    return __builtin_amdgcn_update_dpp(t, v, 0x114, 0xF, 0xA, false);         // row_shr:4
+  } else if constexpr (O == 8) {
+    return __builtin_amdgcn_update_dpp(v, v, 0x128, 0xF, 0xF, false);  // row_ror:8
+  } else if constexpr (O == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (int)((__lane_id() & 16) ? r[0] : r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (int)((__lane_id() & 32) ? r[0] : r[1]);
+  }
+}
+__device__ __forceinline__ float as_float(int v) { return __int_as_float(v); }
+// v op v(lane ^ O), the same operands as v op __shfl_xor(v, O, 64): IEEE add
+// and max are commutative, so the results are bit-identical.  For 16 and 32
+// the swap's two results are the two operands.
+template <int O>
+__device__ __forceinline__ float xor_sum(float v) {
+  if constexpr (O == 16 || O == 32) {
+    const auto r = O == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false)
+                           : __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+    return as_float((int)r[0]) + as_float((int)r[1]);
+  } else {
+    return v + as_float(xor_partner<O>(__float_as_int(v)));
+  }
+}
+template <int O>
+__device__ __forceinline__ float xor_max(float v) {
+  if constexpr (O == 16 || O == 32) {
+    const auto r = O == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false)
+                           : __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+    return fmaxf(as_float((int)r[0]), as_float((int)r[1]));
+  } else {
+    return fmaxf(v, as_float(xor_partner<O>(__float_as_int(v))));
+  }
+}
+
+// xor-butterfly over groups of W consecutive lanes (W a power of two <= 64),
+// distances W/2 down to 1 (the order of the sums)
 template <int W>
 __device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-  for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  if constexpr (W > 32) v = xor_max<32>(v);
+  if constexpr (W > 16) v = xor_max<16>(v);
+  if constexpr (W > 8) v = xor_max<8>(v);
+  if constexpr (W > 4) v = xor_max<4>(v);
+  if constexpr (W > 2) v = xor_max<2>(v);
+  if constexpr (W > 1) v = xor_max<1>(v);
   return v;
 }
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  if constexpr (W > 32) v = xor_sum<32>(v);
+  if constexpr (W > 16) v = xor_sum<16>(v);
+  if constexpr (W > 8) v = xor_sum<8>(v);
+  if constexpr (W > 4) v = xor_sum<4>(v);
+  if constexpr (W > 2) v = xor_sum<2>(v);
+  if constexpr (W > 1) v = xor_sum<1>(v);
   return v;
 }
 

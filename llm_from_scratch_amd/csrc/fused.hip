@@ -34,6 +34,31 @@
 namespace lfs {
 namespace {
 
+// (best, bi) of the whole wave in every lane: the largest value, ties to
+// the lowest index -- a total order, so the butterfly's pairing does not
+// change the result.
+template <int O>
+__device__ __forceinline__ void argmax_step(float& best, int& bi) {
+  const float ob = as_float(xor_partner<O>(__float_as_int(best)));
+  const int oi = xor_partner<O>(bi);
+  if (ob > best || (ob == best && oi < bi)) {
+    best = ob;
+    bi = oi;
+  }
+}
+__device__ __forceinline__ void wave_argmax(float& best, int& bi) {
+  argmax_step<32>(best, bi);
+  argmax_step<16>(best, bi);
+  argmax_step<8>(best, bi);
+  argmax_step<4>(best, bi);
+  argmax_step<2>(best, bi);
+  argmax_step<1>(best, bi);
+}
+// v of lane `src` (wave-uniform)
+__device__ __forceinline__ float lane_value(float v, int src) {
+  return as_float(__builtin_amdgcn_readlane(__float_as_int(v), __builtin_amdgcn_readfirstlane(src)));
+}
+
 // Sum over a workgroup of NW waves; every thread gets the total.
 template <int NW>
 __device__ __forceinline__ float block_sum(float v, float* red) {
@@ -283,14 +308,9 @@ __global__ __launch_bounds__(64 * kRouteTokens) void moe_route_kernel(
     for (int k = 0; k < top_k; ++k) {
       float best = chosen ? -INFINITY : key;
       int bi = valid && !chosen ? lane : kMaxExperts;
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        const float ob = __shfl_xor(best, o, 64);
-        const int oi = __shfl_xor(bi, o, 64);
-        if (ob > best || (ob == best && oi < bi)) { best = ob; bi = oi; }
-      }
+      wave_argmax(best, bi);
       if (lane == bi) { chosen = true; myk = k; }
-      wsum = add_rn(wsum, __shfl(score, bi < 64 ? bi : 0, 64) * (bi < 64 ? 1.f : 0.f));
+      wsum = add_rn(wsum, lane_value(score, bi < 64 ? bi : 0) * (bi < 64 ? 1.f : 0.f));
     }
     float wgt = chosen ? score : 0.f;
     if (top_k > 1) wgt = chosen ? wgt / add_rn(wsum, 1e-10f) : 0.f;
@@ -413,15 +433,10 @@ __device__ __forceinline__ void route_token(
     for (int k = 0; k < top_k; ++k) {
       float best = chosen ? -INFINITY : key;
       int bi = valid && !chosen ? lane : kMaxExperts;
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        const float ob = __shfl_xor(best, o, 64);
-        const int oi = __shfl_xor(bi, o, 64);
-        if (ob > best || (ob == best && oi < bi)) { best = ob; bi = oi; }
-      }
+      wave_argmax(best, bi);
       if (lane == bi) chosen = true;
       if (lane == 0) sel[k] = bi;
-      wsum = add_rn(wsum, __shfl(score, bi < 64 ? bi : 0, 64) * (bi < 64 ? 1.f : 0.f));
+      wsum = add_rn(wsum, lane_value(score, bi < 64 ? bi : 0) * (bi < 64 ? 1.f : 0.f));
     }
     float wgt = chosen ? score : 0.f;
     if (top_k > 1) wgt = chosen ? wgt / add_rn(wsum, 1e-10f) : 0.f;

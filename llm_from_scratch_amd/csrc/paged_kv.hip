@@ -284,13 +284,16 @@ struct DecodeWave {
   // the unnormalised partial to workspace rows prow + g.
   // Sum acc over the token subgroups: afterwards lanes with ts == 0 hold the
   // wave's totals for dims dc*8 .. +7 of every head.
+  // (distances LPR, 2 LPR, ..., 32: the same sums as acc += __shfl_xor(acc, o))
+  template <int O = Geo::LPR>
   __device__ __forceinline__ void reduce_lanes() {
-#pragma unroll
-    for (int o = Geo::LPR; o < 64; o <<= 1)
+    if constexpr (O < 64) {
 #pragma unroll
       for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[g][e] += __shfl_xor(acc[g][e], o, 64);
+        for (int e = 0; e < 8; ++e) acc[g][e] = xor_sum<O>(acc[g][e]);
+      reduce_lanes<2 * O>();
+    }
   }
   __device__ __forceinline__ void finish(bool whole, uint16_t* __restrict__ out, float* __restrict__ ws_o,
                                          float* __restrict__ ws_ml, int64_t b, int kh, int Hq, int64_t prow) {
