@@ -105,7 +105,7 @@
 extern "C" {
 #endif
 
-#define LFS_ABI_VERSION 14
+#define LFS_ABI_VERSION 15
 
 /* argument errors (negative); launch errors are positive hipError_t values */
 #define LFS_EINVAL (-1)
@@ -226,15 +226,22 @@ int lfs_store_kvcache(const void* key, int64_t k_stride_t, const void* value, in
  * same merge.  blocks_per_split = -1: single launch, one 8-wave workgroup
  * per (sequence, pair of kv heads) (one kv head when Hkv is odd) whose waves
  * walk interleaved tiles and merge through LDS; no workspace, no second
- * launch.  Whatever the mode, the grid depends only on the shapes (not on
- * the lengths), so the call is graph-capturable.
+ * launch.  blocks_per_split = -2 (B <= 256): the single launch in the
+ * paired order, one 4-wave workgroup per (sequence, kv head); every
+ * workgroup ranks the sequences by context length (longest first, ties to
+ * the lower index) and takes its (sequence, kv head) from that order so
+ * that the two workgroups a CU holds at once -- w and w + CUs -- are a long
+ * and a short one (the longest run alone when fewer than two rounds).
+ * Whatever the mode, the grid depends only on the shapes (not on the
+ * lengths), so the call is graph-capturable.
  * workspace: at least lfs_paged_decode_workspace_bytes(...) bytes (for 0 a
  * bound from the current device's CU count: size it on that device; for -1
- * zero, and workspace may be NULL).
+ * and -2 zero, and workspace may be NULL).
  * Optionally (q_out and q_scale both non-NULL) also the act_quant of each
  * output row, the output projection's FP8 input: q_out e4m3fn [B, Hq*D],
  * q_scale fp32 [B, Hq*D/128], bit-identical to lfs_act_quant(out, 128)
- * (needs Hq*D % 128 == 0, and for -1 also an even Hkv or G*D % 128 == 0);
+ * (needs Hq*D % 128 == 0, for -1 also an even Hkv or G*D % 128 == 0, for
+ * -2 G*D % 128 == 0);
  * the merge then runs one workgroup per (128-value group, sequence) instead
  * of one per (head, sequence).
  * D in {64, 128}; Hq % Hkv == 0, Hq/Hkv <= 8; block_size a multiple of 16.
@@ -266,7 +273,11 @@ int lfs_paged_decode(const void* q, const void* k_cache, const void* v_cache,
  * q_rot (optional, bf16 [B, Hq, D]) receives the rotated q.  Needs
  * (Hq + Hkv) * D / 16 <= 256 besides lfs_paged_decode's shape limits.  The
  * results equal the two calls' up to fp32 summation order (the newest token
- * enters the softmax first).
+ * enters the softmax first).  Without q_out, the launch takes the paired
+ * order of blocks_per_split -2 when B <= 256, CUs < B * Hkv <= 2 * CUs and
+ * the table holds at most 8192 tokens; its workgroups then run the q/k
+ * prologue before their walks, and the newest token enters the softmax
+ * last.
  */
 int lfs_paged_decode_rope(const void* qkv, int64_t ld, const float* q_weight, const float* k_weight,
                           const float* cos_sin, int64_t max_positions, const int64_t* positions,

@@ -11,7 +11,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "liblfs_kernels.so"
-ABI_VERSION = 14
+ABI_VERSION = 15
 # size of the library's static paged-decode workspace (LFS_DECODE_SCRATCH_BYTES)
 DECODE_SCRATCH_BYTES = 64 << 20
 

@@ -336,7 +336,8 @@ struct DecodeWave {
 // is t_begin = s*tile, tstride S.  btrow: the sequence's block-table row;
 // block ids at or past id_end are never loaded.  pw: the wave's private
 // LDS slice (T * GP floats).  pro() runs once, after the first tile's loads
-// are issued and before anything reads qa (a caller may fill qa there).
+// are issued and before anything reads qa (a caller may fill qa there); an
+// empty walk does not run it.
 struct NoPrologue {
   __device__ __forceinline__ void operator()() const {}
 };
@@ -642,15 +643,16 @@ struct RopeIn {
   float eps;
 };
 
-template <int D, int G, int HG, int NW, bool ROPE>
-__global__ __launch_bounds__(64 * NW) void paged_decode_pairs(
+template <int D, int G, int HG, int NW, bool ROPE, bool PAIR>
+__global__ __launch_bounds__(64 * NW, PAIR ? 2 : 1) void paged_decode_pairs(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
     const int64_t* __restrict__ ctx_lens, const int32_t* __restrict__ bt, int64_t bt_stride,
     uint16_t* __restrict__ out, uint8_t* __restrict__ qo, float* __restrict__ qs, int Hkv, int BS, int64_t NB,
-    int max_blocks, int tile, float scale_log2, int ngrp, RopeIn ri) {
+    int max_blocks, int tile, float scale_log2, int ngrp, int ncu, RopeIn ri) {
   using Geo = DecodeGeom<D>;
   using W = DecodeWave<D, G>;
   constexpr int S = NW / HG;
+  static_assert(!PAIR || (HG == 1 && NW == 4), "the paired order runs one kv head per 4-wave workgroup");
   constexpr int E = HG * G * D;  // output values of the workgroup
   __shared__ __attribute__((aligned(16))) float p_lds[NW][Geo::T * W::GP];
   __shared__ __attribute__((aligned(16))) float part_o[NW][G * D];
@@ -661,10 +663,67 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_pairs(
   __shared__ float red[8];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int hl = wave / S, s = wave - hl * S;
-  const int b = blockIdx.x / ngrp, grp = blockIdx.x - b * ngrp;
-  const int kh = grp * HG + hl;
   const int Hq = Hkv * G;
-  const int64_t L = ctx_lens[b];
+  constexpr int CPH = D / 8;  // 16-byte chunks per head row
+  RopeRow<1> rr;
+  if constexpr (ROPE) {
+    rr.init(Hq, Hkv, D, threadIdx.x);
+    rr.load_weights(ri.qw, ri.kw);  // the same for every sequence: before the order is known
+  }
+  int b, grp;
+  int64_t L;
+  if constexpr (PAIR) {
+    // Sequences ranked by context length, longest first (ties: lower index),
+    // and workgroup w given unit rank r(w) so that the two workgroups a CU
+    // holds at once -- w and w + ncu, the first round dealt one per CU --
+    // pair a long (sequence, kv head) with a short one: ranks 0 .. ncu-P-1
+    // (the longest) run alone, rank ncu-P+c shares CU c < P with rank
+    // W-1-c, P = W - ncu.  A permutation of the units for any W.
+    // key = (length clamped to 2^40) << 8 | (255 - index): distinct keys,
+    // larger for a longer context or, at equal length, a lower index; the
+    // rank of sequence i is the number of larger keys, counted by threads i
+    // (keys 0..127) and i + 128 (keys 128..255) from 16-byte LDS reads
+    __shared__ __attribute__((aligned(16))) uint64_t pkey[256];
+    __shared__ int64_t plen[256];
+    __shared__ int prank[256];
+    __shared__ int porder[256];
+    const int B = gridDim.x / ngrp;  // <= 256: checked on the host
+    const int t = threadIdx.x;
+    const int64_t lt = t < B ? ctx_lens[t] : 0;
+    pkey[t] = t < B ? ((uint64_t)min(max(lt, (int64_t)0), (int64_t)1 << 40) << 8) | (uint64_t)(255 - t) : 0;
+    plen[t] = lt;
+    auto count = [&](int i, int half) {  // keys of half `half` larger than sequence i's
+      int r = 0;
+      if (i < B && 128 * half < B) {
+        const uint64_t ki = pkey[i];
+        const uint4* kk = reinterpret_cast<const uint4*>(pkey + 128 * half);
+#pragma unroll 4
+        for (int j2 = 0; j2 < 64; ++j2) {  // padding keys are 0: never larger
+          const uint4 two = kk[j2];
+          r += (((uint64_t)two.y << 32 | two.x) > ki) + (((uint64_t)two.w << 32 | two.z) > ki);
+        }
+      }
+      return r;
+    };
+    for (int base = 0; base < B; base += 128) {  // sequences base .. base + 127
+      __syncthreads();
+      prank[t] = count(base + (t & 127), t >> 7);
+      __syncthreads();
+      if (t < 128 && base + t < B) porder[prank[t] + prank[t + 128]] = base + t;
+    }
+    __syncthreads();
+    const int Wg = gridDim.x, w = blockIdx.x;
+    const int P = max(0, min(Wg - ncu, ncu));
+    const int r = w >= ncu ? Wg - 1 - (w - ncu) : (w < P ? ncu - P + w : w - P);
+    b = porder[r / ngrp];
+    grp = r - (r / ngrp) * ngrp;
+    L = plen[b];
+  } else {
+    b = blockIdx.x / ngrp;
+    grp = blockIdx.x - b * ngrp;
+    L = ctx_lens[b];
+  }
+  const int kh = grp * HG + hl;
   // with ROPE the walks cover [0, L-1): the new token comes from the qkv row
   const int64_t Lc = min(ROPE ? L - 1 : L, (int64_t)max_blocks * BS);
 
@@ -672,9 +731,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_pairs(
   // scalar load returns with the context length's, which the walk waits for
   // anyway), so that its arithmetic in pro() waits for none of the walk's
   // loads: issued after the first tile's, they would have to return first
-  constexpr int CPH = D / 8;  // 16-byte chunks per head row
-  const int h0 = grp * HG;    // first kv head of the workgroup
-  RopeRow<1> rr;
+  const int h0 = grp * HG;  // first kv head of the workgroup
   int64_t slot = -1, p = 0;
   uint4 vnew = make_uint4(0, 0, 0, 0);
   const uint16_t* row = nullptr;
@@ -683,8 +740,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_pairs(
     p = ri.pos[b];
     p = p < 0 ? 0 : (p >= ri.max_pos ? ri.max_pos - 1 : p);
     slot = ri.slots != nullptr ? ri.slots[b] : -1;
-    rr.load(row, Hq, Hkv, D, threadIdx.x);
-    rr.load_weights(ri.qw, ri.kw);
+    rr.load(row);
     if (threadIdx.x < HG * CPH && h0 + (int)threadIdx.x / CPH < Hkv)
       vnew = *reinterpret_cast<const uint4*>(row + (int64_t)(Hq + Hkv + h0) * D + threadIdx.x * 8);
     rr.load_rope(ri.cos_sin + p * D);
@@ -722,25 +778,39 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_pairs(
   if (kh < Hkv) {
     W w(lane, Hkv);
     typename W::QBuf qa;
+    // the new token as a tile of one row, on the first walk of its head
+    auto new_token = [&]() {
+      typename W::KBuf ka;
+      typename W::VBuf va;
+      w.row_tile(ka, va, &new_kv[hl * D], &new_kv[(HG + hl) * D]);
+      w.tile(ka, va, qa, 1, scale_log2, p_lds[wave]);
+    };
     auto pro = [&]() {
       prologue();
       if constexpr (ROPE) {
         w.load_q_lds(qa, &new_q[hl * G * D]);
-        // the new token, on the first walk of its head, while the walk's
-        // first tile is still in flight
-        if (s == 0 && L >= 1) {
-          typename W::KBuf ka;
-          typename W::VBuf va;
-          w.row_tile(ka, va, &new_kv[hl * D], &new_kv[(HG + hl) * D]);
-          w.tile(ka, va, qa, 1, scale_log2, p_lds[wave]);
-        }
+        // while the walk's first tile is still in flight; the paired form
+        // adds it after the walk, where the walk's buffers are free
+        if (!PAIR && s == 0 && L >= 1) new_token();
       }
     };
     if (!ROPE) w.load_q(qa, q, b, kh, Hq);
-    if (Lc > (int64_t)s * tile)
-      decode_walk<D, G>(w, qa, kc, vc, bt + (int64_t)b * bt_stride, BS, NB, tile, scale_log2, kh,
-                        (int64_t)s * tile, Lc, S, max_blocks, p_lds[wave], pro);
+    // the paired form (two workgroups per CU, 256 registers a wave) runs the
+    // prologue before its walk: run inside the walk, its registers would be
+    // live across the walk's loop and spill
+    if constexpr (PAIR) pro();
+    if (Lc > (int64_t)s * tile) {
+      if constexpr (PAIR)
+        decode_walk<D, G>(w, qa, kc, vc, bt + (int64_t)b * bt_stride, BS, NB, tile, scale_log2, kh,
+                          (int64_t)s * tile, Lc, S, max_blocks, p_lds[wave]);
+      else
+        decode_walk<D, G>(w, qa, kc, vc, bt + (int64_t)b * bt_stride, BS, NB, tile, scale_log2, kh,
+                          (int64_t)s * tile, Lc, S, max_blocks, p_lds[wave], pro);
+    }
     if (!pro_done) pro();
+    if constexpr (ROPE && PAIR) {
+      if (s == 0 && L >= 1) new_token();
+    }
     w.reduce_lanes();
     if (w.ts == 0) {
 #pragma unroll
@@ -979,15 +1049,24 @@ bool dispatch_balanced(int G, unsigned nwg, dim3 block, hipStream_t st, const ui
 #undef LFS_G
 }
 
-template <int D, int HG, int NW, bool ROPE>
+int decode_cu_count();
+// the paired order ranks the sequences with one context length per thread
+constexpr int kPairMaxB = 256;
+// longest table (tokens) lfs_paged_decode_rope takes the paired order for:
+// a workgroup walks a whole (sequence, kv head), so the longest context
+// bounds the call
+constexpr int64_t kPairMaxContext = 8192;
+
+template <int D, int HG, int NW, bool ROPE, bool PAIR = false>
 bool dispatch_pairs_hg(int G, unsigned nwg, hipStream_t st, const uint16_t* q, const uint16_t* kc,
                        const uint16_t* vc, const int64_t* cl, const int32_t* bt, int64_t bts, uint16_t* out,
                        uint8_t* qo, float* qs, int Hkv, int BS, int64_t NB, int max_blocks, int tile, float sl2,
                        int ngrp, const RopeIn& ri) {
+  const int ncu = decode_cu_count();
 #define LFS_G(GG)                                                                                               \
   case GG:                                                                                                      \
-    hipLaunchKernelGGL((paged_decode_pairs<D, GG, HG, NW, ROPE>), dim3(nwg), dim3(64 * NW), 0, st, q, kc, vc,  \
-                       cl, bt, bts, out, qo, qs, Hkv, BS, NB, max_blocks, tile, sl2, ngrp, ri);                 \
+    hipLaunchKernelGGL((paged_decode_pairs<D, GG, HG, NW, ROPE, PAIR>), dim3(nwg), dim3(64 * NW), 0, st, q, kc, \
+                       vc, cl, bt, bts, out, qo, qs, Hkv, BS, NB, max_blocks, tile, sl2, ngrp, ncu, ri);        \
     return true;
   switch (G) {
     LFS_G(1) LFS_G(2) LFS_G(3) LFS_G(4) LFS_G(5) LFS_G(6) LFS_G(7) LFS_G(8)
@@ -1000,7 +1079,11 @@ template <int D, bool ROPE>
 bool dispatch_pairs(int HG, int G, unsigned nwg, hipStream_t st, const uint16_t* q, const uint16_t* kc,
                     const uint16_t* vc, const int64_t* cl, const int32_t* bt, int64_t bts, uint16_t* out,
                     uint8_t* qo, float* qs, int Hkv, int BS, int64_t NB, int max_blocks, int tile, float sl2,
-                    int ngrp, const RopeIn& ri) {
+                    int ngrp, const RopeIn& ri, bool pair = false) {
+  // paired order: one kv head per 4-wave workgroup, two workgroups per CU
+  if (pair)
+    return dispatch_pairs_hg<D, 1, 4, ROPE, true>(G, nwg, st, q, kc, vc, cl, bt, bts, out, qo, qs, Hkv, BS, NB,
+                                                  max_blocks, tile, sl2, ngrp, ri);
   // the RoPE prologue runs on 4 waves per workgroup (one per SIMD, so up to
   // 512 registers a wave): with 8 its registers and the walk's do not fit in
   // 256 and spill inside the tile loop
@@ -1100,8 +1183,8 @@ extern "C" int lfs_store_kvcache(const void* key, int64_t k_stride_t, const void
 extern "C" int64_t lfs_paged_decode_workspace_bytes(int64_t B, int32_t num_q_heads,
                                                     int32_t head_dim, int32_t max_blocks,
                                                     int32_t blocks_per_split) {
-  if (B < 0 || num_q_heads <= 0 || head_dim <= 0 || max_blocks < 0 || blocks_per_split < -1) return -1;
-  if (blocks_per_split == -1) return 0;  // single launch: the partials stay in LDS
+  if (B < 0 || num_q_heads <= 0 || head_dim <= 0 || max_blocks < 0 || blocks_per_split < -2) return -1;
+  if (blocks_per_split < 0) return 0;  // single launch: the partials stay in LDS
   if (blocks_per_split == 0) {
     // balanced split: partial rows (nwg + B*ngroups)*wpg*G <= (8*CUs + 2*B)*Hq
     // (wpg*G <= Hq, nwg*wpg <= 4*CUs, ngroups*wpg < 2*Hkv), then B+1 ints
@@ -1127,8 +1210,9 @@ int paged_decode_impl(const void* q, const void* k_cache, const void* v_cache, c
   LFS_REQUIRE(Hq % Hkv == 0 && Hq / Hkv <= 8,
               "paged_decode: num_q_heads (%d) must be a multiple of num_kv_heads (%d), ratio <= 8", Hq, Hkv);
   LFS_REQUIRE(BS % 16 == 0, "paged_decode: block_size must be a multiple of 16 (got %d)", BS);
-  LFS_REQUIRE(blocks_per_split >= -1,
-              "paged_decode: blocks_per_split must be >= -1 (-1: single launch, 0: balanced split)");
+  LFS_REQUIRE(blocks_per_split >= -2,
+              "paged_decode: blocks_per_split must be >= -2 (-1: single launch, -2: single launch in the "
+              "paired order, 0: balanced split)");
   LFS_REQUIRE(blocks_per_split > 0 || B <= BAL_MAXB, "paged_decode: the balanced split (blocks_per_split 0) needs B <= %d",
               BAL_MAXB);
   LFS_REQUIRE(bt_stride >= max_blocks, "paged_decode: block table stride < max_blocks");
@@ -1156,11 +1240,15 @@ int paged_decode_impl(const void* q, const void* k_cache, const void* v_cache, c
     if (BS % t == 0) { tile = t; break; }
   const float sl2 = scale * 1.4426950408889634f;
   const int G = Hq / Hkv;
-  if (blocks_per_split == -1) {
-    const int HG = pairs_heads_per_group(Hkv);
+  if (blocks_per_split < 0) {
+    const bool pair = blocks_per_split == -2;
+    const int HG = pair ? 1 : pairs_heads_per_group(Hkv);
     LFS_REQUIRE(q_out == nullptr || (HG * G * D) % 128 == 0,
-                "paged_decode: the single launch (blocks_per_split -1) cannot quantise this output "
-                "(Hkv = %d, G*D = %d: needs an even Hkv or G*D a multiple of 128)", Hkv, G * D);
+                "paged_decode: the single launch (blocks_per_split %d) cannot quantise this output "
+                "(Hkv = %d, G*D = %d: needs %s)", blocks_per_split, Hkv, G * D,
+                pair ? "G*D a multiple of 128" : "an even Hkv or G*D a multiple of 128");
+    LFS_REQUIRE(!pair || B <= kPairMaxB, "paged_decode: the paired order (blocks_per_split -2) needs B <= %d",
+                kPairMaxB);
     const int ngrp = (Hkv + HG - 1) / HG;
     LFS_REQUIRE(B * ngrp < (1ll << 31), "paged_decode: too many (sequence, kv head) workgroups");
     const RopeIn none{};
@@ -1168,11 +1256,11 @@ int paged_decode_impl(const void* q, const void* k_cache, const void* v_cache, c
         ? dispatch_pairs<64, false>(HG, G, (unsigned)(B * ngrp), st, (const uint16_t*)q, (const uint16_t*)k_cache,
                                     (const uint16_t*)v_cache, context_lens, block_tables, bt_stride,
                                     (uint16_t*)out, (uint8_t*)q_out, q_scale, Hkv, BS, num_blocks, max_blocks,
-                                    tile, sl2, ngrp, none)
+                                    tile, sl2, ngrp, none, pair)
         : dispatch_pairs<128, false>(HG, G, (unsigned)(B * ngrp), st, (const uint16_t*)q,
                                      (const uint16_t*)k_cache, (const uint16_t*)v_cache, context_lens,
                                      block_tables, bt_stride, (uint16_t*)out, (uint8_t*)q_out, q_scale, Hkv, BS,
-                                     num_blocks, max_blocks, tile, sl2, ngrp, none);
+                                     num_blocks, max_blocks, tile, sl2, ngrp, none, pair);
     LFS_REQUIRE(ok, "paged_decode: unsupported group size %d", G);
     return check_launch("paged_decode(single launch)");
   }
@@ -1321,7 +1409,13 @@ extern "C" int lfs_paged_decode_rope(const void* qkv, int64_t ld, const float* q
               "paged_decode_rope: qkv, weights, cos_sin, q_rot, caches and out must be 16-byte aligned");
   LFS_REQUIRE((q_out == nullptr) == (q_scale == nullptr), "paged_decode_rope: q_out and q_scale go together");
   const int G = Hq / Hkv;
-  const int HG = pairs_heads_per_group(Hkv);
+  // Without the quantised output, the paired order (one kv head per 4-wave
+  // workgroup, a long and a short one per CU) when the B*Hkv workgroups fill
+  // between one and two per CU
+  const int64_t units = B * (int64_t)Hkv, ncu = decode_cu_count();
+  const bool pair = q_out == nullptr && B <= kPairMaxB && units > ncu && units <= 2 * ncu &&
+                    (int64_t)max_blocks * BS <= kPairMaxContext;
+  const int HG = pair ? 1 : pairs_heads_per_group(Hkv);
   LFS_REQUIRE(q_out == nullptr || (HG * G * D) % 128 == 0,
               "paged_decode_rope: cannot quantise this output (Hkv = %d, G*D = %d: needs an even Hkv or G*D "
               "a multiple of 128)", Hkv, G * D);
@@ -1337,10 +1431,12 @@ extern "C" int lfs_paged_decode_rope(const void* qkv, int64_t ld, const float* q
   const bool ok = D == 64
       ? dispatch_pairs<64, true>(HG, G, (unsigned)(B * ngrp), st, nullptr, (const uint16_t*)k_cache,
                                  (const uint16_t*)v_cache, context_lens, block_tables, bt_stride, (uint16_t*)out,
-                                 (uint8_t*)q_out, q_scale, Hkv, BS, num_blocks, max_blocks, tile, sl2, ngrp, ri)
+                                 (uint8_t*)q_out, q_scale, Hkv, BS, num_blocks, max_blocks, tile, sl2, ngrp, ri,
+                                 pair)
       : dispatch_pairs<128, true>(HG, G, (unsigned)(B * ngrp), st, nullptr, (const uint16_t*)k_cache,
                                   (const uint16_t*)v_cache, context_lens, block_tables, bt_stride, (uint16_t*)out,
-                                  (uint8_t*)q_out, q_scale, Hkv, BS, num_blocks, max_blocks, tile, sl2, ngrp, ri);
+                                  (uint8_t*)q_out, q_scale, Hkv, BS, num_blocks, max_blocks, tile, sl2, ngrp, ri,
+                                  pair);
   LFS_REQUIRE(ok, "paged_decode_rope: unsupported group size %d", G);
   return check_launch("paged_decode_rope");
 }

@@ -24,6 +24,7 @@ constexpr int kRopeUPT = 4;
 
 // One token row, in phases so that a caller can issue every load early and
 // do the arithmetic later:
+//   init(...)       the shape and the thread (load(row, ...) = init + load(row));
 //   load(row, ...)  issues the loads of the thread's units of q and k;
 //   load_weights(q_weight, k_weight), load_rope(cs)  those of the units'
 //                   norm weights and of the token's RoPE row
@@ -61,11 +62,18 @@ struct RopeRow {
     d0 = (uu % upr) * 8;
   }
 
-  __device__ __forceinline__ void load(const uint16_t* __restrict__ row, int Hq_, int Hkv_, int D_, int tid_) {
+  __device__ __forceinline__ void init(int Hq_, int Hkv_, int D_, int tid_) {
     Hq = Hq_;
     Hkv = Hkv_;
     D = D_;
     tid = tid_;
+  }
+  __device__ __forceinline__ void load(const uint16_t* __restrict__ row, int Hq_, int Hkv_, int D_, int tid_) {
+    init(Hq_, Hkv_, D_, tid_);
+    load(row);
+  }
+  // after init()
+  __device__ __forceinline__ void load(const uint16_t* __restrict__ row) {
 #pragma unroll
     for (int i = 0; i < UPT; ++i) {
       ra[i] = rb[i] = make_uint4(0, 0, 0, 0);

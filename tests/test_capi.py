@@ -127,7 +127,8 @@ def test_workspace_bytes(lib):
     assert lib.lfs_paged_decode_workspace_bytes(64, 16, 64, 16, 1) == 4 * 64 * 16 * 16 * 66
     assert lib.lfs_paged_decode_workspace_bytes(3, 8, 128, 10, 4) == 4 * 3 * 3 * 8 * 130
     assert lib.lfs_paged_decode_workspace_bytes(3, 8, 128, 10, -1) == 0  # single launch: none
-    assert lib.lfs_paged_decode_workspace_bytes(3, 8, 128, 10, -2) == -1
+    assert lib.lfs_paged_decode_workspace_bytes(3, 8, 128, 10, -2) == 0  # paired single launch: none
+    assert lib.lfs_paged_decode_workspace_bytes(3, 8, 128, 10, -3) == -1
     # balanced split (0): (8 * CUs + 2 * B) * Hq partial rows of D + 2 floats, then B + 1 ints
     v = lib.lfs_paged_decode_workspace_bytes(3, 8, 128, 10, 0)
     rows, rem = divmod(v - 4 * 4, 4 * 8 * 130)
@@ -135,15 +136,23 @@ def test_workspace_bytes(lib):
 
 
 def test_default_decode_split_rule():
-    """The decode mode is chosen from shapes only (capturable): the single
-    launch (-1) when Hkv is even, the B * Hkv / 2 workgroups cover every CU
-    (at most four rounds) and the table holds <= 8192 tokens; else the
-    balanced split (0) up to 8192 sequences, else fixed chunks."""
+    """The decode mode is chosen from shapes only (capturable): the paired
+    single launch (-2) when B <= 256, the B * Hkv workgroups are more than
+    one and at most two per CU, the table holds <= 8192 tokens and a
+    quantised output has whole 128-value groups per kv head; else the
+    single launch (-1) when Hkv is even, the B * Hkv / 2 workgroups cover
+    every CU (at most four rounds) and the table holds <= 8192 tokens; else
+    the balanced split (0) up to 8192 sequences, else fixed chunks."""
     from llm_from_scratch_amd import kernels as K
-    assert K.default_blocks_per_split(128, 4, 16, 256, cus=256) == -1   # cfg5 step, B 128
+    assert K.default_blocks_per_split(128, 4, 16, 256, cus=256) == -2   # cfg5 attention shape, no act_quant
+    assert K.default_blocks_per_split(128, 4, 16, 256, cus=256, quant_values=192) == -1  # cfg5 step (G*D 192)
+    assert K.default_blocks_per_split(128, 4, 16, 256, cus=256, quant_values=256) == -2
+    assert K.default_blocks_per_split(300, 1, 16, 256, cus=256) != -2   # more than 256 sequences
+    assert K.default_blocks_per_split(128, 4, 64, 256, cus=256) != -2   # tables past 8192 tokens
     assert K.default_blocks_per_split(64, 4, 16, 256, cus=256) == 0     # cfg3: 128 workgroups
     assert K.default_blocks_per_split(256, 8, 128, 256, cus=256) == 0   # cfg4: tables of 32768 tokens
-    assert K.default_blocks_per_split(128, 3, 16, 256, cus=256) == 0    # odd Hkv
+    assert K.default_blocks_per_split(128, 3, 16, 256, cus=256) == -2   # odd Hkv: one head per workgroup
+    assert K.default_blocks_per_split(128, 3, 16, 256, cus=256, quant_values=192) == 0  # odd Hkv, G*D 192
     assert K.default_blocks_per_split(1024, 4, 16, 256, cus=256) == 0   # more than four rounds
     assert K.default_blocks_per_split(8200, 1, 4, 16, cus=256) > 0      # above the balanced limit
 

@@ -146,10 +146,12 @@ def make_q(case, seed):
                        dtype=torch.bfloat16)
 
 
-@pytest.mark.parametrize("bps", [None, 0, -1])
+@pytest.mark.parametrize("bps", [None, 0, -1, -2])
 def test_paged_decode_cfg3_full(bps):
     """cfg3 against the float64 oracle: the default split, the balanced
-    split and the single launch (one workgroup per (sequence, kv head))."""
+    split, the single launch (one workgroup per (sequence, pair of kv
+    heads)) and the single launch in the paired order (one per (sequence, kv
+    head))."""
     case = W.paged_case("cfg3", seed=2)
     kc, vc = W.fill_pool(case, seed=2, device=DEV, only_referenced=False)
     q = make_q(case, 2)
@@ -210,9 +212,60 @@ def test_paged_decode_split_independence():
     case = W.paged_case("cfg3", seed=5, batch=12)
     kc, vc = W.fill_pool(case, seed=5, device=DEV)
     q = make_q(case, 5)
-    outs = [run_decode(case, kc, vc, q, bps).float() for bps in (0, 1, 2, 3, 16, -1)]
+    outs = [run_decode(case, kc, vc, q, bps).float() for bps in (0, 1, 2, 3, 16, -1, -2)]
     for o in outs[1:]:
         assert_close(o.cpu().numpy(), outs[0].cpu().numpy(), "split")
+
+
+@pytest.mark.parametrize("B,Hkv,G,D", [(128, 4, 3, 64), (96, 4, 3, 64), (256, 2, 4, 128), (40, 8, 2, 64)])
+def test_paged_decode_paired_order(B, Hkv, G, D):
+    """The paired order (blocks_per_split -2) at grids of one to two
+    workgroups per CU (cfg5's B 128 x Hkv 4 = 512 on 256 CUs, 384, 512 and
+    320): every (sequence, kv head) lands in exactly one workgroup whatever
+    the ranking, so the output equals the single launch's (-1, the same four
+    interleaved walks per head) bit for bit, and the float64 oracle within
+    the file's bar.  Lengths with ties, zeros and a one-token context."""
+    rng = np.random.default_rng(B * 10 + Hkv)
+    BS = 256
+    lens = rng.integers(1, 2049, B).astype(np.int64)
+    lens[:6] = [0, 1, 2048, 2048, 700, 700]
+    nblk = -(-lens // BS)
+    NB = int(nblk.sum()) + 4
+    maxb = int(nblk.max())
+    perm = rng.permutation(NB)
+    bt = np.full((B, maxb), -1, np.int32)
+    off = 0
+    for b in range(B):
+        bt[b, :nblk[b]] = perm[off:off + nblk[b]]
+        off += int(nblk[b])
+    g = torch.Generator(device=DEV).manual_seed(B + D)
+    kc = torch.randn(NB, BS, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
+    vc = torch.randn(NB, BS, Hkv, D, generator=g, device=DEV).to(torch.bfloat16)
+    q = torch.randn(B, Hkv * G, D, generator=g, device=DEV).to(torch.bfloat16)
+    cl, btd = torch.from_numpy(lens).to(DEV), torch.from_numpy(bt).to(DEV)
+    print(f"paired order: B {B} Hkv {Hkv} G {G} D {D}", flush=True)
+    o2 = K.paged_attention_decode(q, kc, vc, cl, btd, blocks_per_split=-2)
+    o1 = K.paged_attention_decode(q, kc, vc, cl, btd, blocks_per_split=-1)
+    torch.cuda.synchronize()
+    assert torch.equal(o2, o1)
+    ref = P.paged_decode(q.float().cpu().numpy(), kc.float().cpu().numpy(), vc.float().cpu().numpy(), lens, bt,
+                         1 / math.sqrt(D))
+    assert_close(o2.float().cpu().numpy(), ref, "paired order")
+    assert bool((o2[0] == 0).all())
+
+
+def test_paged_decode_paired_order_rejects():
+    """-2 needs B <= 256, and a quantised output needs whole 128-value
+    groups per kv head (G * D % 128 == 0)."""
+    BS, D, Hkv = 16, 64, 2
+    kc = torch.zeros(4, BS, Hkv, D, device=DEV, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    for B, Hq, quant, msg in ((257, 4, False, "B <= 256"), (4, 6, True, "cannot quantise")):
+        q = torch.zeros(B, Hq, D, device=DEV, dtype=torch.bfloat16)
+        cl = torch.ones(B, device=DEV, dtype=torch.int64)
+        bt = torch.zeros(B, 1, device=DEV, dtype=torch.int32)
+        with pytest.raises(ValueError, match=msg):
+            K.paged_attention_decode(q, kc, vc, cl, bt, blocks_per_split=-2, quant=quant)
 
 
 @pytest.mark.parametrize("Hq,Hkv,D,BS", [(12, 4, 64, 256), (8, 8, 128, 16), (16, 2, 128, 32),
@@ -238,7 +291,7 @@ def test_paged_decode_shapes(Hq, Hkv, D, BS):
                          lens, bt, scale)
     G = Hq // Hkv
     v0 = vc[int(bt[0, 0]), 0].float().cpu().numpy()  # L=1 -> v0 of the matching kv head
-    for bps in (None, -1):  # the default split and the single launch
+    for bps in (None, -1, -2):  # the default split and the single launches
         o = K.paged_attention_decode(q, kc, vc, torch.from_numpy(lens).to(DEV), torch.from_numpy(bt).to(DEV),
                                      blocks_per_split=bps)
         torch.cuda.synchronize()
@@ -272,7 +325,7 @@ def test_paged_decode_fused_quant_equals_act_quant(Hq, Hkv, D, BS):
     # balanced (7 rows over the whole grid), chunks of one and two blocks, and
     # the single launch (its act_quant inside the workgroup: one kv head per
     # workgroup when G*D is a multiple of 128, else two)
-    for bps in (0, 1, 2, -1):
+    for bps in (0, 1, 2, -1) + ((-2,) if (Hq // Hkv) * D % 128 == 0 else ()):
         o, oq, os_ = K.paged_attention_decode(q, kc, vc, cl, btd, blocks_per_split=bps, quant=True)
         plain = K.paged_attention_decode(q, kc, vc, cl, btd, blocks_per_split=bps)
         assert torch.equal(o, plain)
@@ -344,9 +397,19 @@ def test_paged_decode_rope_equals_store_then_decode(Hq, Hkv, D, BS, B):
     assert np.all(got[1] == 0)  # padding row
     rq, rs = K.act_quant(o_b.view(B, -1))
     assert torch.equal(oq_b.view(torch.uint8), rq.view(torch.uint8)) and torch.equal(os_b, rs)
-    # and without the quantised output or the q copy
-    o_c = K.paged_attention_decode_rope(qkv, qw, kw, cos_sin, pos, Hq, Hkv, eps, kc, vc, sl, cl, btd, scale)
-    assert torch.equal(o_c, o_b)
+    # and without the quantised output: the paired order where B * Hkv is
+    # between one and two workgroups per CU (the newest token then enters
+    # the softmax last), the same launch as above elsewhere
+    q_c = torch.empty_like(q)
+    kc_c, vc_c = kc_a.clone(), vc_a.clone()
+    o_c = K.paged_attention_decode_rope(qkv, qw, kw, cos_sin, pos, Hq, Hkv, eps, kc_c, vc_c, sl, cl, btd, scale,
+                                        q_rot=q_c)
+    torch.cuda.synchronize()
+    assert torch.equal(q_c.view(torch.int16), q.view(torch.int16)), "rotated q differs (no quant)"
+    assert torch.equal(kc_c.view(torch.int16), kc_a.view(torch.int16))
+    assert torch.equal(vc_c.view(torch.int16), vc_a.view(torch.int16))
+    assert_close(o_c.float().cpu().numpy(), ref, "fused, no quant, vs oracle")
+    assert np.all(o_c[1].float().cpu().numpy() == 0)
 
 
 def test_paged_decode_rope_rejects_bad_shapes():
