@@ -162,6 +162,21 @@ int lfs_fp8_gemm(const void* a, const float* a_s, const void* b, const float* b_
                  void* stream);
 
 /*
+ * FP8Linear's forward (model/architecture/mlp.py:56-58, GQA.py:34-37 with
+ * the linears in FP8) in one launch: c = lfs_fp8_gemm(act_quant(a, 128),
+ * b, b_s, bias) for bf16 a [M, K] with row stride lda (>= K, a multiple of
+ * 8), bit for bit -- the act_quant codes and scales are computed inside the
+ * one-shot kernel's workgroups, where lfs_fp8_gemm would copy them.  No
+ * counterpart in the reference as one call.  Only the shapes that
+ * lfs_fp8_gemm runs on its one-shot kernel (16 < M <= 128, K and N small
+ * enough): lfs_fp8_gemm_act_supported(M, N, K) returns 1 for them; other
+ * shapes are refused with LFS_EINVAL.
+ */
+int lfs_fp8_gemm_act_supported(int64_t M, int64_t N, int64_t K);
+int lfs_fp8_gemm_act(const void* a, int64_t lda, const void* b, const float* b_s, const float* bias,
+                     int64_t bias_ld, void* c, int64_t M, int64_t N, int64_t K, void* stream);
+
+/*
  * fp8_gemm with the K blocks split over `splits` workgroups per output tile
  * (for small M, where the tiles alone cannot fill the GPU): each split sums
  * ceil((K/128) / splits) consecutive K blocks into an fp32 partial tile in

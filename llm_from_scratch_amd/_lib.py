@@ -26,6 +26,9 @@ SIGNATURES = {
     "lfs_weight_dequant": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_p]),
     "lfs_fp8_gemm": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
                                     _c_p]),
+    "lfs_fp8_gemm_act_supported": (ctypes.c_int, [_c_i64, _c_i64, _c_i64]),
+    "lfs_fp8_gemm_act": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
+                                        _c_p]),
     "lfs_fp8_gemm_workspace_bytes": (ctypes.c_int64, [_c_i64, _c_i64, _c_i64, _c_i32]),
     "lfs_fp8_gemm_splitk": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64,
                                            _c_i32, _c_p, _c_i64, _c_p]),

@@ -609,11 +609,17 @@ __global__ __launch_bounds__(64 * KW * WGM) void fp8_gemm_skinny(
 // LDS: K block j of the range holds A (16 * MT rows) then, after all A
 // blocks, B (16 * NC rows), 128-byte rows in the swizzled chunk order of the
 // tile kernels.
-template <int MT, int NC, int KBM, int WR, int WK>
+// AQ: A is bf16 (row stride lda elements) and the workgroup quantises its
+// rows itself as act_quant(A, 128) does -- each 128-value group's amax over
+// 16 lanes, the same scale and codes -- writing the codes to LDS where the
+// copies would have put act_quant's, and the scales to a small LDS table:
+// the result equals act_quant followed by the same kernel on its output,
+// bit for bit (one split only).
+template <int MT, int NC, int KBM, int WR, int WK, bool AQ = false>
 __global__ __launch_bounds__(64 * WR * WK) void fp8_gemm_flat(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ B,
     const float* __restrict__ Bs, const float* __restrict__ bias, int64_t bias_ld, uint16_t* __restrict__ C,
-    float* __restrict__ ws, int M, int N, int K, int kps) {
+    float* __restrict__ ws, int M, int N, int K, int kps, int64_t lda = 0) {
   constexpr int NW = WR * WK;
   constexpr int RT = MT / WR;                  // row tiles per wave
   constexpr int KW = (KBM + WK - 1) / WK;      // K blocks per wave (at most)
@@ -625,6 +631,7 @@ __global__ __launch_bounds__(64 * WR * WK) void fp8_gemm_flat(
   constexpr bool ONE_SB = 128 % (16 * NC) == 0;
   static_assert((WK - 1) * WR * RT * NC * 1024 <= KBM * (A_BLK + B_BLK), "K-group sums must fit the LDS");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[KBM * (A_BLK + B_BLK)];
+  __shared__ float sa_lds[AQ ? MT * 16 * KBM : 1];  // AQ: scale of (row, K block)
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -642,11 +649,50 @@ __global__ __launch_bounds__(64 * WR * WK) void fp8_gemm_flat(
   for (int i = wave; i < nkb * SEGS; i += NW) {
     const int j = i / SEGS, seg = i - j * SEGS;
     const bool isA = seg < 2 * MT;
+    if (AQ && isA) continue;  // quantised into LDS below
     const int r = 8 * (isA ? seg : seg - 2 * MT) + lrow;  // tile row of this lane
     const int c = (lane & 7) ^ (((r >> 1) & 7) ^ ((r & 1) << 2));
     const uint8_t* src = isA ? A + (size_t)min(m0 + r, M - 1) * K : B + (size_t)min(n0 + r, N - 1) * K;
     const unsigned dst = lds0 + (isA ? j * A_BLK + (r - lrow) * BK : KBM * A_BLK + j * B_BLK + (r - lrow) * BK);
     dma16(src + (size_t)(kb0 + j) * BK + c * 16, dst);
+  }
+  if constexpr (AQ) {
+    // the workgroup's 16*MT rows x nkb K blocks of bf16 A as 8-value chunks,
+    // chunk c = (row, K block, 16-byte-of-codes half): the 16 chunks of a
+    // 128-value group are 16 consecutive lanes
+    constexpr int NT = 64 * NW;
+    constexpr int CPT = (MT * 16 * KBM * 16 + NT - 1) / NT;
+    const int total = MT * 16 * nkb * 16;
+    const uint16_t* Ab = reinterpret_cast<const uint16_t*>(A);
+    uint4 raw[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int c = threadIdx.x + NT * k;
+      raw[k] = make_uint4(0, 0, 0, 0);
+      if (c < total) {
+        const int r = c / (nkb * 16), kc = c - r * (nkb * 16);
+        raw[k] = *reinterpret_cast<const uint4*>(Ab + (int64_t)min(m0 + r, M - 1) * lda +
+                                                 (int64_t)(kb0 * 16 + kc) * 8);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int c = threadIdx.x + NT * k;
+      if (c >= total) break;  // whole 16-lane groups are in or out (total % 16 == 0)
+      const int r = c / (nkb * 16), kc = c - r * (nkb * 16);
+      const int j = kc >> 4, cc = kc & 15;  // K block, chunk of the block
+      float f[8];
+      unpack8(raw[k], f);
+      float amax = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(f[e]));
+      amax = group_max<16>(amax);
+      const float sc = scale_from_amax(amax, false);
+      // logical 16-byte unit cc/2 of row r sits at unit (cc/2) ^ swz(r)
+      const int unit = (cc >> 1) ^ (((r >> 1) & 7) ^ ((r & 1) << 2));
+      *reinterpret_cast<uint2*>(smem + j * A_BLK + r * BK + unit * 16 + (cc & 1) * 8) = quant8(f, sc);
+      if (cc == 0) sa_lds[r * KBM + j] = sc;
+    }
   }
   // scales of this wave's rows and K blocks, and the bias vector, in the same round trip
   constexpr int NSB = ONE_SB ? 1 : NC;  // weight scales per K block: per column tile unless one block
@@ -657,8 +703,10 @@ __global__ __launch_bounds__(64 * WR * WK) void fp8_gemm_flat(
     const int kb = kb0 + min(j, nkb - 1);
 #pragma unroll
     for (int c = 0; c < NSB; ++c) sb[c][jj] = Bs[(size_t)(min(n0 + 16 * c, N - 1) / 128) * KT + kb];
+    if constexpr (!AQ) {
 #pragma unroll
-    for (int t = 0; t < RT; ++t) sa[t][jj] = As[(size_t)min(m0 + 16 * (rg * RT + t) + r16, M - 1) * KT + kb];
+      for (int t = 0; t < RT; ++t) sa[t][jj] = As[(size_t)min(m0 + 16 * (rg * RT + t) + r16, M - 1) * KT + kb];
+    }
   }
   float bvec[NC][4];
 #pragma unroll
@@ -670,6 +718,14 @@ __global__ __launch_bounds__(64 * WR * WK) void fp8_gemm_flat(
     }
   wait_vm<0>();
   __syncthreads();
+  if constexpr (AQ) {
+#pragma unroll
+    for (int jj = 0; jj < KW; ++jj) {
+      const int j = min(kg + WK * jj, nkb - 1);
+#pragma unroll
+      for (int t = 0; t < RT; ++t) sa[t][jj] = sa_lds[(16 * (rg * RT + t) + r16) * KBM + j];
+    }
+  }
 
   v4f acc[RT][NC];
 #pragma unroll
@@ -1423,15 +1479,24 @@ FlatVariant flat_variant(int64_t M, int64_t N, int64_t K, int64_t kps, bool spli
   return FLAT_NONE;
 }
 
+// aq: a is bf16 with row stride lda, quantised inside the kernel (one split)
 void launch_flat(FlatVariant v, const void* a, const float* a_s, const void* b, const float* b_s, const float* bias,
-                 int64_t bias_ld, void* c, float* ws, int64_t M, int64_t N, int64_t K, int kps, hipStream_t st) {
+                 int64_t bias_ld, void* c, float* ws, int64_t M, int64_t N, int64_t K, int kps, hipStream_t st,
+                 bool aq = false, int64_t lda = 0) {
   const int nsplit = (int)((K / 128 + kps - 1) / kps);
 #define LFS_FLAT(MT, NC, KBM, WR, WK)                                                                               \
-  hipLaunchKernelGGL((fp8_gemm_flat<MT, NC, KBM, WR, WK>),                                                           \
-                     dim3((unsigned)((N + 16 * NC - 1) / (16 * NC)), (unsigned)nsplit,                               \
-                          (unsigned)((M + 16 * MT - 1) / (16 * MT))),                                                \
-                     dim3(64 * WR * WK), 0, st, (const uint8_t*)a, a_s, (const uint8_t*)b, b_s, bias, bias_ld,       \
-                     (uint16_t*)c, ws, (int)M, (int)N, (int)K, kps)
+  if (aq)                                                                                                            \
+    hipLaunchKernelGGL((fp8_gemm_flat<MT, NC, KBM, WR, WK, true>),                                                   \
+                       dim3((unsigned)((N + 16 * NC - 1) / (16 * NC)), (unsigned)nsplit,                             \
+                            (unsigned)((M + 16 * MT - 1) / (16 * MT))),                                              \
+                       dim3(64 * WR * WK), 0, st, (const uint8_t*)a, a_s, (const uint8_t*)b, b_s, bias, bias_ld,     \
+                       (uint16_t*)c, ws, (int)M, (int)N, (int)K, kps, lda);                                          \
+  else                                                                                                               \
+    hipLaunchKernelGGL((fp8_gemm_flat<MT, NC, KBM, WR, WK>),                                                         \
+                       dim3((unsigned)((N + 16 * NC - 1) / (16 * NC)), (unsigned)nsplit,                             \
+                            (unsigned)((M + 16 * MT - 1) / (16 * MT))),                                              \
+                       dim3(64 * WR * WK), 0, st, (const uint8_t*)a, a_s, (const uint8_t*)b, b_s, bias, bias_ld,     \
+                       (uint16_t*)c, ws, (int)M, (int)N, (int)K, kps)
   switch (v) {
     case FLAT_R32_C16: LFS_FLAT(2, 1, 8, 2, 4); break;
     case FLAT_R32_C32: LFS_FLAT(2, 2, 8, 2, 2); break;
@@ -1566,6 +1631,32 @@ extern "C" int lfs_fp8_gemm(const void* a, const float* a_s, const void* b, cons
                             const float* bias, int64_t bias_ld, void* c, int64_t M, int64_t N,
                             int64_t K, void* stream) {
   return fp8_gemm_impl(a, a_s, b, b_s, bias, bias_ld, c, M, N, K, 1, nullptr, 0, stream);
+}
+
+extern "C" int lfs_fp8_gemm_act_supported(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 128 != 0 || M >= (1ll << 31) || N >= (1ll << 31) || K >= (1ll << 31))
+    return 0;
+  return flat_variant(M, N, K, K / 128, false) != FLAT_NONE ? 1 : 0;
+}
+
+extern "C" int lfs_fp8_gemm_act(const void* a, int64_t lda, const void* b, const float* b_s, const float* bias,
+                                int64_t bias_ld, void* c, int64_t M, int64_t N, int64_t K, void* stream) {
+  LFS_REQUIRE(M >= 0 && N >= 0 && K >= 0, "fp8_gemm_act: negative shape");
+  LFS_REQUIRE(K % 128 == 0 && K > 0, "fp8_gemm_act: K=%lld must be a positive multiple of 128", (long long)K);
+  if (M == 0 || N == 0) return 0;
+  LFS_REQUIRE(lfs_fp8_gemm_act_supported(M, N, K),
+              "fp8_gemm_act: no one-shot tiling for M=%lld N=%lld K=%lld (16 < M <= 128, small K and N)",
+              (long long)M, (long long)N, (long long)K);
+  LFS_REQUIRE(a && b && b_s && c, "fp8_gemm_act: null pointer");
+  LFS_REQUIRE(lda >= K && lda % 8 == 0, "fp8_gemm_act: the row stride lda=%lld must be >= K and a multiple of 8",
+              (long long)lda);
+  LFS_REQUIRE((((uintptr_t)a | (uintptr_t)b | (uintptr_t)c) & 15u) == 0,
+              "fp8_gemm_act: a, b and c must be 16-byte aligned");
+  LFS_REQUIRE(bias_ld == 0 || (bias != nullptr && bias_ld >= N), "fp8_gemm_act: bias_ld must be 0 or >= N");
+  const FlatVariant fv = flat_variant(M, N, K, K / 128, false);
+  launch_flat(fv, a, nullptr, b, b_s, bias, bias_ld, c, nullptr, M, N, K, (int)(K / 128), (hipStream_t)stream, true,
+              lda);
+  return check_launch("fp8_gemm_act");
 }
 
 extern "C" int lfs_fp8_gemm_splitk(const void* a, const float* a_s, const void* b, const float* b_s,

@@ -22,8 +22,10 @@ Interface (nano-vLLM style, as the runner expects):
 
 Kernels per layer: add_rmsnorm (+act_quant) -> qkv FP8 GEMM ->
 qk_norm_rope_store -> paged decode (split + merge with the act_quant of its
-output; where the single launch is the default split, one launch does the
-norms, RoPE, slot write and attention: paged_attention_decode_rope) -> output FP8 GEMM -> add_rmsnorm_route (the ffn_norm with its act_quant
+output; where a single launch is the default split, one launch does the
+norms, RoPE, slot write and attention: paged_attention_decode_rope -- in
+the paired order, with the act_quant then done inside the output GEMM,
+where that order applies and the GEMM is one-shot) -> output FP8 GEMM -> add_rmsnorm_route (the ffn_norm with its act_quant
 and the MoE gate in one launch; add_rmsnorm then moe_route for grouped
 batches) -> gate/up FP8 GEMM -> swiglu_quant -> down FP8 GEMM.  Setting ``model.trace = {}`` makes an
 eager forward record every intermediate (per layer) for parity tests.
@@ -172,18 +174,29 @@ class PagedGQAAttention(nn.Module):
         T = xq.size(0)
         assert self.k_cache.numel(), "PagedGQAAttention needs the KV pool (ModelRunner.allocate_kv_cache)"
         qkv = self.qkv_proj.gemm(xq, xs)
-        if not ctx.is_prefill and kernels.use_fused_decode_rope(
-                T, self.num_heads, self.num_kv_heads, self.head_dim, ctx.block_tables.size(1),
-                self.k_cache.size(1)):
+        shape = (T, self.num_heads, self.num_kv_heads, self.head_dim, ctx.block_tables.size(1),
+                 self.k_cache.size(1)) if not ctx.is_prefill else None
+        # the paired order (one workgroup per (sequence, kv head), a long and
+        # a short one per CU) when the output projection can quantise its
+        # input itself; else one workgroup per pair of kv heads with the
+        # act_quant fused into the attention
+        paired = (shape is not None and kernels.decode_rope_paired(*shape)
+                  and self.output_proj.fused_act(T))
+        if paired or (shape is not None and kernels.use_fused_decode_rope(*shape)):
             # q/k norms, RoPE, the slot write and the attention in one launch
             q = torch.empty(T, self.num_heads, self.head_dim, dtype=torch.bfloat16,
                             device=qkv.device) if trace is not None else None
-            o, oq, os_ = kernels.paged_attention_decode_rope(
+            res = kernels.paged_attention_decode_rope(
                 qkv, self.q_norm.weight, self.k_norm.weight, self.rope.cos_sin_cached, positions,
                 self.num_heads, self.num_kv_heads, self.q_norm.eps, self.k_cache, self.v_cache,
-                ctx.slot_mapping, ctx.context_lens, ctx.block_tables, self.scale, quant=True, q_rot=q)
-            o = o.reshape(T, -1)
-            out = self.output_proj.gemm(oq, os_)
+                ctx.slot_mapping, ctx.context_lens, ctx.block_tables, self.scale, quant=not paired, q_rot=q)
+            if paired:
+                o = res.reshape(T, -1)
+                out = self.output_proj(o)  # act_quant inside the GEMM
+            else:
+                o, oq, os_ = res
+                o = o.reshape(T, -1)
+                out = self.output_proj.gemm(oq, os_)
             if trace is not None:
                 trace.update(qkv=qkv, q=q, att_o=o, att_out=out)
             return out

@@ -59,8 +59,18 @@ class FP8Linear(nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         x = x.to(torch.bfloat16).contiguous()
+        if self.fused_act(x.numel() // self.in_features):
+            # act_quant inside the GEMM's workgroups: the same codes, scales and bits
+            return kernels.fp8_gemm_act(x, self.weight, self.weight_scale, self.bias)
         xq, xs = kernels.act_quant(x, 128)
         return self.gemm(xq, xs)
+
+    def fused_act(self, rows: int) -> bool:
+        """Whether forward on `rows` input rows quantises them inside the
+        GEMM (the one-shot shapes that fp8_gemm runs in one split)."""
+        M, N, K = rows, self.out_features, self.in_features
+        return (kernels.fp8_gemm_act_supported(M, N, K) and not kernels.use_skinny_gemm(M, N, K)
+                and kernels.default_gemm_splits(M, N, K) == 1)
 
     def gemm(self, xq: torch.Tensor, xs: torch.Tensor) -> torch.Tensor:
         """The linear on an input already quantised by act_quant (codes and

@@ -259,6 +259,38 @@ def fp8_gemm(a: torch.Tensor, a_s: torch.Tensor, b: torch.Tensor, b_s: torch.Ten
     return c
 
 
+def fp8_gemm_act_supported(M: int, N: int, K: int) -> bool:
+    """Whether fp8_gemm_act takes the shape: the one-shot tilings of
+    fp8_gemm (16 < M <= 128, small K and N)."""
+    return bool(_lib.load().lfs_fp8_gemm_act_supported(M, N, K))
+
+
+def fp8_gemm_act(x: torch.Tensor, b: torch.Tensor, b_s: torch.Tensor,
+                 bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """fp8_gemm(*act_quant(x, 128), b, b_s, bias, splits=1) in one launch,
+    bit for bit: the act_quant codes and scales of x are computed inside the
+    GEMM's workgroups.  x: bf16 [..., K] (rows may be strided, K contiguous);
+    only the shapes fp8_gemm_act_supported accepts."""
+    assert x.stride(-1) == 1, "x must be contiguous along K"
+    _on_gpu(x, b, b_s)
+    _dtype(x, torch.bfloat16, "x")
+    _dtype(b, FP8, "b")
+    _dtype(b_s, torch.float32, "b_s")
+    K = x.size(-1)
+    x2 = x.reshape(-1, K)
+    M, N = x2.size(0), b.size(0)
+    assert b.dim() == 2 and b.size(1) == K and b.is_contiguous(), "b must be contiguous [N, K]"
+    assert b_s.shape == (math.ceil(N / 128), K // 128) and b_s.is_contiguous(), "b_s must be [ceil(N/128), K/128]"
+    if bias is not None:
+        _dtype(bias, torch.float32, "bias")
+        assert bias.is_contiguous() and bias.shape == (N,), "bias must be fp32 [N]"
+    c = x.new_empty(*x.shape[:-1], N, dtype=torch.bfloat16)
+    rc = _lib.load().lfs_fp8_gemm_act(_ptr(x2), x2.stride(0), _ptr(b), _ptr(b_s), _ptr(bias), 0, _ptr(c), M, N, K,
+                                      _stream(x))
+    _lib.check(rc, "fp8_gemm_act")
+    return c
+
+
 # ------------------------------------------------------------- paged KV path --
 def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
                   v_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
@@ -484,6 +516,15 @@ def paged_attention_decode_rope(qkv: torch.Tensor, q_weight: torch.Tensor, k_wei
         block_tables.size(1), float(scale), _ptr(oq), _ptr(os_), _stream(qkv))
     _lib.check(rc, "paged_attention_decode_rope")
     return (o, oq, os_) if quant else o
+
+
+def decode_rope_paired(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, max_blocks: int,
+                       block_size: int) -> bool:
+    """Whether paged_attention_decode_rope without the quantised output
+    runs the paired order (blocks_per_split -2): the rule
+    lfs_paged_decode_rope applies when q_out is NULL."""
+    return (use_fused_decode_rope(batch, num_q_heads, num_kv_heads, head_dim, max_blocks, block_size, quant=False)
+            and default_blocks_per_split(batch, num_kv_heads, max_blocks, block_size) == -2)
 
 
 def use_fused_decode_rope(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, max_blocks: int,

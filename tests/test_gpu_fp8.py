@@ -319,6 +319,50 @@ def test_fp8_gemm_flat(M, N, Kd, variant):
         assert_close(f32(got), gemm_oracle(a, a_s, b, b_s, bb), f"flat {M}x{N}x{Kd} {what}")
 
 
+@pytest.mark.parametrize("M,N,Kd,variant", [(17, 250, 384, "r32c16"), (128, 768, 768, "r32c16"),
+                                            (100, 4096, 768, "r32c32"), (128, 9216, 768, "r128c48"),
+                                            (70, 12290, 768, "r128c64"), (40, 1000, 1536, "r16c16"),
+                                            (128, 1024, 4096, "r16c16")])
+def test_fp8_gemm_act_equals_act_quant_then_gemm(M, N, Kd, variant):
+    """fp8_gemm_act (the act_quant of bf16 rows done inside the one-shot
+    GEMM's workgroups) against act_quant followed by fp8_gemm in one split,
+    bit for bit, in each one-shot geometry: ragged M (rows past M read the
+    last row and are dropped), strided rows, outliers that set a group's
+    scale, an all-zero group, bias vector or none; and the oracle's bar on
+    the result.  FP8Linear.forward takes this path on these shapes."""
+    assert K.flat_gemm_variant(M, N, Kd) == variant and K.fp8_gemm_act_supported(M, N, Kd)
+    rng = np.random.default_rng(M * 7 + N + Kd)
+    g = torch.Generator(device=DEV).manual_seed(M + N)
+    wide = torch.randn(M, Kd + 64, generator=g, device=DEV).to(torch.bfloat16)
+    wide[0, :128] = 0                      # one all-zero group
+    wide[M // 2, 5] = 300.0                # an outlier sets its group's scale
+    x = wide[:, :Kd]                       # rows with stride Kd + 64
+    _, _, b, b_s = _random_codes(rng, M, N, Kd)
+    bias = torch.from_numpy(rng.standard_normal(N).astype(np.float32)).to(DEV)
+    print(f"fp8_gemm_act {M}x{N}x{Kd} {variant}", flush=True)
+    for bb in (None, bias):
+        got = K.fp8_gemm_act(x, b, b_s, bb)
+        xq, xs = K.act_quant(x.contiguous(), 128)
+        ref = K.fp8_gemm(xq, xs, b, b_s, bb, splits=1)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), f"{M}x{N}x{Kd} bias={bb is not None}"
+        assert_close(f32(got), gemm_oracle(xq, xs, b, b_s, bb), f"fp8_gemm_act {M}x{N}x{Kd}")
+
+
+def test_fp8_gemm_act_rejects_other_shapes():
+    """Shapes outside the one-shot tilings (M <= 16, M > 128, long K) and a
+    misaligned row stride are refused."""
+    b = torch.zeros(256, 256, device=DEV, dtype=torch.float8_e4m3fn)
+    b_s = torch.ones(2, 2, device=DEV)
+    for M in (8, 200):
+        assert not K.fp8_gemm_act_supported(M, 256, 256)
+        with pytest.raises(ValueError, match="no one-shot tiling"):
+            K.fp8_gemm_act(torch.zeros(M, 256, device=DEV, dtype=torch.bfloat16), b, b_s)
+    x = torch.zeros(64, 260, device=DEV, dtype=torch.bfloat16)[:, 2:258]
+    with pytest.raises(ValueError, match="row stride|aligned"):
+        K.fp8_gemm_act(x, b, b_s)
+
+
 @pytest.mark.parametrize("M,N,Kd", [(1, 768, 768), (5, 1282, 128), (16, 1280, 768), (13, 31, 512),
                                     (1, 1024, 4096), (7, 5632, 2048), (16, 96, 1536), (3, 250, 3072),
                                     (1, 200, 3200), (16, 96, 16384), (16, 1024, 4608), (9, 4096, 1024),
